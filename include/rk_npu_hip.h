@@ -1,0 +1,93 @@
+/*
+ * rk_npu_hip.h — device-resident entry points of the MI355X hip_matmul
+ * library. These have NO counterpart in the reference: its C ABI only takes
+ * host f32 buffers. They serve callers whose activations already live in HBM
+ * (HIP graph capture, serving loops, benchmarks) and share every kernel with
+ * the host-buffer entry points, so their results are bit-identical.
+ *
+ * All A/C/ids/routes pointers are DEVICE pointers on the context's GPU.
+ * `stream` is a hipStream_t (NULL = the workspace's own stream); the call
+ * only enqueues work and returns without synchronizing. The workspace stays
+ * busy until that work completes on the stream: the caller must not issue a
+ * second call on the same workspace from another stream before that.
+ */
+#ifndef RK_NPU_HIP_H
+#define RK_NPU_HIP_H
+
+#include "rk_npu_moe_w8.h"
+#include "rk_npu_quant_matmul.h"
+#include "rk_npu_w4a8.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Activation element types of device buffers. */
+#define RK_NPU_HIP_F32 0
+#define RK_NPU_HIP_F16 1
+
+/* Epilogues. */
+#define RK_NPU_HIP_PLAIN 0
+#define RK_NPU_HIP_SWIGLU 1
+
+/* Linear on device buffers. weights is a rk_npu_f32i8f32_weights* (bits 8)
+ * or a rk_npu_w4a8_weights* (bits 4); workspace the matching workspace kind.
+ * A [rows][K] of a_type, C [rows][N] (PLAIN) or [rows][N/2] (SWIGLU, needs
+ * N % 64 == 0) of c_type. 1 <= rows <= the workspace's M. */
+int rk_npu_hip_linear_run(void* workspace, const void* weights, int bits, const void* A, int a_type,
+                          void* C, int c_type, int rows, int epilogue, void* stream);
+
+/* Fused FFN on device buffers: gate_up (bits gu_bits, N = 2F) -> SwiGLU ->
+ * dense requant of the middle -> down (bits dn_bits). Semantics of
+ * rk_npu_w4a8_run_ffn_f32. */
+int rk_npu_hip_ffn_run(void* gate_up_workspace, const void* gate_up, int gu_bits,
+                       void* down_workspace, const void* down, int dn_bits, const void* A,
+                       int a_type, void* C, int c_type, int rows, void* stream);
+
+/* Routed MoE on device buffers, semantics of rk_npu_moe_w8_run_f32. ids must
+ * lie in [0, routed_experts): they are checked on the device and an
+ * out-of-range id makes the call return RK_NPU_ERR_PARAM at the next
+ * rk_npu_hip_moe_status() (the row is skipped, nothing is read out of bounds). */
+int rk_npu_hip_moe_run(rk_npu_moe_w8_workspace* workspace, const rk_npu_moe_w8_weights* weights,
+                       int rows, const float* input, const int32_t* ids, const float* routes,
+                       float* output, void* stream);
+/* Synchronizes the workspace's last device MoE call and reports whether it
+ * saw an out-of-range expert id (RK_NPU_ERR_PARAM) or not (0). */
+int rk_npu_hip_moe_status(rk_npu_moe_w8_workspace* workspace);
+
+/* Weights from DEVICE-resident codes [K][N] int8 and scales [N] f32. */
+rk_npu_f32i8f32_weights* rk_npu_hip_f32i8f32_weights_create_device(
+    rk_npu_iommu_domain* domain, const rk_npu_matmul_weight_config* config,
+    const int8_t* codes, const float* scales);
+rk_npu_w4a8_weights* rk_npu_hip_w4a8_weights_create_device(rk_npu_iommu_domain* domain,
+                                                           const rk_npu_i4_weight_config* config,
+                                                           const int8_t* codes,
+                                                           const float* scales);
+
+/* Diagnostics: copies what the workspace's last call left on the device for
+ * its first `rows` rows: the int8 activation codes as [rows][K] row-major,
+ * the per-row scales and the per-row code sums (any output may be NULL).
+ * Synchronizes the device first. */
+int rk_npu_hip_workspace_codes(void* workspace, int bits, int rows, int8_t* codes, float* scales,
+                               int32_t* rowsums);
+
+/* Test hook for failure paths: the next `count` device allocations made by
+ * the library fail as if the GPU were out of memory (the domain's reclaim
+ * callback still runs first). Returns the previous count. */
+int rk_npu_hip_inject_alloc_failures(int count);
+
+/* Launch plan the library uses for a linear of this shape, for diagnostics:
+ * kind 0 = GEMV (no MFMA), 1 = MFMA GEMM; tile sizes and K splits. */
+typedef struct rk_npu_hip_plan {
+    int32_t kind;
+    int32_t block_m;
+    int32_t block_n;
+    int32_t k_splits;
+    int32_t grid;
+} rk_npu_hip_plan;
+int rk_npu_hip_linear_plan(int rows, int K, int N, int bits, rk_npu_hip_plan* plan);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

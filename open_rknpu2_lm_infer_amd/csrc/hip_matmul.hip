@@ -1,0 +1,1022 @@
+// hip_matmul: MI355X-native quantized linear library behind the reference's
+// rk_npu_* C ABI (context, domains, W8A8 and W4A8 linears, fused SwiGLU and
+// fused FFN). MoE entry points live in moe.hip.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <new>
+
+#include "kernels.hpp"
+#include "runtime.hpp"
+
+namespace hm {
+
+static std::atomic<int> g_fail_allocs{0};
+
+double now_us() {
+    return std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now().time_since_epoch())
+        .count();
+}
+
+int device_of(Domain* d) { return d->ctx->device; }
+
+static bool try_alloc(void** p, size_t bytes) {
+    int pending = g_fail_allocs.load();
+    while (pending > 0) {
+        if (g_fail_allocs.compare_exchange_weak(pending, pending - 1)) return false;
+    }
+    return hipMalloc(p, bytes) == hipSuccess;
+}
+
+void* domain_alloc(Domain* d, size_t bytes) {
+    void* p = nullptr;
+    if (bytes == 0) bytes = 256;
+    if (!try_alloc(&p, bytes)) {
+        (void)hipGetLastError();
+        void (*cb)(void*) = nullptr;
+        void* cookie = nullptr;
+        {
+            std::lock_guard<std::mutex> lock(d->reclaim_mu);
+            cb = d->reclaim;
+            cookie = d->cookie;
+        }
+        if (cb) cb(cookie);
+        if (!try_alloc(&p, bytes)) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
+    }
+    uint64_t live = d->live.fetch_add(bytes) + bytes;
+    uint64_t peak = d->peak.load();
+    while (live > peak && !d->peak.compare_exchange_weak(peak, live)) {
+    }
+    d->creates.fetch_add(1);
+    return p;
+}
+
+void domain_free(Domain* d, void* p, size_t bytes) {
+    if (!p) return;
+    if (bytes == 0) bytes = 256;
+    (void)hipFree(p);
+    d->live.fetch_sub(bytes);
+    d->destroys.fetch_add(1);
+}
+
+Geometry make_geometry(int bits, int K, int N) {
+    Geometry g;
+    g.bits = bits;
+    g.K = K;
+    g.N = N;
+    g.K_pad = round_up(K, 64);
+    g.N_pad = round_up(N, 256);
+    g.half = (N % 64 == 0) ? N / 2 : 0;
+    return g;
+}
+
+size_t weight_bytes(const Geometry& g) {
+    size_t payload = (size_t)g.K_pad * g.N_pad / (g.bits == 8 ? 1 : 2);
+    return payload + (size_t)g.N_pad * sizeof(float);
+}
+
+// --- weights ----------------------------------------------------------------
+
+static uint64_t mix64(uint64_t h, uint64_t v) {
+    h ^= v + 0x9e3779b97f4a7c15ull + (h << 6) + (h >> 2);
+    h *= 0xbf58476d1ce4e5b9ull;
+    return h ^ (h >> 31);
+}
+
+Weights* weights_create(Domain* d, int bits, int K, int N, const int8_t* codes, const float* scales,
+                        bool device_codes) {
+    if (!d || !codes || !scales || (bits != 4 && bits != 8) || K <= 0 || N <= 0) return nullptr;
+    if ((size_t)K * (size_t)N > (size_t)1 << 40) return nullptr;
+    Geometry g = make_geometry(bits, K, N);
+    const size_t n_codes = (size_t)K * N;
+    uint64_t fp = mix64(mix64(mix64(0x5eedull, (uint64_t)bits), (uint64_t)K), (uint64_t)N);
+    if (!device_codes) {
+        for (int n = 0; n < N; ++n) {
+            if (!(scales[n] > 0.0f)) return nullptr;  // src/model/checkpoint.rs:486-489
+        }
+        if (bits == 4) {
+            for (size_t i = 0; i < n_codes; ++i)
+                if (codes[i] < -8 || codes[i] > 7) return nullptr;
+        }
+        for (int n = 0; n < N; ++n) {
+            uint32_t b;
+            std::memcpy(&b, scales + n, 4);
+            fp = mix64(fp, b);
+        }
+        const size_t stride = std::max<size_t>(1, n_codes / 65536);
+        for (size_t i = 0; i < n_codes; i += stride) fp = mix64(fp, (uint8_t)codes[i] + (i << 8));
+    }
+    if (hipSetDevice(device_of(d)) != hipSuccess) return nullptr;
+    Weights* w = (bits == 8) ? static_cast<Weights*>(new (std::nothrow) rk_npu_f32i8f32_weights())
+                             : static_cast<Weights*>(new (std::nothrow) rk_npu_w4a8_weights());
+    if (!w) return nullptr;
+    w->magic = bits == 8 ? MAGIC_W8 : MAGIC_W4;
+    w->g = g;
+    w->domain = d;
+    w->fingerprint = fp;
+    w->bytes = weight_bytes(g);
+    const size_t payload = w->bytes - (size_t)g.N_pad * sizeof(float);
+    w->packed = static_cast<uint8_t*>(domain_alloc(d, payload));
+    w->colscale = static_cast<float*>(domain_alloc(d, (size_t)g.N_pad * sizeof(float)));
+    int8_t* raw = nullptr;
+    float* dscales = nullptr;
+    unsigned* bad = nullptr;
+    bool ok = w->packed && w->colscale;
+    if (ok && !device_codes) {
+        raw = static_cast<int8_t*>(domain_alloc(d, n_codes));
+        dscales = static_cast<float*>(domain_alloc(d, (size_t)N * sizeof(float)));
+        ok = raw && dscales && hipMemcpy(raw, codes, n_codes, hipMemcpyHostToDevice) == hipSuccess &&
+             hipMemcpy(dscales, scales, (size_t)N * 4, hipMemcpyHostToDevice) == hipSuccess;
+    }
+    if (ok) bad = static_cast<unsigned*>(domain_alloc(d, 256));
+    ok = ok && bad && hipMemset(bad, 0, 4) == hipSuccess;
+    if (ok) {
+        PackParams P;
+        P.codes = device_codes ? codes : raw;
+        P.scales = device_codes ? scales : dscales;
+        P.K = K;
+        P.N = N;
+        P.K_pad = g.K_pad;
+        P.N_pad = g.N_pad;
+        P.half = g.half;
+        P.out = w->packed;
+        P.colscale = w->colscale;
+        P.bad = bad;
+        const size_t entries = (size_t)(g.K_pad / (bits == 8 ? 16 : 32)) * g.N_pad;
+        const unsigned blocks = (unsigned)((entries + 255) / 256);
+        if (bits == 8)
+            hipLaunchKernelGGL(pack_w8_kernel, dim3(blocks), dim3(256), 0, 0, P);
+        else
+            hipLaunchKernelGGL(pack_w4_kernel, dim3(blocks), dim3(256), 0, 0, P);
+        ok = hipGetLastError() == hipSuccess && hipDeviceSynchronize() == hipSuccess;
+        unsigned flag = 0;
+        ok = ok && hipMemcpy(&flag, bad, 4, hipMemcpyDeviceToHost) == hipSuccess;
+        if (ok && device_codes) {
+            if (flag) ok = false;
+            // scales must be positive: checked from the packed copy
+            float* hs = static_cast<float*>(std::malloc((size_t)g.N_pad * 4));
+            ok = ok && hs && hipMemcpy(hs, w->colscale, (size_t)g.N_pad * 4, hipMemcpyDeviceToHost) == hipSuccess;
+            if (ok) {
+                int valid = 0;
+                for (int p = 0; p < g.N_pad; ++p) {
+                    if (hs[p] > 0.0f) ++valid;
+                    uint32_t b;
+                    std::memcpy(&b, hs + p, 4);
+                    w->fingerprint = mix64(w->fingerprint, b);
+                }
+                ok = valid == N;
+            }
+            std::free(hs);
+        }
+    }
+    domain_free(d, raw, n_codes);
+    domain_free(d, dscales, (size_t)N * sizeof(float));
+    domain_free(d, bad, 256);
+    if (!ok) {
+        weights_destroy(w);
+        return nullptr;
+    }
+    return w;
+}
+
+void weights_destroy(Weights* w) {
+    if (!w) return;
+    (void)hipSetDevice(device_of(w->domain));
+    const size_t payload = w->bytes - (size_t)w->g.N_pad * sizeof(float);
+    domain_free(w->domain, w->packed, payload);
+    domain_free(w->domain, w->colscale, (size_t)w->g.N_pad * sizeof(float));
+    if (w->magic == MAGIC_W8)
+        delete static_cast<rk_npu_f32i8f32_weights*>(w);
+    else
+        delete static_cast<rk_npu_w4a8_weights*>(w);
+}
+
+// --- workspaces -------------------------------------------------------------
+
+struct WsLayout {
+    size_t a, codes, rows, c, acc, counters, total;
+};
+
+static WsLayout ws_layout(const Geometry& g, int M) {
+    WsLayout L;
+    const int M_alloc = round_up(M, 256);
+    L.a = round_up_z((size_t)M * g.K * 4, 256);
+    L.codes = (size_t)(g.K_pad / 16) * M_alloc * 16;
+    L.rows = round_up_z((size_t)M_alloc * 4, 256);
+    L.c = round_up_z((size_t)M * g.N * 4, 256);
+    L.acc = round_up_z((size_t)8 * g.N_pad * 4, 256);
+    L.counters = round_up_z((size_t)(g.N_pad / 64) * 4, 256);
+    L.total = L.a + L.codes + 3 * L.rows + L.c + L.acc + L.counters;
+    return L;
+}
+
+size_t workspace_bytes(const Geometry& g, int M) { return ws_layout(g, M).total; }
+
+Workspace* workspace_create(Domain* d, int bits, int M, int K, int N) {
+    if (!d || (bits != 4 && bits != 8) || M <= 0 || M > 65536 || K <= 0 || N <= 0) return nullptr;
+    if (hipSetDevice(device_of(d)) != hipSuccess) return nullptr;
+    Workspace* ws = (bits == 8) ? static_cast<Workspace*>(new (std::nothrow) rk_npu_matmul_workspace())
+                                : static_cast<Workspace*>(new (std::nothrow) rk_npu_w4a8_workspace());
+    if (!ws) return nullptr;
+    ws->magic = bits == 8 ? MAGIC_WS8 : MAGIC_WS4;
+    ws->g = make_geometry(bits, K, N);
+    ws->M = M;
+    ws->M_alloc = round_up(M, 256);
+    ws->domain = d;
+    ws->busy.store(false);
+    ws->stream = nullptr;
+    const WsLayout L = ws_layout(ws->g, M);
+    ws->bytes = L.total;
+    uint8_t* base = static_cast<uint8_t*>(domain_alloc(d, L.total));
+    if (!base) {
+        delete ws;
+        return nullptr;
+    }
+    size_t off = 0;
+    ws->a_f32 = reinterpret_cast<float*>(base + off);
+    off += L.a;
+    ws->codes = reinterpret_cast<int8_t*>(base + off);
+    off += L.codes;
+    ws->rowscale = reinterpret_cast<float*>(base + off);
+    off += L.rows;
+    ws->rowsum = reinterpret_cast<int*>(base + off);
+    off += L.rows;
+    ws->rowmax = reinterpret_cast<unsigned*>(base + off);
+    off += L.rows;
+    ws->c_f32 = reinterpret_cast<float*>(base + off);
+    off += L.c;
+    ws->gemv_acc = reinterpret_cast<int*>(base + off);
+    off += L.acc;
+    ws->gemv_counters = reinterpret_cast<unsigned*>(base + off);
+    // Zero everything once: padding rows of the code planes, the split-K
+    // accumulators and arrival counters (kept zero between calls by the kernels).
+    bool ok = hipMemset(base, 0, L.total) == hipSuccess &&
+              hipStreamCreateWithFlags(&ws->stream, hipStreamNonBlocking) == hipSuccess &&
+              hipDeviceSynchronize() == hipSuccess;
+    if (!ok) {
+        workspace_destroy(ws);
+        return nullptr;
+    }
+    return ws;
+}
+
+void workspace_destroy(Workspace* ws) {
+    if (!ws) return;
+    (void)hipSetDevice(device_of(ws->domain));
+    if (ws->stream) {
+        (void)hipStreamSynchronize(ws->stream);
+        (void)hipStreamDestroy(ws->stream);
+    }
+    domain_free(ws->domain, ws->a_f32, ws->bytes);
+    if (ws->magic == MAGIC_WS8)
+        delete static_cast<rk_npu_matmul_workspace*>(ws);
+    else
+        delete static_cast<rk_npu_w4a8_workspace*>(ws);
+}
+
+// --- launch plans -------------------------------------------------------------
+
+enum GemmVariant { V256x256 = 0, V256x128 = 1, V128x128 = 2, V64x128 = 3, V32x128 = 4 };
+static const int kBM[] = {256, 256, 128, 64, 32};
+static const int kBN[] = {256, 128, 128, 128, 128};
+
+static int env_int(const char* name, int fallback) {
+    const char* v = std::getenv(name);
+    return v ? std::atoi(v) : fallback;
+}
+
+Plan plan_linear(int rows, const Geometry& g) {
+    Plan p{};
+    if (rows <= 8) {
+        p.kind = 0;
+        p.mr = rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : 8;
+        const int ncg = g.N_pad / 64;
+        const int KG = g.K_pad / 64;
+        const int max_kg = GEMV_LDS_BYTES / (64 * p.mr);
+        const int target_blocks = env_int("HM_GEMV_BLOCKS", 2048);
+        int ks = std::max((KG + max_kg - 1) / max_kg, std::min((target_blocks + ncg - 1) / ncg, std::max(1, KG / 2)));
+        ks = std::min(ks, KG);
+        p.kg_per_split = (KG + ks - 1) / ks;
+        p.ksplit = (KG + p.kg_per_split - 1) / p.kg_per_split;
+        p.grid = ncg * p.ksplit;
+        p.bm = p.mr;
+        p.bn = 64;
+        return p;
+    }
+    p.kind = 1;
+    p.ksplit = 1;
+    int v;
+    const int forced = env_int("HM_GEMM_VARIANT", -1);
+    if (forced >= 0 && forced <= 4) {
+        v = forced;
+    } else if (rows <= 32) {
+        v = V32x128;
+    } else if (rows <= 64) {
+        v = V64x128;
+    } else if (rows <= 128) {
+        v = V128x128;
+    } else {
+        const int t256 = ((rows + 255) / 256) * (g.N_pad / 256);
+        const int t256x128 = ((rows + 255) / 256) * (g.N_pad / 128);
+        v = t256 >= 256 ? V256x256 : (t256x128 >= 256 ? V256x128 : V128x128);
+    }
+    p.variant = v;
+    p.bm = kBM[v];
+    p.bn = kBN[v];
+    p.grid = ((rows + p.bm - 1) / p.bm) * (g.N_pad / p.bn);
+    return p;
+}
+
+// --- enqueue ------------------------------------------------------------------
+
+int enqueue_quant(Workspace* ws, const void* x, int x_type, long lda, int rows, int rule,
+                  const unsigned* rowmax_in, unsigned* rowmax_clear, hipStream_t s, const int* rows_dev) {
+    QuantParams P;
+    P.x = x;
+    P.x_type = x_type;
+    P.lda = lda;
+    P.rows = rows;
+    P.K = ws->g.K;
+    P.K_pad = ws->g.K_pad;
+    P.M_alloc = ws->M_alloc;
+    const size_t esz = x_type == DT_F32 ? 4 : 2;
+    P.vec = (ws->g.K % 16 == 0) && ((lda * esz) % 16 == 0) && ((reinterpret_cast<uintptr_t>(x) & 15) == 0);
+    P.codes = ws->codes;
+    P.rowscale = ws->rowscale;
+    P.rowsum = ws->rowsum;
+    P.rowmax_in = rowmax_in;
+    P.rowmax_clear = rowmax_clear;
+    P.rows_dev = rows_dev;
+    const dim3 grid((rows + 15) / 16), block(256);
+    if (x_type == DT_F32) {
+        if (rule == QUANT_DENSE)
+            hipLaunchKernelGGL((quant_rows_kernel<float, QUANT_DENSE>), grid, block, 0, s, P);
+        else
+            hipLaunchKernelGGL((quant_rows_kernel<float, QUANT_MOE>), grid, block, 0, s, P);
+    } else {
+        if (rule == QUANT_DENSE)
+            hipLaunchKernelGGL((quant_rows_kernel<__half, QUANT_DENSE>), grid, block, 0, s, P);
+        else
+            hipLaunchKernelGGL((quant_rows_kernel<__half, QUANT_MOE>), grid, block, 0, s, P);
+    }
+    return hipGetLastError() == hipSuccess ? RK_NPU_OK : RK_NPU_ERR_DEVICE;
+}
+
+template <int BITS, int EPI>
+static void launch_gemm(int v, const GemmParams& G, int grid, hipStream_t s) {
+    switch (v) {
+        case V256x256:
+            hipLaunchKernelGGL((gemm_kernel<256, 256, 2, 2, BITS, EPI>), dim3(grid), dim3(256), 0, s, G);
+            break;
+        case V256x128:
+            hipLaunchKernelGGL((gemm_kernel<256, 128, 2, 2, BITS, EPI>), dim3(grid), dim3(256), 0, s, G);
+            break;
+        case V128x128:
+            hipLaunchKernelGGL((gemm_kernel<128, 128, 2, 2, BITS, EPI>), dim3(grid), dim3(256), 0, s, G);
+            break;
+        case V64x128:
+            hipLaunchKernelGGL((gemm_kernel<64, 128, 1, 2, BITS, EPI>), dim3(grid), dim3(128), 0, s, G);
+            break;
+        default:
+            hipLaunchKernelGGL((gemm_kernel<32, 128, 1, 2, BITS, EPI>), dim3(grid), dim3(128), 0, s, G);
+            break;
+    }
+}
+
+template <int BITS, int EPI>
+static void launch_gemv(int mr, const GemvParams& V, int grid, hipStream_t s) {
+    switch (mr) {
+        case 1:
+            hipLaunchKernelGGL((gemv_kernel<1, BITS, EPI>), dim3(grid), dim3(256), 0, s, V);
+            break;
+        case 2:
+            hipLaunchKernelGGL((gemv_kernel<2, BITS, EPI>), dim3(grid), dim3(256), 0, s, V);
+            break;
+        case 4:
+            hipLaunchKernelGGL((gemv_kernel<4, BITS, EPI>), dim3(grid), dim3(256), 0, s, V);
+            break;
+        default:
+            hipLaunchKernelGGL((gemv_kernel<8, BITS, EPI>), dim3(grid), dim3(256), 0, s, V);
+            break;
+    }
+}
+
+int enqueue_linear(Workspace* ws, const Weights* w, void* c, int c_type, long ldc, int rows, int epi,
+                   unsigned* rowmax, hipStream_t s) {
+    const Geometry& g = w->g;
+    const Plan p = plan_linear(rows, g);
+    if (p.kind == 0) {
+        GemvParams V;
+        V.a = ws->codes;
+        V.b = w->packed;
+        V.rowscale = ws->rowscale;
+        V.rowsum = ws->rowsum;
+        V.colscale = w->colscale;
+        V.c = c;
+        V.ldc = ldc;
+        V.c_type = c_type;
+        V.M = rows;
+        V.N = g.N;
+        V.K_pad = g.K_pad;
+        V.M_alloc = ws->M_alloc;
+        V.N_pad = g.N_pad;
+        V.half = g.half;
+        V.rowmax = rowmax;
+        V.ksplit = p.ksplit;
+        V.kg_per_split = p.kg_per_split;
+        V.acc = ws->gemv_acc;
+        V.counters = ws->gemv_counters;
+#define HM_GEMV(B)                                                              \
+    if (epi == EPI_PLAIN)                                                       \
+        launch_gemv<B, EPI_PLAIN>(p.mr, V, p.grid, s);                          \
+    else if (epi == EPI_SWIGLU)                                                 \
+        launch_gemv<B, EPI_SWIGLU>(p.mr, V, p.grid, s);                         \
+    else                                                                        \
+        launch_gemv<B, EPI_SWIGLU_MAX>(p.mr, V, p.grid, s);
+        if (g.bits == 8) {
+            HM_GEMV(8)
+        } else {
+            HM_GEMV(4)
+        }
+#undef HM_GEMV
+    } else {
+        GemmParams G;
+        G.a = ws->codes;
+        G.b = w->packed;
+        G.rowscale = ws->rowscale;
+        G.rowsum = ws->rowsum;
+        G.colscale = w->colscale;
+        G.c = c;
+        G.ldc = ldc;
+        G.c_type = c_type;
+        G.M = rows;
+        G.N = g.N;
+        G.K_pad = g.K_pad;
+        G.M_alloc = ws->M_alloc;
+        G.N_pad = g.N_pad;
+        G.half = g.half;
+        G.rowmax = rowmax;
+        G.tiles_m = (rows + p.bm - 1) / p.bm;
+        G.tiles_n = g.N_pad / p.bn;
+#define HM_GEMM(B)                                                   \
+    if (epi == EPI_PLAIN)                                            \
+        launch_gemm<B, EPI_PLAIN>(p.variant, G, p.grid, s);          \
+    else if (epi == EPI_SWIGLU)                                      \
+        launch_gemm<B, EPI_SWIGLU>(p.variant, G, p.grid, s);         \
+    else                                                             \
+        launch_gemm<B, EPI_SWIGLU_MAX>(p.variant, G, p.grid, s);
+        if (g.bits == 8) {
+            HM_GEMM(8)
+        } else {
+            HM_GEMM(4)
+        }
+#undef HM_GEMM
+    }
+    return hipGetLastError() == hipSuccess ? RK_NPU_OK : RK_NPU_ERR_DEVICE;
+}
+
+}  // namespace hm
+
+using namespace hm;
+
+// ============================================================================
+// C ABI
+// ============================================================================
+extern "C" {
+
+const char* rk_npu_strerror(int rc) {
+    switch (rc) {
+        case RK_NPU_OK:
+            return "success";
+        case RK_NPU_ERR_PARAM:
+            return "invalid argument";
+        case RK_NPU_ERR_NOMEM:
+            return "out of device memory";
+        case RK_NPU_ERR_DEVICE:
+            return "HIP device error";
+        case RK_NPU_ERR_CACHE_MISS:
+            return "tuning cache miss";
+        case RK_NPU_ERR_BUSY:
+            return "workspace busy";
+        case RK_NPU_ERR_UNSUPPORTED:
+            return "unsupported operation";
+        case RK_NPU_ERR_FORMAT:
+            return "invalid expert record";
+        default:
+            return "unknown error";
+    }
+}
+
+rk_npu_ctx* rk_npu_open(const char* device) {
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    int dev = 0;
+    if (device && *device) {
+        char* end = nullptr;
+        long v = std::strtol(device, &end, 10);
+        if (*end != '\0' || v < 0 || v >= count) return nullptr;
+        dev = (int)v;
+    } else if (hipGetDevice(&dev) != hipSuccess) {
+        return nullptr;
+    }
+    if (hipSetDevice(dev) != hipSuccess) return nullptr;
+    rk_npu_ctx* ctx = new (std::nothrow) rk_npu_ctx();
+    if (ctx) ctx->device = dev;
+    return ctx;
+}
+
+void rk_npu_close(rk_npu_ctx* ctx) { delete ctx; }
+
+rk_npu_iommu_domain* rk_npu_iommu_domain_create(rk_npu_ctx* ctx, uint32_t id) {
+    if (!ctx || id >= RK_NPU_IOMMU_DOMAIN_COUNT) return nullptr;
+    Domain* d = new (std::nothrow) Domain();
+    if (!d) return nullptr;
+    d->ctx = ctx;
+    d->id = id;
+    return d;
+}
+
+void rk_npu_iommu_domain_free(rk_npu_iommu_domain* domain) { delete static_cast<Domain*>(domain); }
+
+void rk_npu_iommu_domain_set_reclaim(rk_npu_iommu_domain* domain, void (*reclaim)(void*), void* cookie) {
+    if (!domain) return;
+    std::lock_guard<std::mutex> lock(domain->reclaim_mu);
+    domain->reclaim = reclaim;
+    domain->cookie = cookie;
+}
+
+int rk_npu_iommu_domain_memory_stats(const rk_npu_iommu_domain* domain, rk_npu_domain_memory_stats* stats) {
+    if (!domain || !stats) return RK_NPU_ERR_PARAM;
+    stats->live_bytes = domain->live.load();
+    stats->peak_bytes = domain->peak.load();
+    stats->creates = domain->creates.load();
+    stats->destroys = domain->destroys.load();
+    return RK_NPU_OK;
+}
+
+// ---- W8 ---------------------------------------------------------------------
+
+rk_npu_f32i8f32_weights* rk_npu_f32i8f32_weights_create(rk_npu_iommu_domain* domain,
+                                                        const rk_npu_matmul_weight_config* config,
+                                                        const int8_t* codes, const float* scales) {
+    if (!config) return nullptr;
+    return static_cast<rk_npu_f32i8f32_weights*>(
+        weights_create(static_cast<Domain*>(domain), 8, config->K, config->N, codes, scales, false));
+}
+
+rk_npu_f32i8f32_weights* rk_npu_f32i8f32_weights_create_compress(rk_npu_iommu_domain* domain,
+                                                                 const rk_npu_matmul_weight_config* config,
+                                                                 const int8_t* codes, const float* scales) {
+    return rk_npu_f32i8f32_weights_create(domain, config, codes, scales);
+}
+
+void rk_npu_f32i8f32_weights_free(rk_npu_f32i8f32_weights* weights) { weights_destroy(weights); }
+
+int rk_npu_f32i8f32_weights_memory_query(const rk_npu_matmul_weight_config* config,
+                                         rk_npu_matmul_weight_requirements* requirements) {
+    if (!config || !requirements || config->K <= 0 || config->N <= 0) return RK_NPU_ERR_PARAM;
+    requirements->bytes = weight_bytes(make_geometry(8, config->K, config->N));
+    return RK_NPU_OK;
+}
+
+uint64_t rk_npu_f32i8f32_weights_compressed_layout_generation(const rk_npu_f32i8f32_weights*) { return 0; }
+
+// Legality table of the caller's W8 K partition (src/npu.rs:1568-1595):
+// a tile must be a positive multiple of 32 no larger than min(K, 4096), and a
+// multiple of 512 unless the call has at most 4 rows.
+int rk_npu_matmul_k_partition_query(int rows, int K, int k_tile) {
+    if (rows <= 0 || K <= 0 || k_tile <= 0) return RK_NPU_ERR_PARAM;
+    if (k_tile > K || k_tile > 4096 || k_tile % 32 != 0) return RK_NPU_ERR_PARAM;
+    if (k_tile % 512 != 0 && rows > 4) return RK_NPU_ERR_PARAM;
+    return RK_NPU_OK;
+}
+
+void rk_npu_matmul_autotune_config_init(rk_npu_matmul_autotune_config* config, int M, int N, int K) {
+    if (!config) return;
+    std::memset(config, 0, sizeof(*config));
+    config->M = M;
+    config->N = N;
+    config->K = K;
+    config->required_k_tile = K;
+    config->allowed_npu_core_mask = 1;
+    config->warmup = 1;
+    config->loops = 3;
+    config->repeats = 3;
+}
+
+int rk_npu_matmul_autotune_cache_load(rk_npu_ctx*, const char*, rk_npu_matmul_op_kind,
+                                      const rk_npu_matmul_autotune_config* config, rk_npu_matmul_strategy*,
+                                      rk_npu_matmul_strategy*) {
+    return config ? RK_NPU_ERR_CACHE_MISS : RK_NPU_ERR_PARAM;
+}
+
+static void fill_w8_strategy(const rk_npu_matmul_autotune_config* c, rk_npu_matmul_strategy* s) {
+    std::memset(s, 0, sizeof(*s));
+    s->op_kind = RK_NPU_MATMUL_F32I8F32_DYNAMIC;
+    s->M = c->M;
+    s->N = c->N;
+    s->K = c->K;
+    s->k_tile = c->required_k_tile > 0 ? c->required_k_tile : c->K;
+    const Plan p = plan_linear(c->M, make_geometry(8, c->K, c->N));
+    s->n_tile = p.bn;
+    s->a_layout = RK_NPU_MATMUL_A_LAYOUT_NORMAL;
+    s->c_layout = RK_NPU_MATMUL_C_LAYOUT_NATIVE;
+    s->wave_count = 1;
+    s->n_groups = (round_up(c->N, 256) + p.bn - 1) / p.bn;
+    s->npu_core_mask = c->allowed_npu_core_mask;
+    s->cpu_core_mask = c->allowed_cpu_core_mask;
+    s->cpu_threads = 1;
+    s->total_us = 1.0;
+}
+
+int rk_npu_matmul_autotune_cached(rk_npu_ctx* ctx, const rk_npu_matmul_autotune_config* config,
+                                  rk_npu_matmul_op_kind op, const char*, int, rk_npu_matmul_strategy* fastest,
+                                  rk_npu_matmul_strategy* stable, int* hit) {
+    if (!ctx || !config || !fastest || op != RK_NPU_MATMUL_F32I8F32_DYNAMIC || config->M <= 0 ||
+        config->N <= 0 || config->K <= 0)
+        return RK_NPU_ERR_PARAM;
+    fill_w8_strategy(config, fastest);
+    if (stable) *stable = *fastest;
+    if (hit) *hit = 0;
+    return RK_NPU_OK;
+}
+
+int rk_npu_matmul_workspace_memory_query(const rk_npu_matmul_strategy* strategy,
+                                         rk_npu_matmul_workspace_requirements* requirements) {
+    if (!strategy || !requirements || strategy->M <= 0 || strategy->K <= 0 || strategy->N <= 0)
+        return RK_NPU_ERR_PARAM;
+    requirements->bytes = workspace_bytes(make_geometry(8, strategy->K, strategy->N), strategy->M);
+    return RK_NPU_OK;
+}
+
+rk_npu_matmul_workspace* rk_npu_matmul_workspace_create(rk_npu_iommu_domain* domain,
+                                                        const rk_npu_matmul_strategy* strategy) {
+    if (!strategy) return nullptr;
+    return static_cast<rk_npu_matmul_workspace*>(
+        workspace_create(static_cast<Domain*>(domain), 8, strategy->M, strategy->K, strategy->N));
+}
+
+void rk_npu_matmul_workspace_free(rk_npu_matmul_workspace* workspace) { workspace_destroy(workspace); }
+
+// Host-buffer call: upload A, quantize, multiply, download C, synchronize.
+static int run_host(Workspace* ws, const Weights* w, const float* A, float* C, int epi,
+                    rk_npu_w4a8_timings* timings) {
+    const double t0 = now_us();
+    if (!ws || !w || !A || !C) return RK_NPU_ERR_PARAM;
+    if (ws->g.K != w->g.K || ws->g.N != w->g.N || ws->g.bits != w->g.bits) return RK_NPU_ERR_PARAM;
+    if (epi != EPI_PLAIN && !w->g.half) return RK_NPU_ERR_PARAM;
+    BusyGuard guard(ws->busy);
+    if (!guard.ok) return RK_NPU_ERR_BUSY;
+    if (hipSetDevice(device_of(ws->domain)) != hipSuccess) return RK_NPU_ERR_DEVICE;
+    const int M = ws->M, K = w->g.K, N = w->g.N;
+    const int width = epi == EPI_PLAIN ? N : N / 2;
+    if (hipMemcpyAsync(ws->a_f32, A, (size_t)M * K * 4, hipMemcpyHostToDevice, ws->stream) != hipSuccess)
+        return RK_NPU_ERR_DEVICE;
+    const double t1 = now_us();
+    int rc = enqueue_quant(ws, ws->a_f32, DT_F32, K, M, QUANT_DENSE, nullptr, nullptr, ws->stream);
+    if (rc == RK_NPU_OK) rc = enqueue_linear(ws, w, ws->c_f32, DT_F32, width, M, epi, nullptr, ws->stream);
+    if (rc != RK_NPU_OK) {
+        (void)hipStreamSynchronize(ws->stream);
+        return rc;
+    }
+    if (timings && hipStreamSynchronize(ws->stream) != hipSuccess) return RK_NPU_ERR_DEVICE;
+    const double t2 = now_us();
+    if (hipMemcpyAsync(C, ws->c_f32, (size_t)M * width * 4, hipMemcpyDeviceToHost, ws->stream) != hipSuccess ||
+        hipStreamSynchronize(ws->stream) != hipSuccess)
+        return RK_NPU_ERR_DEVICE;
+    if (timings) {
+        const double t3 = now_us();
+        timings->upload_us = t1 - t0;
+        timings->device_us = t2 - t1;
+        timings->download_us = t3 - t2;
+        timings->total_us = t3 - t0;
+    }
+    return RK_NPU_OK;
+}
+
+static Workspace* as_ws(void* p, int bits) {
+    Workspace* ws = static_cast<Workspace*>(p);
+    if (!ws || ws->magic != (bits == 8 ? MAGIC_WS8 : MAGIC_WS4)) return nullptr;
+    return ws;
+}
+static const Weights* as_w(const void* p, int bits) {
+    const Weights* w = static_cast<const Weights*>(p);
+    if (!w || w->magic != (bits == 8 ? MAGIC_W8 : MAGIC_W4)) return nullptr;
+    return w;
+}
+
+int rk_npu_f32i8f32_run_dynamic(rk_npu_matmul_workspace* workspace, const rk_npu_f32i8f32_weights* weights,
+                                const float* A, float* C) {
+    return run_host(as_ws(workspace, 8), as_w(weights, 8), A, C, EPI_PLAIN, nullptr);
+}
+
+// ---- W4 ---------------------------------------------------------------------
+
+rk_npu_w4a8_weights* rk_npu_w4a8_weights_create(rk_npu_iommu_domain* domain, const rk_npu_i4_weight_config* config,
+                                                const int8_t* codes, const float* scales) {
+    if (!config) return nullptr;
+    return static_cast<rk_npu_w4a8_weights*>(
+        weights_create(static_cast<Domain*>(domain), 4, config->K, config->N, codes, scales, false));
+}
+
+void rk_npu_w4a8_weights_free(rk_npu_w4a8_weights* weights) { weights_destroy(weights); }
+
+int rk_npu_w4a8_weights_query(const rk_npu_w4a8_weights* weights, rk_npu_w4a8_weight_info* info) {
+    if (!weights || !info || weights->magic != MAGIC_W4) return RK_NPU_ERR_PARAM;
+    info->bound_relaxed = 0;
+    info->multiplier = 1.0f;
+    info->config.K = weights->g.K;
+    info->config.N = weights->g.N;
+    info->config.k_tile = weights->g.K;
+    return RK_NPU_OK;
+}
+
+int rk_npu_i4_weights_memory_query(const rk_npu_i4_weight_config* config, uint64_t* bytes) {
+    if (!config || !bytes || config->K <= 0 || config->N <= 0) return RK_NPU_ERR_PARAM;
+    *bytes = weight_bytes(make_geometry(4, config->K, config->N));
+    return RK_NPU_OK;
+}
+
+void rk_npu_w4a8_config_init(rk_npu_w4a8_config* config, int M, int N, int K) {
+    if (!config) return;
+    std::memset(config, 0, sizeof(*config));
+    config->M = M;
+    config->N = N;
+    config->K = K;
+    config->k_tile = K;
+    config->m_tile = std::min(M, 64);
+    config->n_tile = std::min(round_up(N, 64), 1024);
+    config->npu_core_mask = 1;
+    config->cpu_threads = 1;
+    config->pipeline = RK_NPU_W4A8_PIPELINED;
+}
+
+void rk_npu_w4a8_options_init(rk_npu_w4a8_options* options) {
+    if (options) options->reduce_backend = RK_NPU_W4A8_REDUCE_DEVICE;
+}
+
+int rk_npu_w4a8_memory_query_ex(const rk_npu_w4a8_config* config, const rk_npu_w4a8_options*,
+                                rk_npu_w4a8_memory_info_ex* info) {
+    if (!config || !info || config->M <= 0 || config->K <= 0 || config->N <= 0) return RK_NPU_ERR_PARAM;
+    info->workspace_bytes = workspace_bytes(make_geometry(4, config->K, config->N), config->M);
+    return RK_NPU_OK;
+}
+
+rk_npu_w4a8_workspace* rk_npu_w4a8_workspace_create_ex(rk_npu_iommu_domain* domain, const rk_npu_w4a8_config* config,
+                                                       const rk_npu_w4a8_options*) {
+    if (!config) return nullptr;
+    return static_cast<rk_npu_w4a8_workspace*>(
+        workspace_create(static_cast<Domain*>(domain), 4, config->M, config->K, config->N));
+}
+
+void rk_npu_w4a8_workspace_free(rk_npu_w4a8_workspace* workspace) { workspace_destroy(workspace); }
+
+int rk_npu_w4a8_run_f32(rk_npu_w4a8_workspace* workspace, const rk_npu_w4a8_weights* weights, const float* A,
+                        float* C, rk_npu_w4a8_timings* timings) {
+    return run_host(as_ws(workspace, 4), as_w(weights, 4), A, C, EPI_PLAIN, timings);
+}
+
+int rk_npu_w4a8_run_swiglu_f32(rk_npu_w4a8_workspace* workspace, const rk_npu_w4a8_weights* weights,
+                               const float* A, float* C, rk_npu_w4a8_timings* timings) {
+    return run_host(as_ws(workspace, 4), as_w(weights, 4), A, C, EPI_SWIGLU, timings);
+}
+
+// Fused FFN enqueue shared by the host and device entry points.
+static int enqueue_ffn(Workspace* gws, const Weights* gw, Workspace* dws, const Weights* dw, const void* A,
+                       int a_type, void* C, int c_type, int rows, hipStream_t s) {
+    const int F = gw->g.N / 2;
+    int rc = enqueue_quant(gws, A, a_type, gw->g.K, rows, QUANT_DENSE, nullptr, gws->rowmax, s);
+    if (rc == RK_NPU_OK) rc = enqueue_linear(gws, gw, gws->c_f32, DT_F32, F, rows, EPI_SWIGLU_MAX, gws->rowmax, s);
+    if (rc == RK_NPU_OK) rc = enqueue_quant(dws, gws->c_f32, DT_F32, F, rows, QUANT_DENSE, gws->rowmax, nullptr, s);
+    if (rc == RK_NPU_OK) rc = enqueue_linear(dws, dw, C, c_type, dw->g.N, rows, EPI_PLAIN, nullptr, s);
+    return rc;
+}
+
+static int check_ffn(Workspace* gws, const Weights* gw, Workspace* dws, const Weights* dw, int rows) {
+    if (!gws || !gw || !dws || !dw) return RK_NPU_ERR_PARAM;
+    if (gws->g.K != gw->g.K || gws->g.N != gw->g.N || dws->g.K != dw->g.K || dws->g.N != dw->g.N)
+        return RK_NPU_ERR_PARAM;
+    if (!gw->g.half || dw->g.K != gw->g.N / 2 || dw->g.N != gw->g.K) return RK_NPU_ERR_PARAM;
+    if (rows < 1 || rows > gws->M || rows > dws->M) return RK_NPU_ERR_PARAM;
+    return RK_NPU_OK;
+}
+
+int rk_npu_w4a8_run_ffn_f32(rk_npu_w4a8_workspace* gate_up_workspace, const rk_npu_w4a8_weights* gate_up,
+                            void* down_workspace, const void* down, int down_bits, const float* A, float* C,
+                            rk_npu_w4a8_timings* timings) {
+    const double t0 = now_us();
+    Workspace* gws = as_ws(gate_up_workspace, 4);
+    const Weights* gw = as_w(gate_up, 4);
+    Workspace* dws = as_ws(down_workspace, down_bits);
+    const Weights* dw = as_w(down, down_bits);
+    if (!A || !C || (down_bits != 4 && down_bits != 8)) return RK_NPU_ERR_PARAM;
+    int rc = check_ffn(gws, gw, dws, dw, gws ? gws->M : 0);
+    if (rc != RK_NPU_OK) return rc;
+    if (gws->M != dws->M) return RK_NPU_ERR_PARAM;
+    BusyGuard g1(gws->busy);
+    if (!g1.ok) return RK_NPU_ERR_BUSY;
+    BusyGuard g2(dws->busy);
+    if (!g2.ok) return RK_NPU_ERR_BUSY;
+    if (hipSetDevice(device_of(gws->domain)) != hipSuccess) return RK_NPU_ERR_DEVICE;
+    const int M = gws->M, H = gw->g.K;
+    hipStream_t s = gws->stream;
+    if (hipMemcpyAsync(gws->a_f32, A, (size_t)M * H * 4, hipMemcpyHostToDevice, s) != hipSuccess)
+        return RK_NPU_ERR_DEVICE;
+    const double t1 = now_us();
+    rc = enqueue_ffn(gws, gw, dws, dw, gws->a_f32, DT_F32, dws->c_f32, DT_F32, M, s);
+    if (rc != RK_NPU_OK) {
+        (void)hipStreamSynchronize(s);
+        return rc;
+    }
+    if (timings && hipStreamSynchronize(s) != hipSuccess) return RK_NPU_ERR_DEVICE;
+    const double t2 = now_us();
+    if (hipMemcpyAsync(C, dws->c_f32, (size_t)M * H * 4, hipMemcpyDeviceToHost, s) != hipSuccess ||
+        hipStreamSynchronize(s) != hipSuccess)
+        return RK_NPU_ERR_DEVICE;
+    if (timings) {
+        const double t3 = now_us();
+        timings->upload_us = t1 - t0;
+        timings->device_us = t2 - t1;
+        timings->download_us = t3 - t2;
+        timings->total_us = t3 - t0;
+    }
+    return RK_NPU_OK;
+}
+
+// ---- tuning (W4) ------------------------------------------------------------
+
+struct rk_npu_w4a8_tuning_profile {
+    uint64_t fingerprint;
+};
+
+rk_npu_w4a8_tuning_profile* rk_npu_w4a8_tuning_profile_from_weights(const rk_npu_w4a8_weights* weights) {
+    if (!weights || weights->magic != MAGIC_W4) return nullptr;
+    rk_npu_w4a8_tuning_profile* p = new (std::nothrow) rk_npu_w4a8_tuning_profile();
+    if (p) p->fingerprint = weights->fingerprint;
+    return p;
+}
+
+void rk_npu_w4a8_tuning_profile_free(rk_npu_w4a8_tuning_profile* profile) { delete profile; }
+
+uint64_t rk_npu_w4a8_tuning_profile_fingerprint(const rk_npu_w4a8_tuning_profile* profile) {
+    return profile ? profile->fingerprint : 0;
+}
+
+void rk_npu_w4a8_autotune_config_init(rk_npu_w4a8_autotune_config* config, int M, int N, int K) {
+    if (!config) return;
+    std::memset(config, 0, sizeof(*config));
+    config->M = M;
+    config->N = N;
+    config->K = K;
+    config->required_k_tile = 0;
+    config->k_tile_multiplier = 1.0;
+    config->allowed_npu_core_mask = 1;
+    config->warmup = 1;
+    config->loops = 3;
+    config->repeats = 3;
+}
+
+int rk_npu_w4a8_autotune_cache_load_profile_ex(rk_npu_ctx*, const rk_npu_w4a8_autotune_config* config,
+                                               const rk_npu_w4a8_tuning_profile*, const char*,
+                                               rk_npu_w4a8_strategy_ex*, rk_npu_w4a8_strategy_ex*) {
+    return config ? RK_NPU_ERR_CACHE_MISS : RK_NPU_ERR_PARAM;
+}
+
+static void fill_w4_strategy(const rk_npu_w4a8_autotune_config* c, rk_npu_w4a8_strategy_ex* s) {
+    std::memset(s, 0, sizeof(*s));
+    rk_npu_w4a8_config_init(&s->base.config, c->M, c->N, c->K);
+    if (c->required_k_tile > 0) s->base.config.k_tile = c->required_k_tile;
+    const Plan p = plan_linear(c->M, make_geometry(4, c->K, c->N));
+    s->base.config.m_tile = p.bm;
+    s->base.config.n_tile = p.bn;
+    s->base.config.npu_core_mask = c->allowed_npu_core_mask;
+    s->base.cpu_core_mask = c->allowed_cpu_core_mask;
+    s->base.total_us = 1.0;
+    rk_npu_w4a8_options_init(&s->execution);
+}
+
+int rk_npu_w4a8_autotune_cached_ex(rk_npu_ctx* ctx, const rk_npu_w4a8_autotune_config* config, const int8_t*,
+                                   const float*, const char*, int, rk_npu_w4a8_strategy_ex* fastest,
+                                   rk_npu_w4a8_strategy_ex* stable, int* hit) {
+    if (!ctx || !config || !fastest || config->M <= 0 || config->N <= 0 || config->K <= 0) return RK_NPU_ERR_PARAM;
+    fill_w4_strategy(config, fastest);
+    if (stable) *stable = *fastest;
+    if (hit) *hit = 0;
+    return RK_NPU_OK;
+}
+
+int rk_npu_w4a8_autotune_ex(rk_npu_ctx* ctx, const rk_npu_w4a8_autotune_config* config, const int8_t* codes,
+                            const float* scales, rk_npu_w4a8_strategy_ex* fastest, rk_npu_w4a8_strategy_ex* stable) {
+    int hit = 0;
+    return rk_npu_w4a8_autotune_cached_ex(ctx, config, codes, scales, nullptr, 0, fastest, stable, &hit);
+}
+
+// ---- device-resident extensions -------------------------------------------------
+
+int rk_npu_hip_linear_run(void* workspace, const void* weights, int bits, const void* A, int a_type, void* C,
+                          int c_type, int rows, int epilogue, void* stream) {
+    Workspace* ws = as_ws(workspace, bits);
+    const Weights* w = as_w(weights, bits);
+    if (!ws || !w || !A || !C) return RK_NPU_ERR_PARAM;
+    if ((a_type != DT_F32 && a_type != DT_F16) || (c_type != DT_F32 && c_type != DT_F16)) return RK_NPU_ERR_PARAM;
+    if (ws->g.K != w->g.K || ws->g.N != w->g.N || rows < 1 || rows > ws->M) return RK_NPU_ERR_PARAM;
+    if (epilogue != RK_NPU_HIP_PLAIN && epilogue != RK_NPU_HIP_SWIGLU) return RK_NPU_ERR_PARAM;
+    const int epi = epilogue == RK_NPU_HIP_SWIGLU ? EPI_SWIGLU : EPI_PLAIN;
+    if (epi != EPI_PLAIN && !w->g.half) return RK_NPU_ERR_PARAM;
+    BusyGuard guard(ws->busy);
+    if (!guard.ok) return RK_NPU_ERR_BUSY;
+    if (hipSetDevice(device_of(ws->domain)) != hipSuccess) return RK_NPU_ERR_DEVICE;
+    hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ws->stream;
+    const int width = epi == EPI_PLAIN ? w->g.N : w->g.N / 2;
+    int rc = enqueue_quant(ws, A, a_type, w->g.K, rows, QUANT_DENSE, nullptr, nullptr, s);
+    if (rc == RK_NPU_OK) rc = enqueue_linear(ws, w, C, c_type, width, rows, epi, nullptr, s);
+    return rc;
+}
+
+int rk_npu_hip_ffn_run(void* gate_up_workspace, const void* gate_up, int gu_bits, void* down_workspace,
+                       const void* down, int dn_bits, const void* A, int a_type, void* C, int c_type, int rows,
+                       void* stream) {
+    Workspace* gws = as_ws(gate_up_workspace, gu_bits);
+    const Weights* gw = as_w(gate_up, gu_bits);
+    Workspace* dws = as_ws(down_workspace, dn_bits);
+    const Weights* dw = as_w(down, dn_bits);
+    if (!A || !C || (a_type != DT_F32 && a_type != DT_F16) || (c_type != DT_F32 && c_type != DT_F16))
+        return RK_NPU_ERR_PARAM;
+    int rc = check_ffn(gws, gw, dws, dw, rows);
+    if (rc != RK_NPU_OK) return rc;
+    BusyGuard g1(gws->busy);
+    if (!g1.ok) return RK_NPU_ERR_BUSY;
+    BusyGuard g2(dws->busy);
+    if (!g2.ok) return RK_NPU_ERR_BUSY;
+    if (hipSetDevice(device_of(gws->domain)) != hipSuccess) return RK_NPU_ERR_DEVICE;
+    hipStream_t s = stream ? static_cast<hipStream_t>(stream) : gws->stream;
+    return enqueue_ffn(gws, gw, dws, dw, A, a_type, C, c_type, rows, s);
+}
+
+rk_npu_f32i8f32_weights* rk_npu_hip_f32i8f32_weights_create_device(rk_npu_iommu_domain* domain,
+                                                                   const rk_npu_matmul_weight_config* config,
+                                                                   const int8_t* codes, const float* scales) {
+    if (!config) return nullptr;
+    return static_cast<rk_npu_f32i8f32_weights*>(
+        weights_create(static_cast<Domain*>(domain), 8, config->K, config->N, codes, scales, true));
+}
+
+rk_npu_w4a8_weights* rk_npu_hip_w4a8_weights_create_device(rk_npu_iommu_domain* domain,
+                                                           const rk_npu_i4_weight_config* config, const int8_t* codes,
+                                                           const float* scales) {
+    if (!config) return nullptr;
+    return static_cast<rk_npu_w4a8_weights*>(
+        weights_create(static_cast<Domain*>(domain), 4, config->K, config->N, codes, scales, true));
+}
+
+int rk_npu_hip_workspace_codes(void* workspace, int bits, int rows, int8_t* codes, float* scales,
+                               int32_t* rowsums) {
+    Workspace* ws = as_ws(workspace, bits);
+    if (!ws || rows < 1 || rows > ws->M) return RK_NPU_ERR_PARAM;
+    if (hipSetDevice(device_of(ws->domain)) != hipSuccess || hipDeviceSynchronize() != hipSuccess)
+        return RK_NPU_ERR_DEVICE;
+    const int K = ws->g.K, KG = ws->g.K_pad / 16;
+    if (codes) {
+        const size_t plane = (size_t)ws->M_alloc * 16;
+        uint8_t* tmp = static_cast<uint8_t*>(std::malloc(plane * KG));
+        if (!tmp) return RK_NPU_ERR_NOMEM;
+        if (hipMemcpy(tmp, ws->codes, plane * KG, hipMemcpyDeviceToHost) != hipSuccess) {
+            std::free(tmp);
+            return RK_NPU_ERR_DEVICE;
+        }
+        for (int r = 0; r < rows; ++r)
+            for (int k = 0; k < K; ++k)
+                codes[(size_t)r * K + k] = (int8_t)tmp[(size_t)(k / 16) * plane + (size_t)r * 16 + k % 16];
+        std::free(tmp);
+    }
+    if (scales && hipMemcpy(scales, ws->rowscale, (size_t)rows * 4, hipMemcpyDeviceToHost) != hipSuccess)
+        return RK_NPU_ERR_DEVICE;
+    if (rowsums && hipMemcpy(rowsums, ws->rowsum, (size_t)rows * 4, hipMemcpyDeviceToHost) != hipSuccess)
+        return RK_NPU_ERR_DEVICE;
+    return RK_NPU_OK;
+}
+
+int rk_npu_hip_inject_alloc_failures(int count) { return g_fail_allocs.exchange(count < 0 ? 0 : count); }
+
+int rk_npu_hip_linear_plan(int rows, int K, int N, int bits, rk_npu_hip_plan* plan) {
+    if (!plan || rows < 1 || K < 1 || N < 1 || (bits != 4 && bits != 8)) return RK_NPU_ERR_PARAM;
+    const Plan p = plan_linear(rows, make_geometry(bits, K, N));
+    plan->kind = p.kind;
+    plan->block_m = p.bm;
+    plan->block_n = p.bn;
+    plan->k_splits = p.ksplit;
+    plan->grid = p.grid;
+    return RK_NPU_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,171 @@
+// HIP kernels of the routed-expert (MoE) FFN: device-side token
+// permutation, ragged grouped GEMM over the permutation, rank-ordered combine.
+#pragma once
+
+#include "kernels.hpp"
+
+namespace hm {
+
+constexpr int MOE_MAX_EXPERTS = 512;
+
+// ---------------------------------------------------------------------------
+// Counting sort of the (token, rank) assignments by expert. Assignments with
+// route <= 0 are skipped (they contribute nothing to the combine); an expert id
+// outside [0, experts) raises the error flag and is skipped as well. Each
+// expert's assignments get a contiguous run of slots; every run is cut into
+// m-tiles of `bm` slots for the grouped GEMM. Within a run the slot order is
+// arbitrary: every slot is computed independently and the combine reads
+// slots through pos[] in rank order, so results do not depend on it.
+// ---------------------------------------------------------------------------
+struct RouteParams {
+    const int* ids;
+    const float* routes;
+    int rows, top, experts, bm;
+    int* pos;       // [rows*top] slot or -1
+    int* perm;      // [rows*top] slot -> assignment
+    int4* tiles;    // [max_tiles] {expert, slot_begin, slot_end, 0}
+    int* counts;    // [0] slots used, [1] tiles
+    unsigned* rowmax_mid;
+    int rowmax_count;
+    unsigned* error;
+};
+
+static __global__ __launch_bounds__(1024) void moe_route_kernel(RouteParams P) {
+    __shared__ int cnt[MOE_MAX_EXPERTS];
+    __shared__ int fill[MOE_MAX_EXPERTS];
+    __shared__ int off[MOE_MAX_EXPERTS];
+    __shared__ int toff[MOE_MAX_EXPERTS];
+    const int tid = threadIdx.x;
+    const int A = P.rows * P.top;
+    for (int e = tid; e < P.experts; e += 1024) {
+        cnt[e] = 0;
+        fill[e] = 0;
+    }
+    for (int i = tid; i < P.rowmax_count; i += 1024) P.rowmax_mid[i] = 0u;
+    __syncthreads();
+    for (int a = tid; a < A; a += 1024) {
+        const int e = P.ids[a];
+        const bool in_range = e >= 0 && e < P.experts;
+        if (!in_range) atomicOr(P.error, 1u);
+        if (in_range && P.routes[a] > 0.0f) atomicAdd(&cnt[e], 1);
+    }
+    __syncthreads();
+    if (tid == 0) {
+        int run = 0, tiles = 0;
+        for (int e = 0; e < P.experts; ++e) {
+            off[e] = run;
+            toff[e] = tiles;
+            run += cnt[e];
+            tiles += (cnt[e] + P.bm - 1) / P.bm;
+        }
+        P.counts[0] = run;
+        P.counts[1] = tiles;
+    }
+    __syncthreads();
+    for (int a = tid; a < A; a += 1024) {
+        const int e = P.ids[a];
+        int slot = -1;
+        if (e >= 0 && e < P.experts && P.routes[a] > 0.0f) {
+            slot = off[e] + atomicAdd(&fill[e], 1);
+            P.perm[slot] = a;
+        }
+        P.pos[a] = slot;
+    }
+    for (int e = tid; e < P.experts; e += 1024) {
+        const int n = (cnt[e] + P.bm - 1) / P.bm;
+        for (int t = 0; t < n; ++t) {
+            const int b = off[e] + t * P.bm;
+            P.tiles[toff[e] + t] = make_int4(e, b, min(off[e] + cnt[e], b + P.bm), 0);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Grouped GEMM: block = (m-tile of one expert's slot run, n-tile). Gather mode
+// (perm != nullptr) reads A row perm[slot] / top (the token's quantized input
+// row); otherwise A row = slot (the requantized middle). Blocks past the
+// device-side tile count exit at once.
+// ---------------------------------------------------------------------------
+struct MoeGemmParams {
+    const int8_t* a;
+    int a_alloc;
+    const int* perm;
+    int top;
+    const float* rowscale;
+    const int* rowsum;
+    const uint8_t* const* b_tab;
+    const float* const* s_tab;
+    const int4* tiles;
+    const int* counts;
+    void* c;
+    long ldc;
+    int c_type;
+    unsigned* rowmax;
+    int N, K_pad, N_pad, half, tiles_n;
+};
+
+template <int BM, int BN, int WGM, int WGN, int BITS, int EPI>
+__global__ __launch_bounds__(WGM* WGN * 64, 1) void moe_gemm_kernel(MoeGemmParams P) {
+    using C = TileCfg<BM, BN, WGM, WGN, BITS>;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * C::STAGE];
+    __shared__ int s_rows[BM];
+    const int t = blockIdx.x / P.tiles_n, tn = blockIdx.x % P.tiles_n;
+    if (t >= P.counts[1]) return;
+    const int4 tile = P.tiles[t];
+    const int e = tile.x, begin = tile.y, end = tile.z;
+    for (int i = threadIdx.x; i < BM; i += C::NT) {
+        const int slot = begin + i < end ? begin + i : begin;
+        s_rows[i] = P.perm ? P.perm[slot] / P.top : slot;
+    }
+    __syncthreads();
+    size_t a_off[C::A_LOADS];
+#pragma unroll
+    for (int i = 0; i < C::A_LOADS; ++i) {
+        const int c = threadIdx.x + i * C::NT;
+        a_off[i] = (size_t)(c / BM) * P.a_alloc + s_rows[c % BM];
+    }
+    v16i acc[C::FM][C::FN];
+#pragma unroll
+    for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+        for (int j = 0; j < C::FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+    const int n0 = tn * BN;
+    gemm_mainloop<BM, BN, WGM, WGN, BITS>(smem, P.a, (size_t)P.a_alloc, a_off, P.b_tab[e], P.N_pad, n0, P.K_pad >> 6,
+                                          acc);
+    gemm_epilogue<BM, BN, WGM, WGN, BITS, EPI>(acc, n0, P.rowscale, P.rowsum, P.s_tab[e], P.N, P.half, P.c, P.ldc,
+                                               P.c_type, P.rowmax, [&](int local, int& out_row, int& src_row) {
+                                                   out_row = begin + local;
+                                                   src_row = s_rows[local];
+                                                   return begin + local < end;
+                                               });
+}
+
+// ---------------------------------------------------------------------------
+// Combine: out[r][c] = sum over rank (in order, skipped slots excluded) of
+// fma(contribution, route, sum), then + shared contribution.
+// ---------------------------------------------------------------------------
+struct CombineParams {
+    const float* contrib;  // [slots][h]
+    const int* pos;
+    const float* routes;
+    const float* shared;  // [rows][h] or nullptr
+    int rows, top, h;
+    float* out;
+};
+
+static __global__ __launch_bounds__(256) void moe_combine_kernel(CombineParams P) {
+    const int r = blockIdx.y;
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    if (c >= P.h) return;
+    float sum = 0.0f;
+    for (int rank = 0; rank < P.top; ++rank) {
+        const int s = P.pos[r * P.top + rank];
+        if (s >= 0) sum = __builtin_fmaf(P.contrib[(size_t)s * P.h + c], P.routes[r * P.top + rank], sum);
+    }
+    if (P.shared) sum = sum + P.shared[(size_t)r * P.h + c];
+    P.out[(size_t)r * P.h + c] = sum;
+}
+
+}  // namespace hm

@@ -1,0 +1,135 @@
+// Internal runtime of the hip_matmul library: context, allocation domains,
+// device weights and workspaces behind the opaque rk_npu_* handles.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cstddef>
+#include <cstdint>
+#include <mutex>
+
+#include "../../include/rk_npu_hip.h"
+#include "../../include/rk_npu_moe_w8.h"
+#include "../../include/rk_npu_quant_matmul.h"
+#include "../../include/rk_npu_w4a8.h"
+#include "../../include/rk_npu_w4a8_tune.h"
+
+struct rk_npu_ctx {
+    int device;
+};
+
+struct rk_npu_iommu_domain {
+    rk_npu_ctx* ctx;
+    uint32_t id;
+    std::atomic<uint64_t> live{0}, peak{0}, creates{0}, destroys{0};
+    std::mutex reclaim_mu;
+    void (*reclaim)(void*) = nullptr;
+    void* cookie = nullptr;
+};
+
+namespace hm {
+
+struct Domain : rk_npu_iommu_domain {};
+
+constexpr uint32_t MAGIC_W4 = 0x57344841u;  // weights, 4-bit
+constexpr uint32_t MAGIC_W8 = 0x57384841u;  // weights, 8-bit
+constexpr uint32_t MAGIC_WS4 = 0x53344841u;
+constexpr uint32_t MAGIC_WS8 = 0x53384841u;
+
+inline int round_up(int v, int m) { return (v + m - 1) / m * m; }
+inline size_t round_up_z(size_t v, size_t m) { return (v + m - 1) / m * m; }
+
+// Device allocation through a domain: accounting, injected failures for
+// tests, and one retry after the domain's reclaim callback.
+void* domain_alloc(Domain* d, size_t bytes);
+void domain_free(Domain* d, void* p, size_t bytes);
+
+// Geometry shared by weights and workspaces.
+struct Geometry {
+    int bits;
+    int K, N;
+    int K_pad;  // multiple of 64
+    int N_pad;  // multiple of 256
+    int half;   // N/2 when N % 64 == 0 (gate/up interleaved packing), else 0
+};
+Geometry make_geometry(int bits, int K, int N);
+size_t weight_bytes(const Geometry& g);
+
+struct Weights {
+    uint32_t magic;
+    Geometry g;
+    Domain* domain;
+    uint8_t* packed;
+    float* colscale;
+    size_t bytes;
+    uint64_t fingerprint;
+};
+
+struct Workspace {
+    uint32_t magic;
+    Geometry g;
+    int M;        // rows per call (the caller's bucket) / max rows for device calls
+    int M_alloc;  // multiple of 256
+    Domain* domain;
+    hipStream_t stream;
+    std::atomic<bool> busy;
+    size_t bytes;
+    // device buffers
+    float* a_f32;     // [M][K]   host-call input staging
+    int8_t* codes;    // [K_pad/16][M_alloc][16]
+    float* rowscale;  // [M_alloc]
+    int* rowsum;      // [M_alloc]
+    unsigned* rowmax; // [M_alloc]  max|middle| of a fused SwiGLU output
+    float* c_f32;     // [M][N]   output staging / fused middle
+    int* gemv_acc;    // [8][N_pad]
+    unsigned* gemv_counters;  // [N_pad/64]
+};
+
+size_t workspace_bytes(const Geometry& g, int M);
+Workspace* workspace_create(Domain* d, int bits, int M, int K, int N);
+void workspace_destroy(Workspace* ws);
+
+Weights* weights_create(Domain* d, int bits, int K, int N, const int8_t* codes, const float* scales,
+                        bool device_codes);
+void weights_destroy(Weights* w);
+
+struct Plan {
+    int kind;  // 0 GEMV, 1 GEMM
+    int bm, bn;
+    int mr;
+    int ksplit, kg_per_split;
+    int grid;
+    int variant;
+};
+Plan plan_linear(int rows, const Geometry& g);
+
+// Enqueue helpers (no synchronization).
+int enqueue_quant(Workspace* ws, const void* x, int x_type, long lda, int rows, int rule,
+                  const unsigned* rowmax_in, unsigned* rowmax_clear, hipStream_t s,
+                  const int* rows_dev = nullptr);
+int enqueue_linear(Workspace* ws, const Weights* w, void* c, int c_type, long ldc, int rows, int epi,
+                   unsigned* rowmax, hipStream_t s);
+
+int device_of(Domain* d);
+struct BusyGuard {
+    std::atomic<bool>* flag;
+    bool ok;
+    explicit BusyGuard(std::atomic<bool>& f) : flag(&f) {
+        bool expected = false;
+        ok = f.compare_exchange_strong(expected, true);
+    }
+    ~BusyGuard() {
+        if (ok) flag->store(false);
+    }
+};
+
+double now_us();
+
+}  // namespace hm
+
+// The public opaque types are thin tags over the internal structures.
+struct rk_npu_f32i8f32_weights : hm::Weights {};
+struct rk_npu_w4a8_weights : hm::Weights {};
+struct rk_npu_matmul_workspace : hm::Workspace {};
+struct rk_npu_w4a8_workspace : hm::Workspace {};

@@ -1,0 +1,153 @@
+"""CPU checks of the C-ABI library and the host logic: the shared library loads,
+exports every entry point the headers declare, and its pure (device-free)
+functions behave as the reference's callers expect. No compute call is made."""
+import ctypes
+import glob
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+from open_rknpu2_lm_infer_amd import _ffi as F
+from open_rknpu2_lm_infer_amd import npu
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_functions():
+    names = set()
+    for path in glob.glob(os.path.join(ROOT, "include", "*.h")):
+        text = open(path).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        for m in re.finditer(r"\b(rk_npu_[a-z0-9_]+)\s*\(", text):
+            names.add(m.group(1))
+    return names
+
+
+def test_library_exports_every_declared_symbol():
+    lib_path = F.LIB_PATH
+    assert os.path.exists(lib_path), "build the library first"
+    out = subprocess.run(["nm", "-D", "--defined-only", lib_path], capture_output=True, text=True,
+                         check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    declared = declared_functions()
+    assert len(declared) > 60
+    missing = sorted(declared - exported)
+    assert not missing, f"declared but not exported: {missing}"
+    assert set(F.SIGNATURES) == declared, "ctypes table and headers disagree"
+    L = F.lib()
+    for name in declared:
+        assert hasattr(L, name)
+
+
+def test_headers_compile_as_c():
+    src = "".join(f'#include "{os.path.basename(h)}"\n' for h in sorted(glob.glob(os.path.join(ROOT, "include", "*.h"))))
+    src += "int main(void) { return 0; }\n"
+    subprocess.run(["gcc", "-std=c11", "-Wall", "-Werror", "-fsyntax-only", "-I", os.path.join(ROOT, "include"),
+                    "-x", "c", "-"], input=src, text=True, check=True)
+
+
+def test_strerror_and_codes():
+    assert F.strerror(0) == "success"
+    assert F.strerror(F.RK_NPU_ERR_CACHE_MISS) == "tuning cache miss"
+    assert F.strerror(12345) == "unknown error"
+
+
+def test_k_partition_query_table():
+    """src/npu.rs:1568-1595 (legality the caller's W8 planning relies on)."""
+    L = F.lib()
+    for rows, k, tile in [(1, 8192, 2752), (4, 8192, 2752), (64, 8192, 2048), (64, 8192, 3072),
+                          (64, 8192, 4096), (64, 6144, 3072), (64, 2560, 2560), (64, 5120, 4096)]:
+        assert L.rk_npu_matmul_k_partition_query(rows, k, tile) == 0
+    for rows, k, tile in [(64, 8192, 2752), (5, 8192, 2752), (64, 3840, 3840), (64, 3840, 4096),
+                          (0, 8192, 4096), (64, 8192, 0)]:
+        assert L.rk_npu_matmul_k_partition_query(rows, k, tile) == F.RK_NPU_ERR_PARAM
+
+
+def test_queries_and_config_init_without_a_device():
+    L = F.lib()
+    req = F.rk_npu_matmul_weight_requirements()
+    assert L.rk_npu_f32i8f32_weights_memory_query(ctypes.byref(F.rk_npu_matmul_weight_config(2560, 9728, 2560)),
+                                                  ctypes.byref(req)) == 0
+    assert req.bytes == 2560 * 9728 + 9728 * 4
+    nb = ctypes.c_uint64()
+    assert L.rk_npu_i4_weights_memory_query(ctypes.byref(F.rk_npu_i4_weight_config(2560, 19456, 0)),
+                                            ctypes.byref(nb)) == 0
+    assert nb.value == 2560 * 19456 // 2 + 19456 * 4
+    cfg = F.rk_npu_w4a8_config()
+    L.rk_npu_w4a8_config_init(ctypes.byref(cfg), 128, 19456, 2560)
+    assert (cfg.M, cfg.N, cfg.K, cfg.m_tile, cfg.n_tile) == (128, 19456, 2560, 64, 1024)
+    info = F.rk_npu_w4a8_memory_info_ex()
+    opt = F.rk_npu_w4a8_options()
+    L.rk_npu_w4a8_options_init(ctypes.byref(opt))
+    assert L.rk_npu_w4a8_memory_query_ex(ctypes.byref(cfg), ctypes.byref(opt), ctypes.byref(info)) == 0
+    assert info.workspace_bytes > 128 * 2560
+    at = F.rk_npu_matmul_autotune_config()
+    L.rk_npu_matmul_autotune_config_init(ctypes.byref(at), 1, 256, 256)
+    s1, s2 = F.rk_npu_matmul_strategy(), F.rk_npu_matmul_strategy()
+    assert L.rk_npu_matmul_autotune_cache_load(None, b"/nonexistent", F.RK_NPU_MATMUL_F32I8F32_DYNAMIC,
+                                               ctypes.byref(at), ctypes.byref(s1),
+                                               ctypes.byref(s2)) == F.RK_NPU_ERR_CACHE_MISS
+    mc = F.rk_npu_moe_w8_config()
+    L.rk_npu_moe_w8_config_init(ctypes.byref(mc), 2048, 768, 128, 0, 8, 512)
+    assert (mc.weights.hidden, mc.weights.intermediate, mc.weights.routed_experts, mc.top, mc.max_rows) == \
+        (2048, 768, 128, 8, 512)
+
+
+def test_plans():
+    L = F.lib()
+    plan = F.rk_npu_hip_plan()
+    assert L.rk_npu_hip_linear_plan(1, 2560, 19456, 4, ctypes.byref(plan)) == 0
+    assert plan.kind == 0 and plan.block_n == 64 and plan.k_splits >= 1
+    assert L.rk_npu_hip_linear_plan(4096, 2560, 9728, 8, ctypes.byref(plan)) == 0
+    assert plan.kind == 1 and plan.block_m == 256 and plan.block_n == 256
+    assert L.rk_npu_hip_linear_plan(0, 2560, 9728, 8, ctypes.byref(plan)) == F.RK_NPU_ERR_PARAM
+
+
+def test_open_without_gpu_returns_null_or_context():
+    L = F.lib()
+    ctx = L.rk_npu_open(b"999")
+    assert not ctx  # no such ordinal on any box
+    assert not L.rk_npu_iommu_domain_create(None, 0)
+    assert not L.rk_npu_w4a8_weights_create(None, ctypes.byref(F.rk_npu_i4_weight_config(8, 8, 0)), None, None)
+
+
+def test_host_mirror_logic():
+    """src/npu.rs:1442-1466 (validate) and the bucket rule."""
+    assert [npu.bucket(r) for r in (1, 2, 3, 5, 9, 17, 65, 128, 129, 192, 193, 256)] == \
+        [1, 2, 4, 8, 16, 32, 128, 128, 192, 192, 256, 256]
+    for bad in (0, 257):
+        with pytest.raises(npu.NpuError):
+            npu.bucket(bad)
+    for bits in (4, 8):
+        m = npu.QuantMatrix(bits, 64, 128, np.zeros(64 * 128, np.int8), np.ones(128, np.float32))
+        m.validate()
+        m.codes = m.codes[:-1]
+        with pytest.raises(npu.NpuError):
+            m.validate()
+        m.codes = np.zeros(64 * 128, np.int8)
+        m.scales = np.ones(0, np.float32)
+        with pytest.raises(npu.NpuError):
+            m.validate()
+        m.scales = np.ones(129, np.float32)
+        with pytest.raises(npu.NpuError):
+            m.validate()
+        m.scales = np.ones(128, np.float32)
+        m.k = 2**64
+        with pytest.raises(npu.NpuError):
+            m.validate()
+    with pytest.raises(npu.NpuError):
+        npu.QuantMatrix(3, 1, 1, np.zeros(1, np.int8), np.ones(1, np.float32)).validate()
+
+
+def test_router_mirror_matches_oracle():
+    from oracle import oracle
+    g = np.random.default_rng(3)
+    for _ in range(20):
+        logits = g.standard_normal(128).astype(np.float32)
+        ids, w = npu.routes(logits, 8)
+        oi, ow = oracle.routes(logits, 8)
+        assert ids == oi.tolist()
+        assert np.allclose(w, ow, rtol=0, atol=2e-7)

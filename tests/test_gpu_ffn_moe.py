@@ -1,0 +1,204 @@
+"""GPU parity of the fused FFN (gate_up -> SwiGLU -> requant -> down) and the
+grouped routed MoE FFN against the oracle, through the C ABI."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from oracle import oracle
+from open_rknpu2_lm_infer_amd import _ffi as F
+from open_rknpu2_lm_infer_amd import npu
+from tests import refdata as R
+
+pytestmark = pytest.mark.gpu
+
+
+def _ptr(a, t):
+    return a.ctypes.data_as(ctypes.POINTER(t))
+
+
+class FFN:
+    """Gate_up (W4) and down (W4 or W8) weights plus same-M workspaces."""
+
+    def __init__(self, backend, h, f, m, dn_bits, seed_name):
+        L = F.lib()
+        self.gc, self.gs = R.weights(2, seed_name + "-gu", 4, h, 2 * f)
+        self.dc, self.ds = R.weights(2, seed_name + "-dn", dn_bits, f, h)
+        self.h, self.f, self.m, self.dn_bits = h, f, m, dn_bits
+        dom = backend.domain
+        self.gw = npu._Handle(L.rk_npu_w4a8_weights_create(dom, ctypes.byref(F.rk_npu_i4_weight_config(h, 2 * f, 0)),
+                                                           _ptr(self.gc.reshape(-1), ctypes.c_int8),
+                                                           _ptr(self.gs, ctypes.c_float)),
+                              L.rk_npu_w4a8_weights_free, "gate_up", backend._shared)
+        cfg = F.rk_npu_w4a8_config()
+        opt = F.rk_npu_w4a8_options()
+        L.rk_npu_w4a8_config_init(ctypes.byref(cfg), m, 2 * f, h)
+        L.rk_npu_w4a8_options_init(ctypes.byref(opt))
+        self.gws = npu._Handle(L.rk_npu_w4a8_workspace_create_ex(dom, ctypes.byref(cfg), ctypes.byref(opt)),
+                               L.rk_npu_w4a8_workspace_free, "gate_up ws", backend._shared)
+        if dn_bits == 4:
+            self.dw = npu._Handle(L.rk_npu_w4a8_weights_create(dom, ctypes.byref(F.rk_npu_i4_weight_config(f, h, 0)),
+                                                               _ptr(self.dc.reshape(-1), ctypes.c_int8),
+                                                               _ptr(self.ds, ctypes.c_float)),
+                                  L.rk_npu_w4a8_weights_free, "down", backend._shared)
+            L.rk_npu_w4a8_config_init(ctypes.byref(cfg), m, h, f)
+            self.dws = npu._Handle(L.rk_npu_w4a8_workspace_create_ex(dom, ctypes.byref(cfg), ctypes.byref(opt)),
+                                   L.rk_npu_w4a8_workspace_free, "down ws", backend._shared)
+        else:
+            self.dw = npu._Handle(L.rk_npu_f32i8f32_weights_create(dom, ctypes.byref(F.rk_npu_matmul_weight_config(f, h, f)),
+                                                                   _ptr(self.dc.reshape(-1), ctypes.c_int8),
+                                                                   _ptr(self.ds, ctypes.c_float)),
+                                  L.rk_npu_f32i8f32_weights_free, "down", backend._shared)
+            st = F.rk_npu_matmul_strategy()
+            st.M, st.N, st.K, st.k_tile = m, h, f, f
+            self.dws = npu._Handle(L.rk_npu_matmul_workspace_create(dom, ctypes.byref(st)),
+                                   L.rk_npu_matmul_workspace_free, "down ws", backend._shared)
+
+    def run(self, x):
+        out = np.zeros((self.m, self.h), np.float32)
+        x = np.ascontiguousarray(x, np.float32)
+        npu.check(F.lib().rk_npu_w4a8_run_ffn_f32(self.gws.raw, self.gw.raw, self.dws.raw, self.dw.raw,
+                                                  self.dn_bits, _ptr(x, ctypes.c_float), _ptr(out, ctypes.c_float),
+                                                  None), "FFN")
+        return out
+
+
+@pytest.mark.parametrize("dn_bits", [4, 8])
+@pytest.mark.parametrize("m", [1, 4, 8, 64, 128])
+def test_fused_ffn_matches_oracle(dn_bits, m):
+    backend = npu.Backend(npu.ModelOptions(chunk=128))
+    ffn = FFN(backend, 256, 384, m, dn_bits, f"ffn{m}")
+    x = R.activations(2, f"ffn-x{m}", m, 256)
+    print(f"ffn dn_bits={dn_bits} m={m}", flush=True)
+    out = ffn.run(x)
+    ref, mid = oracle.ffn(ffn.gc, ffn.gs, ffn.dc, ffn.ds, x, with_middle=True)
+    assert np.array_equal(out, ref)
+    # the fused path equals run_swiglu followed by Linear::run on the middle
+    g = np.zeros((m, 384), np.float32)
+    assert np.array_equal(mid, oracle.linear_swiglu(ffn.gc, ffn.gs, x))
+
+
+def test_ffn_qwen3_4b_m512_sampled_rows():
+    """Prefill FFN block at its real shape: M=512, H=2560, F=9728, W4 gate_up,
+    W8 down. Rows are independent, so sampled rows are checked against the oracle."""
+    backend = npu.Backend(npu.ModelOptions(chunk=256))
+    ffn = FFN(backend, 2560, 9728, 512, 8, "ffn512")
+    x = R.activations(2, "ffn512-x", 512, 2560)
+    out = ffn.run(x)
+    rows = np.array([0, 1, 77, 255, 256, 300, 511])
+    ref = oracle.ffn(ffn.gc, ffn.gs, ffn.dc, ffn.ds, x[rows])
+    assert np.array_equal(out[rows], ref)
+    assert np.all(np.isfinite(out))
+
+
+def moe_bank(h, inter, experts, dn_bits, tag):
+    gate = [npu.QuantMatrix(4, h, 2 * inter, *R.weights(4, f"{tag}-gu{e}", 4, h, 2 * inter)) for e in range(experts)]
+    down = [npu.QuantMatrix(dn_bits, inter, h, *R.weights(4, f"{tag}-dn{e}", dn_bits, inter, h)) for e in range(experts)]
+    return gate, down
+
+
+def routed(rows, experts, top, tag):
+    g = R.rng_for(4, tag)
+    logits = g.standard_normal((rows, experts)).astype(np.float32)
+    ids = np.zeros((rows, top), np.int32)
+    w = np.zeros((rows, top), np.float32)
+    for r in range(rows):
+        i, v = oracle.routes(logits[r], top)
+        ids[r], w[r] = i, v
+    return ids, w
+
+
+@pytest.mark.parametrize("dn_bits", [4, 8])
+@pytest.mark.parametrize("rows", [1, 3, 40])
+def test_moe_matches_oracle(dn_bits, rows):
+    h, inter, experts, top = 256, 96, 16, 4
+    backend = npu.Backend(npu.ModelOptions(chunk=64))
+    gate, down = moe_bank(h, inter, experts, dn_bits, f"moe{dn_bits}")
+    moe = backend.load_moe(gate, down, top)
+    x = R.activations(4, f"moe-x{rows}", rows, h)
+    ids, w = routed(rows, experts, top, f"moe-r{rows}")
+    if rows >= 3:
+        ids[1, 1] = ids[1, 0]      # duplicate expert in one row
+        w[2, 3] = np.float32(0.0)  # skipped route
+    out = np.zeros((rows, h), np.float32)
+    print(f"moe dn_bits={dn_bits} rows={rows}", flush=True)
+    moe.run(x, ids, w, out, rows)
+    ref = oracle.moe([(g.codes, g.scales) for g in gate], [(d.codes, d.scales) for d in down], x, ids, w)
+    assert np.array_equal(out, ref)
+    again = np.zeros_like(out)
+    moe.run(x, ids, w, again, rows)
+    assert np.array_equal(again, out)
+
+
+def test_moe_with_shared_w8_expert():
+    h, inter, experts, top, rows = 128, 64, 8, 2, 5
+    backend = npu.Backend(npu.ModelOptions(chunk=16))
+    gate, down = moe_bank(h, inter, experts, 4, "moesh")
+    sg = npu.QuantMatrix(8, h, 2 * inter, *R.weights(4, "sh-gu", 8, h, 2 * inter))
+    sd = npu.QuantMatrix(8, inter, h, *R.weights(4, "sh-dn", 8, inter, h))
+    moe = backend.load_moe_with_shared(gate, down, top, (sg, sd))
+    x = R.activations(4, "moesh-x", rows, h)
+    ids, w = routed(rows, experts, top, "moesh-r")
+    out = np.zeros((rows, h), np.float32)
+    moe.run(x, ids, w, out, rows)
+    ref = oracle.moe([(g.codes, g.scales) for g in gate], [(d.codes, d.scales) for d in down], x, ids, w,
+                     shared=((sg.codes, sg.scales), (sd.codes, sd.scales)))
+    assert np.array_equal(out, ref)
+
+
+def test_moe_rejects_out_of_range_ids():
+    backend = npu.Backend(npu.ModelOptions(chunk=4))
+    gate, down = moe_bank(64, 32, 4, 4, "moebad")
+    moe = backend.load_moe(gate, down, 2)
+    x = np.zeros((1, 64), np.float32)
+    with pytest.raises(npu.NpuError):
+        moe.run(x, np.array([[0, 4]], np.int32), np.array([[0.5, 0.5]], np.float32), np.zeros((1, 64), np.float32), 1)
+
+
+def test_moe_35b_a3b_shape_t512_sampled_rows():
+    """Config-4 shape: hidden 2048, 128 experts, top-8, intermediate 768,
+    W4 gate_up + W8 down, T=512 ragged per-expert batches."""
+    h, inter, experts, top, rows = 2048, 768, 128, 8, 512
+    backend = npu.Backend(npu.ModelOptions(chunk=256))
+    backend.options.chunk = 512  # MoE max_rows (the op layer caps Linear at 256, not MoE)
+    gate, down = moe_bank(h, inter, experts, 8, "moe35")
+    moe = backend.load_moe(gate, down, top)
+    x = R.activations(4, "moe35-x", rows, h)
+    ids, w = routed(rows, experts, top, "moe35-r")
+    out = np.zeros((rows, h), np.float32)
+    moe.run(x, ids, w, out, rows)
+    sample = np.array([0, 5, 128, 300, 511])
+    ref = oracle.moe([(g.codes, g.scales) for g in gate], [(d.codes, d.scales) for d in down], x[sample],
+                     ids[sample], w[sample])
+    assert np.array_equal(out[sample], ref)
+
+
+def test_moe_blob_export_import_and_slot_swap():
+    h, inter, experts, top = 128, 64, 4, 2
+    backend = npu.Backend(npu.ModelOptions(chunk=8))
+    gate, down = moe_bank(h, inter, experts, 4, "blob")
+    moe = backend.load_moe(gate, down, top)
+    x = R.activations(4, "blob-x", 3, h)
+    ids = np.array([[0, 1], [2, 3], [1, 2]], np.int32)
+    w = np.array([[0.5, 0.5], [0.7, 0.3], [0.9, 0.1]], np.float32)
+    base = np.zeros((3, h), np.float32)
+    moe.run(x, ids, w, base, 3)
+    blobs = [moe.export(e) for e in range(experts)]
+    assert all(len(b) == moe.blob_bytes() for b in blobs)
+    # reversed bank via import into a second bank of the same geometry
+    other = backend.load_moe(gate[::-1], down[::-1], top)
+    for e in range(experts):
+        other.import_(e, blobs[e])
+    out = np.zeros_like(base)
+    other.run(x, ids, w, out, 3)
+    assert np.array_equal(out, base)
+    # swap slots 0 and 3 between banks: other now holds gate[::-1][0] = gate[3] at 0
+    other.promote(0, moe, 3)
+    moe.promote(3, other, 0)  # swap back
+    out2 = np.zeros_like(base)
+    moe.run(x, ids, w, out2, 3)
+    assert np.array_equal(out2, base)
+    corrupt = bytearray(blobs[0])
+    corrupt[0] ^= 0xFF
+    with pytest.raises(npu.NpuError):
+        other.import_(0, bytes(corrupt))
