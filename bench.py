@@ -1,0 +1,485 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantized-linear hot path on one MI355X.
+
+Primary line (the metric's decode half): W4A8 decode projection set of a
+Qwen3-4B-shaped layer (qkv 2560x6144, o 4096x2560, fused gate_up 2560x19456 +
+SwiGLU -> down 9728x2560), M=1, 36 layers with distinct seeded weights, fp16
+activations resident in HBM. value = algorithmic bytes / wall time (GB/s).
+
+Secondary workloads (same JSON line, "secondary"): M=4 decode, the M=4096
+W8A8/W4A8 prefill projection set x36 + lm_head (int8 TOPS), the M=512 FFN
+block x36, the M=128 W8A8 up projection, and the 35B-A3B-class MoE at T=512
+and T=1.
+
+Timing: the step runs eagerly (host launches between two synchronizations)
+and as a HIP graph replay (checked bit-exact against eager runs) between two
+HIP events; value uses the faster of the two, both are reported.
+roofline: the dominant kernel's algorithmic bytes (or ops) per launch over its
+average launch time: 36 back-to-back launches of that kernel alone (distinct
+layers' weights) captured in a graph and timed with HIP events on the replay
+stream.
+cpu_baseline: the C oracle (OpenMP) on a bounded sample of the same workload
+on this host's cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "int8 TOPS (% MFMA peak) at M=512/4096 prefill; HBM GB/s at M=1 decode"
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+
+# Qwen3-4B layer shapes
+H, Q, KV, F, LAYERS, VOCAB = 2560, 4096, 1024, 9728, 36, 151936
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def torch_setup():
+    import torch
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    torch.cuda.set_device(0)
+    return torch
+
+
+class Gen:
+    """Seeded device-side generators (torch's Philox on cuda) per tensor name."""
+
+    def __init__(self, torch, config):
+        self.torch = torch
+        self.config = config
+
+    def gen(self, name):
+        g = self.torch.Generator(device="cuda")
+        h = 0x5EED0000 + self.config
+        for c in name:
+            h = (h * 1000003 + ord(c)) & 0xFFFFFFFFFFFF
+        g.manual_seed(h)
+        return g
+
+    def codes(self, name, bits, k, n):
+        lo, hi = (-8, 8) if bits == 4 else (-127, 128)
+        return self.torch.randint(lo, hi, (k, n), dtype=self.torch.int8, device="cuda", generator=self.gen(name))
+
+    def scales(self, name, n):
+        return (self.torch.rand(n, device="cuda", generator=self.gen(name + "/s")) * 0.009 + 0.001).float()
+
+    def acts(self, name, rows, k, outliers):
+        t = self.torch
+        g = self.gen(name)
+        x = t.randn(rows, k, device="cuda", generator=g)
+        if outliers:
+            cols = t.randperm(k, device="cuda", generator=g)[: int(math.ceil(0.005 * k))]
+            x[:, cols] *= 20.0
+        return x.half()
+
+
+def lin_bytes(bits, k, n, rows):
+    """Algorithmic bytes of one linear: weights at storage width + f32 scales +
+    fp16 activations in and out."""
+    return k * n * bits // 8 + 4 * n + 2 * rows * (k + n)
+
+
+def time_steps(torch, step, steps, warmup):
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1000.0 / steps
+
+
+def graph_time(torch, fn, reps, check=None):
+    """Capture fn() into a HIP graph and time `reps` replays between two events
+    recorded on the replay stream. check(): called after an eager run and after
+    a replay; both results must be identical (graph replay correctness)."""
+    eager_ref = None
+    fn()
+    torch.cuda.synchronize()
+    if check is not None:
+        eager_ref = check()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()  # warm the capture stream
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=s):
+            fn()
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    ok = True
+    if check is not None:
+        for _ in range(3):
+            g.replay()
+            torch.cuda.synchronize()
+            got = check()
+            ok = ok and all(torch.equal(a, b) for a, b in zip(eager_ref, got))
+            fn()  # eager work between replays
+            torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    cur = torch.cuda.current_stream()
+    e0.record(cur)
+    for _ in range(reps):
+        g.replay()
+    e1.record(cur)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps, ok
+
+
+def roofline(achieved, bound, kernel, avg_us, work, launches, method):
+    if bound == "hbm":
+        peak, unit = HBM_PEAK_GBS, "GB/s"
+    else:
+        peak, unit = INT8_PEAK_TOPS, "TFLOP/s"
+    return {"bound": bound, "kernel": kernel, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+            "frac": round(achieved / peak, 4), "traffic": None, "avg_us": round(avg_us, 3),
+            "work_per_launch": work, "launches": launches, "method": method}
+
+
+# ---------------------------------------------------------------------------------
+# workloads
+# ---------------------------------------------------------------------------------
+
+class DenseLayers:
+    """36 layers of qkv / o / gate_up / down weights and shared workspaces."""
+
+    def __init__(self, torch, ctx, gen, rows, bits, layers=LAYERS, outliers=False, tag="dec"):
+        from open_rknpu2_lm_infer_amd import device as D
+        self.torch, self.ctx, self.rows, self.layers = torch, ctx, rows, layers
+        qkv_b, o_b, gu_b, dn_b = bits
+        self.w = []
+        self.host0 = None
+        for l in range(layers):
+            mats = {}
+            for name, b, k, n in (("qkv", qkv_b, H, Q + 2 * KV), ("o", o_b, Q, H), ("gate_up", gu_b, H, 2 * F),
+                                  ("down", dn_b, F, H)):
+                codes = gen.codes(f"{tag}/l{l}/{name}", b, k, n)
+                scales = gen.scales(f"{tag}/l{l}/{name}", n)
+                mats[name] = ctx.weights(b, codes, scales)
+                if l == 0:
+                    if self.host0 is None:
+                        self.host0 = {}
+                    self.host0[name] = (b, codes.cpu().numpy(), scales.cpu().numpy())
+                del codes, scales
+            self.w.append(mats)
+        self.x_qkv = gen.acts(f"{tag}/x_qkv", rows, H, outliers)
+        self.x_o = gen.acts(f"{tag}/x_o", rows, Q, outliers)
+        self.x_ffn = gen.acts(f"{tag}/x_ffn", rows, H, outliers)
+        self.y_qkv = torch.empty(rows, Q + 2 * KV, dtype=torch.float16, device="cuda")
+        self.y_o = torch.empty(rows, H, dtype=torch.float16, device="cuda")
+        self.y_ffn = torch.empty(rows, H, dtype=torch.float16, device="cuda")
+        w0 = self.w[0]
+        self.ws = {name: ctx.workspace(w0[name].bits, rows, w0[name].k, w0[name].n) for name in w0}
+        self.D = D
+
+    def step(self):
+        D, ctx, r = self.D, self.ctx, self.rows
+        for mats in self.w:
+            D.linear(ctx, mats["qkv"], self.x_qkv, self.y_qkv, r, ws=self.ws["qkv"])
+            D.linear(ctx, mats["o"], self.x_o, self.y_o, r, ws=self.ws["o"])
+            D.ffn(ctx, mats["gate_up"], mats["down"], self.x_ffn, self.y_ffn, r, gws=self.ws["gate_up"],
+                  dws=self.ws["down"])
+
+    def bytes_per_layer(self):
+        w0, r = self.w[0], self.rows
+        return sum(lin_bytes(w0[n].bits, w0[n].k, w0[n].n, r) for n in w0)
+
+    def ops_per_layer(self):
+        w0 = self.w[0]
+        return sum(2.0 * self.rows * w0[n].k * w0[n].n for n in w0)
+
+
+def cpu_decode_baseline(layer0, rows, budget_s=10.0):
+    """Oracle (C, OpenMP) on layer 0's decode set, repeated for ~budget_s."""
+    import numpy as np
+    from oracle import oracle
+    g = np.random.default_rng(1)
+    x = g.standard_normal((rows, H)).astype(np.float16).astype(np.float32)
+    xo = g.standard_normal((rows, Q)).astype(np.float16).astype(np.float32)
+    qkv, o, gu, dn = (layer0[n] for n in ("qkv", "o", "gate_up", "down"))
+    bytes_layer = sum(lin_bytes(b, c.shape[0], c.shape[1], rows) for b, c, _ in (qkv, o, gu, dn))
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        oracle.linear(qkv[1], qkv[2], x)
+        oracle.linear(o[1], o[2], xo)
+        oracle.ffn(gu[1], gu[2], dn[1], dn[2], x)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    return {"value": round(bytes_layer * reps / el / 1e9, 3), "unit": "GB/s", "cores": oracle.threads(),
+            "kind": "port",
+            "sample": f"layer 0 of 36, M={rows} decode set (qkv, o, gate_up+SwiGLU->requant->down), "
+                      f"{reps} repetitions in {el:.1f} s; same algorithmic-byte count as the GPU line"}
+
+
+def run_decode(torch, ctx, rows, steps, warmup, want_cpu, want_roofline=True):
+    from open_rknpu2_lm_infer_amd import device as D
+    gen = Gen(torch, 1)
+    log(f"[bench] decode M={rows}: creating 36 layers of W4 weights")
+    t = DenseLayers(torch, ctx, gen, rows, (4, 4, 4, 4), tag=f"dec{rows}")
+    nbytes = t.bytes_per_layer() * LAYERS
+    ms_eager = time_steps(torch, t.step, steps, warmup)
+    check = lambda: [t.y_qkv.clone(), t.y_o.clone(), t.y_ffn.clone()]
+    ms_graph, ok = graph_time(torch, t.step, steps, check)
+    ms = min(ms_graph, ms_eager) if ok else ms_eager
+    out = {"ms_per_step": ms, "value": nbytes / (ms * 1e-3) / 1e9, "bytes_per_step": nbytes,
+           "ms_eager": ms_eager, "ms_graph": ms_graph, "graph_matches_eager": ok}
+    log(f"[bench] decode M={rows}: eager {ms_eager:.3f} ms/step, graph {ms_graph:.3f} ms/step "
+        f"(replay bit-exact: {ok}) -> {out['value']:.1f} GB/s")
+    if want_roofline:
+        # Dominant kernel: the gate_up GEMV (25 MB of W4 weights per launch),
+        # the same kernel the fused FFN launches. 36 launches on distinct
+        # layers' weights, graph-captured, between two events.
+        gu = [mats["gate_up"] for mats in t.w]
+        mid = torch.empty(rows, F, dtype=torch.float16, device="cuda")
+        ws = t.ws["gate_up"]
+        def gu_run():
+            for w in gu:
+                D.linear(ctx, w, t.x_ffn, mid, rows, swiglu=True, ws=ws)
+        ms_gu, _ = graph_time(torch, gu_run, steps)
+        per_launch_us = ms_gu * 1e3 / len(gu)
+        work = lin_bytes(4, H, 2 * F, rows)
+        out["roofline"] = roofline(work / (per_launch_us * 1e-6) / 1e9, "hbm",
+                                   f"gemv_kernel<__half,{rows if rows in (1, 2, 4) else 8},4,SwiGLU> "
+                                   f"gate_up 2560x19456 W4, M={rows}", per_launch_us, work, len(gu) * steps,
+                                   "graph of 36 back-to-back launches (distinct weights), HIP events on the replay stream")
+        log(f"[bench] decode roofline: {out['roofline']}")
+    if want_cpu:
+        log("[bench] cpu baseline (oracle) on layer 0 ...")
+        out["cpu_baseline"] = cpu_decode_baseline(t.host0, rows)
+        log(f"[bench] cpu baseline: {out['cpu_baseline']}")
+    del t
+    return out
+
+
+def run_prefill(torch, ctx, rows, steps, warmup):
+    """Config 3: M=4096, qkv/o/down W8A8, gate_up W4A8, 36 layers + lm_head W8."""
+    from open_rknpu2_lm_infer_amd import device as D
+    gen = Gen(torch, 3)
+    log(f"[bench] prefill M={rows}: creating 36 layers + lm_head")
+    t = DenseLayers(torch, ctx, gen, rows, (8, 8, 4, 8), outliers=True, tag="pf")
+    head = ctx.weights(8, gen.codes("pf/lm_head", 8, H, VOCAB), gen.scales("pf/lm_head", VOCAB))
+    y_head = torch.empty(rows, VOCAB, dtype=torch.float16, device="cuda")
+    ws_head = ctx.workspace(8, rows, H, VOCAB)
+
+    def step():
+        t.step()
+        D.linear(ctx, head, t.x_qkv, y_head, rows, ws=ws_head)
+
+    ms = time_steps(torch, step, steps, warmup)
+    ops = t.ops_per_layer() * LAYERS + 2.0 * rows * H * VOCAB
+    # dominant kernel: the W4 gate_up GEMM with fused SwiGLU, 36 launches
+    gu = [mats["gate_up"] for mats in t.w]
+    mid = torch.empty(rows, F, dtype=torch.float16, device="cuda")
+    def gu_run():
+        for w in gu:
+            D.linear(ctx, w, t.x_ffn, mid, rows, swiglu=True, ws=t.ws["gate_up"])
+    ms_gu, _ = graph_time(torch, gu_run, max(2, steps // 2))
+    per_us = ms_gu * 1e3 / len(gu)
+    work = 2.0 * rows * H * 2 * F
+    res = {"workload": f"prefill M={rows}: Qwen3-4B qkv/o/down W8A8 + gate_up W4A8 (+SwiGLU) x36 + lm_head W8A8",
+           "value": round(ops / (ms * 1e-3) / 1e12, 2), "unit": "TOPS", "ms_per_step": round(ms, 3),
+           "frac_of_int8_peak": round(ops / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4),
+           "roofline": roofline(work / (per_us * 1e-6) / 1e12, "mfma",
+                                f"gemm_kernel<256,256,2,2,W4,SwiGLU> gate_up 2560x19456, M={rows}", per_us, work,
+                                len(gu), "graph of 36 back-to-back launches, HIP events on the replay stream")}
+    log(f"[bench] prefill: {res['value']} TOPS ({ms:.2f} ms/step)")
+    del t, head
+    return res
+
+
+def run_ffn512(torch, ctx, steps, warmup, rows=512):
+    """Config 2: M=512 W4A8 gate_up -> SwiGLU -> requant -> W8A8 down, 36 layers."""
+    from open_rknpu2_lm_infer_amd import device as D
+    gen = Gen(torch, 2)
+    layers = []
+    for l in range(LAYERS):
+        layers.append((ctx.weights(4, gen.codes(f"ffn/l{l}/gu", 4, H, 2 * F), gen.scales(f"ffn/l{l}/gu", 2 * F)),
+                       ctx.weights(8, gen.codes(f"ffn/l{l}/dn", 8, F, H), gen.scales(f"ffn/l{l}/dn", H))))
+    x = gen.acts("ffn/x", rows, H, True)
+    y = torch.empty(rows, H, dtype=torch.float16, device="cuda")
+    gws = ctx.workspace(4, rows, H, 2 * F)
+    dws = ctx.workspace(8, rows, F, H)
+
+    def step():
+        for gu, dn in layers:
+            D.ffn(ctx, gu, dn, x, y, rows, gws=gws, dws=dws)
+
+    ms = time_steps(torch, step, steps, warmup)
+    ops = LAYERS * 2.0 * rows * (H * 2 * F + F * H)
+    res = {"workload": "FFN block M=512: W4A8 gate_up 2560->2x9728 + SwiGLU + requant + W8A8 down, 36 layers",
+           "value": round(ops / (ms * 1e-3) / 1e12, 2), "unit": "TOPS", "ms_per_step": round(ms, 3),
+           "frac_of_int8_peak": round(ops / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4)}
+    log(f"[bench] ffn512: {res['value']} TOPS")
+    del layers
+    return res
+
+
+def run_up128(torch, ctx, steps, warmup, rows=128):
+    """Config 0: single W8A8 linear M=128 K=2560 N=9728, outlier channels."""
+    from open_rknpu2_lm_infer_amd import device as D
+    gen = Gen(torch, 0)
+    w = ctx.weights(8, gen.codes("up/w", 8, H, F), gen.scales("up/w", F))
+    x = gen.acts("up/x", rows, H, True)
+    y = torch.empty(rows, F, dtype=torch.float16, device="cuda")
+    ws = ctx.workspace(8, rows, H, F)
+    step = lambda: D.linear(ctx, w, x, y, rows, ws=ws)
+    ms = time_steps(torch, step, steps * 10, warmup)
+    ops = 2.0 * rows * H * F
+    return {"workload": "W8A8 linear M=128 K=2560 N=9728 (Qwen3-4B FFN up)", "value": round(ops / (ms * 1e-3) / 1e12, 2),
+            "unit": "TOPS", "ms_per_step": round(ms, 4),
+            "gbs": round(lin_bytes(8, H, F, rows) / (ms * 1e-3) / 1e9, 1)}
+
+
+def run_moe(torch, ctx, steps, warmup, tokens_list=(512, 1)):
+    """Config 4: hidden 2048, 128 experts, top-8, I=768, routed W4 gate_up +
+    W8 down; shared W8 FFN of intermediate 2048 through the dense path."""
+    import ctypes
+
+    import numpy as np
+
+    from open_rknpu2_lm_infer_amd import _ffi as F_
+    from open_rknpu2_lm_infer_amd import device as D
+    from open_rknpu2_lm_infer_amd import npu
+    from oracle import oracle
+    h, inter, experts, top, sh_inter = 2048, 768, 128, 8, 2048
+    g = np.random.default_rng(0x5EED0004)
+    L = F_.lib()
+    keep, arr = [], (F_.rk_npu_moe_w8_expert * experts)()
+    for e in range(experts):
+        gc = g.integers(-8, 8, (h, 2 * inter), dtype=np.int8)
+        gs = g.uniform(0.001, 0.01, 2 * inter).astype(np.float32)
+        dc = g.integers(-127, 128, (inter, h), dtype=np.int8)
+        ds = g.uniform(0.001, 0.01, h).astype(np.float32)
+        keep.append((gc, gs, dc, ds))
+        arr[e] = F_.rk_npu_moe_w8_expert(gc.ctypes.data_as(F_.i8p), gs.ctypes.data_as(F_.f32p),
+                                         dc.ctypes.data_as(F_.i8p), ds.ctypes.data_as(F_.f32p))
+    max_t = max(tokens_list)
+    cfg = F_.rk_npu_moe_w8_config()
+    L.rk_npu_moe_w8_config_init(ctypes.byref(cfg), h, inter, experts, 0, top, max_t)
+    bank = npu._Handle(L.rk_npu_moe_w4w8_weights_create(ctx.domain, ctypes.byref(cfg.weights), arr),
+                       L.rk_npu_moe_w8_weights_free, "MoE bank", ctx.shared)
+    work = npu._Handle(L.rk_npu_moe_w4w8_workspace_create(ctx.domain, ctypes.byref(cfg)),
+                       L.rk_npu_moe_w8_workspace_free, "MoE workspace", ctx.shared)
+    del keep, arr
+    gen = Gen(torch, 4)
+    sgu = ctx.weights(8, gen.codes("moe/sh/gu", 8, h, 2 * sh_inter), gen.scales("moe/sh/gu", 2 * sh_inter))
+    sdn = ctx.weights(8, gen.codes("moe/sh/dn", 8, sh_inter, h), gen.scales("moe/sh/dn", h))
+    results = []
+    for T in tokens_list:
+        logits = g.standard_normal((T, experts)).astype(np.float32)
+        ids = np.zeros((T, top), np.int32)
+        rw = np.zeros((T, top), np.float32)
+        for r in range(T):
+            ids[r], rw[r] = oracle.routes(logits[r], top)
+        x = torch.from_numpy(g.standard_normal((T, h)).astype(np.float32)).cuda()
+        d_ids = torch.from_numpy(ids).cuda()
+        d_rw = torch.from_numpy(rw).cuda()
+        y = torch.empty(T, h, dtype=torch.float32, device="cuda")
+        ys = torch.empty(T, h, dtype=torch.float16, device="cuda")
+        xs = x.half()
+        gws = ctx.workspace(8, T, h, 2 * sh_inter)
+        dws = ctx.workspace(8, T, sh_inter, h)
+
+        def step():
+            rc = L.rk_npu_hip_moe_run(work.raw, bank.raw, T, ctypes.c_void_p(x.data_ptr()),
+                                      ctypes.c_void_p(d_ids.data_ptr()), ctypes.c_void_p(d_rw.data_ptr()),
+                                      ctypes.c_void_p(y.data_ptr()), D.current_stream())
+            npu.check(rc, "MoE run")
+            D.ffn(ctx, sgu, sdn, xs, ys, T, gws=gws, dws=dws)
+
+        ms = time_steps(torch, step, steps * (10 if T == 1 else 1), warmup)
+        routed_ops = 2.0 * T * top * (h * 2 * inter + inter * h)
+        shared_ops = 2.0 * T * (h * 2 * sh_inter + sh_inter * h)
+        routed_bytes = min(experts, T * top) * (h * 2 * inter // 2 + 4 * 2 * inter + inter * h + 4 * h)
+        shared_bytes = h * 2 * sh_inter + 4 * 2 * sh_inter + sh_inter * h + 4 * h
+        res = {"workload": f"MoE 35B-A3B-class T={T}: h2048 E128 top8 I768 W4 gate_up + W8 down, shared W8 FFN I2048",
+               "ms_per_step": round(ms, 4)}
+        if T >= 64:
+            res.update(value=round((routed_ops + shared_ops) / (ms * 1e-3) / 1e12, 2), unit="TOPS")
+        else:
+            res.update(value=round((routed_bytes + shared_bytes) / (ms * 1e-3) / 1e9, 1), unit="GB/s")
+        log(f"[bench] moe T={T}: {res['value']} {res['unit']} ({ms:.3f} ms)")
+        results.append(res)
+    return results
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--primary-only", action="store_true", help="skip the secondary workloads")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: this build has no multi-GPU path "
+              f"(--gpus {args.gpus} requested); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    torch = torch_setup()
+    from open_rknpu2_lm_infer_amd import device as D
+    ctx = D.DeviceContext(0)
+    primary = run_decode(torch, ctx, 1, args.steps, args.warmup, not args.no_cpu_baseline)
+    secondary = []
+    if not args.primary_only:
+        m4 = run_decode(torch, ctx, 4, args.steps, args.warmup, False, want_roofline=True)
+        secondary.append({"workload": "decode M=4 (MTP/draft verify), same W4A8 set x36",
+                          "value": round(m4["value"], 1), "unit": "GB/s", "ms_per_step": round(m4["ms_per_step"], 4),
+                          "roofline": m4["roofline"]})
+        secondary.append(run_prefill(torch, ctx, 4096, max(4, args.steps // 2), 2))
+        secondary.append(run_ffn512(torch, ctx, max(4, args.steps // 2), 2))
+        secondary.append(run_up128(torch, ctx, args.steps, args.warmup))
+        secondary.extend(run_moe(torch, ctx, max(4, args.steps // 2), 2))
+    for s in secondary:
+        s.pop("kernels", None)
+        if "roofline" in s:
+            s["roofline"].pop("work_per_launch", None)
+    roof = dict(primary["roofline"])
+    roof.pop("work_per_launch", None)
+    config_extra = {"ms_eager": round(primary["ms_eager"], 4), "ms_graph": round(primary["ms_graph"], 4),
+                    "graph_matches_eager": primary["graph_matches_eager"]}
+    line = {
+        "metric": METRIC,
+        "value": round(primary["value"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(primary["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded random W4 codes in [-8,7], f32 scales U(0.001,0.01), fp16 N(0,1) activations)",
+        "config": {"workload": "decode: Qwen3-4B-shaped W4A8 projection set (qkv 2560x6144, o 4096x2560, "
+                               "gate_up 2560x19456 + SwiGLU -> down 9728x2560), M=1, 36 layers",
+                   "rows": 1, "layers": 36, "weight_bits": 4, "activations": "fp16 in/out, per-token dynamic int8",
+                   "bytes_per_step": primary["bytes_per_step"], "parallelism": "single GPU",
+                   "timing": "faster of eager launches and HIP graph replay of the same step "
+                             "(replay checked bit-exact vs eager)", **config_extra},
+        "roofline": roof,
+        "cpu_baseline": primary.get("cpu_baseline"),
+        "secondary": secondary,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -76,6 +76,28 @@ int rk_npu_hip_workspace_codes(void* workspace, int bits, int rows, int8_t* code
  * callback still runs first). Returns the previous count. */
 int rk_npu_hip_inject_alloc_failures(int count);
 
+/* Kernel timing for measurement tools. Between profile_begin and
+ * profile_end every GEMM/GEMV/quantization launch of the library is
+ * bracketed by two HIP events recorded on the stream it is launched on (at
+ * most max_launches launches; later ones are not recorded). Not for use under
+ * graph capture. profile_read synchronizes the device and returns one entry
+ * per distinct (kind, bits, epilogue, rows, K, N) with its launch count and
+ * summed event time. kind: 0 GEMV, 1 MFMA GEMM, 2 quantization, 3 grouped GEMM. */
+typedef struct rk_npu_hip_kernel_stat {
+    int32_t kind;
+    int32_t bits;
+    int32_t epilogue;
+    int32_t rows;
+    int32_t K;
+    int32_t N;
+    int32_t launches;
+    double total_ms;
+    char name[64];
+} rk_npu_hip_kernel_stat;
+int rk_npu_hip_profile_begin(int max_launches);
+int rk_npu_hip_profile_end(void);
+int rk_npu_hip_profile_read(rk_npu_hip_kernel_stat* stats, int capacity, int* count);
+
 /* Launch plan the library uses for a linear of this shape, for diagnostics:
  * kind 0 = GEMV (no MFMA), 1 = MFMA GEMM; tile sizes and K splits. */
 typedef struct rk_npu_hip_plan {

@@ -138,6 +138,12 @@ class rk_npu_moe_import_timings(Structure):
                 ("down_sync_us", c_double), ("total_us", c_double)]
 
 
+class rk_npu_hip_kernel_stat(Structure):
+    _fields_ = [("kind", c_int32), ("bits", c_int32), ("epilogue", c_int32), ("rows", c_int32),
+                ("K", c_int32), ("N", c_int32), ("launches", c_int32), ("total_ms", c_double),
+                ("name", ctypes.c_char * 64)]
+
+
 class rk_npu_hip_plan(Structure):
     _fields_ = [("kind", c_int32), ("block_m", c_int32), ("block_n", c_int32),
                 ("k_splits", c_int32), ("grid", c_int32)]
@@ -241,6 +247,9 @@ SIGNATURES = {
     "rk_npu_hip_workspace_codes": (c_int, [c_void_p, c_int, c_int, i8p, f32p, i32p]),
     "rk_npu_hip_inject_alloc_failures": (c_int, [c_int]),
     "rk_npu_hip_linear_plan": (c_int, [c_int, c_int, c_int, c_int, P(rk_npu_hip_plan)]),
+    "rk_npu_hip_profile_begin": (c_int, [c_int]),
+    "rk_npu_hip_profile_end": (c_int, []),
+    "rk_npu_hip_profile_read": (c_int, [P(rk_npu_hip_kernel_stat), c_int, P(c_int)]),
 }
 
 RECLAIM_CALLBACK = ctypes.CFUNCTYPE(None, c_void_p)

@@ -7,8 +7,13 @@
 #include <chrono>
 #include <cstdlib>
 #include <cstring>
+#include <cstdio>
+#include <map>
 #include <mutex>
 #include <new>
+#include <string>
+#include <tuple>
+#include <vector>
 
 #include "kernels.hpp"
 #include "runtime.hpp"
@@ -23,6 +28,32 @@ double now_us() {
 }
 
 int device_of(Domain* d) { return d->ctx->device; }
+
+// --- launch profiling -----------------------------------------------------------
+
+struct ProfRecord {
+    int kind, bits, epi, rows, K, N;
+    std::string name;
+};
+static std::mutex g_prof_mu;
+static std::atomic<bool> g_prof_on{false};
+static std::vector<hipEvent_t> g_prof_events;
+static std::vector<ProfRecord> g_prof_records;
+
+int prof_begin(hipStream_t s, int kind, int bits, int epi, int rows, int K, int N, const char* name) {
+    if (!g_prof_on.load()) return -1;
+    std::lock_guard<std::mutex> lock(g_prof_mu);
+    const size_t slot = g_prof_records.size();
+    if (2 * slot + 1 >= g_prof_events.size()) return -1;
+    g_prof_records.push_back(ProfRecord{kind, bits, epi, rows, K, N, name});
+    (void)hipEventRecord(g_prof_events[2 * slot], s);
+    return (int)slot;
+}
+
+void prof_end(int slot, hipStream_t s) {
+    if (slot < 0) return;
+    (void)hipEventRecord(g_prof_events[2 * slot + 1], s);
+}
 
 static bool try_alloc(void** p, size_t bytes) {
     int pending = g_fail_allocs.load();
@@ -201,7 +232,7 @@ void weights_destroy(Weights* w) {
 // --- workspaces -------------------------------------------------------------
 
 struct WsLayout {
-    size_t a, codes, rows, c, acc, counters, total;
+    size_t a, codes, rows, c, part, total;
 };
 
 static WsLayout ws_layout(const Geometry& g, int M) {
@@ -211,9 +242,8 @@ static WsLayout ws_layout(const Geometry& g, int M) {
     L.codes = (size_t)(g.K_pad / 16) * M_alloc * 16;
     L.rows = round_up_z((size_t)M_alloc * 4, 256);
     L.c = round_up_z((size_t)M * g.N * 4, 256);
-    L.acc = round_up_z((size_t)8 * g.N_pad * 4, 256);
-    L.counters = round_up_z((size_t)(g.N_pad / 64) * 4, 256);
-    L.total = L.a + L.codes + 3 * L.rows + L.c + L.acc + L.counters;
+    L.part = round_up_z((size_t)8 * (g.N_pad / 8) * 4, 256);
+    L.total = L.a + L.codes + 3 * L.rows + L.c + L.part;
     return L;
 }
 
@@ -252,11 +282,8 @@ Workspace* workspace_create(Domain* d, int bits, int M, int K, int N) {
     off += L.rows;
     ws->c_f32 = reinterpret_cast<float*>(base + off);
     off += L.c;
-    ws->gemv_acc = reinterpret_cast<int*>(base + off);
-    off += L.acc;
-    ws->gemv_counters = reinterpret_cast<unsigned*>(base + off);
-    // Zero everything once: padding rows of the code planes, the split-K
-    // accumulators and arrival counters (kept zero between calls by the kernels).
+    ws->partmax = reinterpret_cast<float*>(base + off);
+    // Zero everything once (padding rows of the code planes stay zero).
     bool ok = hipMemset(base, 0, L.total) == hipSuccess &&
               hipStreamCreateWithFlags(&ws->stream, hipStreamNonBlocking) == hipSuccess &&
               hipDeviceSynchronize() == hipSuccess;
@@ -292,22 +319,19 @@ static int env_int(const char* name, int fallback) {
     return v ? std::atoi(v) : fallback;
 }
 
+// Activation codes of the whole K live in the GEMV's LDS.
+constexpr int GEMV_MAX_LDS = 60 * 1024;
+
 Plan plan_linear(int rows, const Geometry& g) {
     Plan p{};
-    if (rows <= 8) {
+    const int mr = rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : 8;
+    if (rows <= 8 && g.K_pad * mr <= GEMV_MAX_LDS && env_int("HM_FORCE_GEMM", 0) == 0) {
         p.kind = 0;
-        p.mr = rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : 8;
-        const int ncg = g.N_pad / 64;
-        const int KG = g.K_pad / 64;
-        const int max_kg = GEMV_LDS_BYTES / (64 * p.mr);
-        const int target_blocks = env_int("HM_GEMV_BLOCKS", 2048);
-        int ks = std::max((KG + max_kg - 1) / max_kg, std::min((target_blocks + ncg - 1) / ncg, std::max(1, KG / 2)));
-        ks = std::min(ks, KG);
-        p.kg_per_split = (KG + ks - 1) / ks;
-        p.ksplit = (KG + p.kg_per_split - 1) / p.kg_per_split;
-        p.grid = ncg * p.ksplit;
+        p.mr = mr;
+        p.ksplit = 1;
+        p.grid = g.N_pad / 8;  // one 8-column tile per block (SwiGLU: a tile pair)
         p.bm = p.mr;
-        p.bn = 64;
+        p.bn = 8;
         return p;
     }
     p.kind = 1;
@@ -336,8 +360,8 @@ Plan plan_linear(int rows, const Geometry& g) {
 
 // --- enqueue ------------------------------------------------------------------
 
-int enqueue_quant(Workspace* ws, const void* x, int x_type, long lda, int rows, int rule,
-                  const unsigned* rowmax_in, unsigned* rowmax_clear, hipStream_t s, const int* rows_dev) {
+int enqueue_quant(Workspace* ws, const void* x, int x_type, long lda, int rows, int rule, RowMax in_max,
+                  unsigned* rowmax_clear, hipStream_t s, const int* rows_dev) {
     QuantParams P;
     P.x = x;
     P.x_type = x_type;
@@ -351,10 +375,12 @@ int enqueue_quant(Workspace* ws, const void* x, int x_type, long lda, int rows, 
     P.codes = ws->codes;
     P.rowscale = ws->rowscale;
     P.rowsum = ws->rowsum;
-    P.rowmax_in = rowmax_in;
+    P.part_in = in_max.p;
+    P.part_count = in_max.count;
     P.rowmax_clear = rowmax_clear;
     P.rows_dev = rows_dev;
     const dim3 grid((rows + 15) / 16), block(256);
+    const int slot = prof_begin(s, 2, 8, rule, rows, ws->g.K, 0, rule == QUANT_DENSE ? "quant_rows<dense>" : "quant_rows<moe>");
     if (x_type == DT_F32) {
         if (rule == QUANT_DENSE)
             hipLaunchKernelGGL((quant_rows_kernel<float, QUANT_DENSE>), grid, block, 0, s, P);
@@ -366,6 +392,7 @@ int enqueue_quant(Workspace* ws, const void* x, int x_type, long lda, int rows, 
         else
             hipLaunchKernelGGL((quant_rows_kernel<__half, QUANT_MOE>), grid, block, 0, s, P);
     }
+    prof_end(slot, s);
     return hipGetLastError() == hipSuccess ? RK_NPU_OK : RK_NPU_ERR_DEVICE;
 }
 
@@ -390,63 +417,108 @@ static void launch_gemm(int v, const GemmParams& G, int grid, hipStream_t s) {
     }
 }
 
-template <int BITS, int EPI>
-static void launch_gemv(int mr, const GemvParams& V, int grid, hipStream_t s) {
+// Resident blocks of a GEMV instantiation on this device (persistent grid).
+template <typename T, int MR, int BITS, int EPI>
+static int gemv_capacity(size_t lds) {
+    static std::mutex mu;
+    static std::map<size_t, int> cache;
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = cache.find(lds);
+    if (it != cache.end()) return it->second;
+    int per_cu = 0, dev = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gemv_kernel<T, MR, BITS, EPI>, 256, lds) != hipSuccess ||
+        per_cu < 1)
+        per_cu = 1;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+        cus = 256;
+    const int cap = per_cu * cus * std::max(1, env_int("HM_GEMV_WAVES_PER_SLOT", 1));
+    cache[lds] = cap;
+    return cap;
+}
+
+template <typename T, int MR, int BITS, int EPI>
+static void launch_gemv_mr(const GemvParams& V, int groups, size_t lds, hipStream_t s) {
+    const int grid = std::min(groups, gemv_capacity<T, MR, BITS, EPI>(lds));
+    hipLaunchKernelGGL((gemv_kernel<T, MR, BITS, EPI>), dim3(grid), dim3(256), lds, s, V);
+}
+
+template <typename T, int BITS, int EPI>
+static void launch_gemv(int mr, const GemvParams& V, int grid, size_t lds, hipStream_t s) {
     switch (mr) {
         case 1:
-            hipLaunchKernelGGL((gemv_kernel<1, BITS, EPI>), dim3(grid), dim3(256), 0, s, V);
+            launch_gemv_mr<T, 1, BITS, EPI>(V, grid, lds, s);
             break;
         case 2:
-            hipLaunchKernelGGL((gemv_kernel<2, BITS, EPI>), dim3(grid), dim3(256), 0, s, V);
+            launch_gemv_mr<T, 2, BITS, EPI>(V, grid, lds, s);
             break;
         case 4:
-            hipLaunchKernelGGL((gemv_kernel<4, BITS, EPI>), dim3(grid), dim3(256), 0, s, V);
+            launch_gemv_mr<T, 4, BITS, EPI>(V, grid, lds, s);
             break;
         default:
-            hipLaunchKernelGGL((gemv_kernel<8, BITS, EPI>), dim3(grid), dim3(256), 0, s, V);
+            launch_gemv_mr<T, 8, BITS, EPI>(V, grid, lds, s);
             break;
     }
 }
 
-int enqueue_linear(Workspace* ws, const Weights* w, void* c, int c_type, long ldc, int rows, int epi,
-                   unsigned* rowmax, hipStream_t s) {
+template <typename T, int BITS>
+static void launch_gemv_epi(int epi, int mr, const GemvParams& V, int grid, size_t lds, hipStream_t s) {
+    if (epi == EPI_PLAIN)
+        launch_gemv<T, BITS, EPI_PLAIN>(mr, V, grid, lds, s);
+    else
+        launch_gemv<T, BITS, EPI_SWIGLU_MAX>(mr, V, grid, lds, s);
+}
+
+int enqueue_linear(Workspace* ws, const Weights* w, const void* x, int x_type, long lda, int rows, int rule,
+                   RowMax in_max, void* c, int c_type, long ldc, int epi, RowMax* out_max, hipStream_t s) {
     const Geometry& g = w->g;
     const Plan p = plan_linear(rows, g);
     if (p.kind == 0) {
         GemvParams V;
-        V.a = ws->codes;
+        V.x = x;
+        V.lda = lda;
+        V.rule = rule;
+        const size_t esz = x_type == DT_F32 ? 4 : 2;
+        V.vec = (g.K % 16 == 0) && ((lda * esz) % 16 == 0) && ((reinterpret_cast<uintptr_t>(x) & 15) == 0);
+        V.part_in = in_max.p;
+        V.part_count = in_max.count;
+        V.part_out = ws->partmax;
         V.b = w->packed;
-        V.rowscale = ws->rowscale;
-        V.rowsum = ws->rowsum;
         V.colscale = w->colscale;
         V.c = c;
         V.ldc = ldc;
         V.c_type = c_type;
         V.M = rows;
+        V.K = g.K;
         V.N = g.N;
         V.K_pad = g.K_pad;
-        V.M_alloc = ws->M_alloc;
         V.N_pad = g.N_pad;
         V.half = g.half;
-        V.rowmax = rowmax;
-        V.ksplit = p.ksplit;
-        V.kg_per_split = p.kg_per_split;
-        V.acc = ws->gemv_acc;
-        V.counters = ws->gemv_counters;
-#define HM_GEMV(B)                                                              \
-    if (epi == EPI_PLAIN)                                                       \
-        launch_gemv<B, EPI_PLAIN>(p.mr, V, p.grid, s);                          \
-    else if (epi == EPI_SWIGLU)                                                 \
-        launch_gemv<B, EPI_SWIGLU>(p.mr, V, p.grid, s);                         \
-    else                                                                        \
-        launch_gemv<B, EPI_SWIGLU_MAX>(p.mr, V, p.grid, s);
-        if (g.bits == 8) {
-            HM_GEMV(8)
+        V.diag_codes = ws->codes;
+        V.diag_scale = ws->rowscale;
+        V.diag_rowsum = ws->rowsum;
+        V.M_alloc = ws->M_alloc;
+        const int grid = epi == EPI_PLAIN ? g.N_pad / 8 : g.N_pad / 16;
+        const size_t lds = (size_t)g.K_pad * p.mr;
+        char name[64];
+        std::snprintf(name, sizeof(name), "gemv<mr=%d,w%d,epi=%d>", p.mr, g.bits, epi);
+        const int slot = prof_begin(s, 0, g.bits, epi, rows, g.K, g.N, name);
+        if (x_type == DT_F32) {
+            if (g.bits == 8)
+                launch_gemv_epi<float, 8>(epi, p.mr, V, grid, lds, s);
+            else
+                launch_gemv_epi<float, 4>(epi, p.mr, V, grid, lds, s);
         } else {
-            HM_GEMV(4)
+            if (g.bits == 8)
+                launch_gemv_epi<__half, 8>(epi, p.mr, V, grid, lds, s);
+            else
+                launch_gemv_epi<__half, 4>(epi, p.mr, V, grid, lds, s);
         }
-#undef HM_GEMV
+        prof_end(slot, s);
+        if (out_max) *out_max = RowMax{ws->partmax, grid};
     } else {
+        int rc = enqueue_quant(ws, x, x_type, lda, rows, rule, in_max, epi != EPI_PLAIN ? ws->rowmax : nullptr, s);
+        if (rc != RK_NPU_OK) return rc;
         GemmParams G;
         G.a = ws->codes;
         G.b = w->packed;
@@ -462,14 +534,15 @@ int enqueue_linear(Workspace* ws, const Weights* w, void* c, int c_type, long ld
         G.M_alloc = ws->M_alloc;
         G.N_pad = g.N_pad;
         G.half = g.half;
-        G.rowmax = rowmax;
+        G.rowmax = ws->rowmax;
         G.tiles_m = (rows + p.bm - 1) / p.bm;
         G.tiles_n = g.N_pad / p.bn;
+        char name[64];
+        std::snprintf(name, sizeof(name), "gemm<%dx%d,w%d,epi=%d>", p.bm, p.bn, g.bits, epi);
+        const int slot = prof_begin(s, 1, g.bits, epi, rows, g.K, g.N, name);
 #define HM_GEMM(B)                                                   \
     if (epi == EPI_PLAIN)                                            \
         launch_gemm<B, EPI_PLAIN>(p.variant, G, p.grid, s);          \
-    else if (epi == EPI_SWIGLU)                                      \
-        launch_gemm<B, EPI_SWIGLU>(p.variant, G, p.grid, s);         \
     else                                                             \
         launch_gemm<B, EPI_SWIGLU_MAX>(p.variant, G, p.grid, s);
         if (g.bits == 8) {
@@ -478,8 +551,22 @@ int enqueue_linear(Workspace* ws, const Weights* w, void* c, int c_type, long ld
             HM_GEMM(4)
         }
 #undef HM_GEMM
+        prof_end(slot, s);
+        if (out_max) *out_max = RowMax{reinterpret_cast<const float*>(ws->rowmax), 1};
     }
     return hipGetLastError() == hipSuccess ? RK_NPU_OK : RK_NPU_ERR_DEVICE;
+}
+
+int enqueue_ffn(Workspace* gws, const Weights* gw, Workspace* dws, const Weights* dw, const void* A, int a_type,
+                void* C, int c_type, int rows, int rule, hipStream_t s) {
+    const int F = gw->g.N / 2;
+    RowMax mid_max{nullptr, 0};
+    int rc = enqueue_linear(gws, gw, A, a_type, gw->g.K, rows, rule, RowMax{nullptr, 0}, gws->c_f32, DT_F32, F,
+                            EPI_SWIGLU_MAX, &mid_max, s);
+    if (rc == RK_NPU_OK)
+        rc = enqueue_linear(dws, dw, gws->c_f32, DT_F32, F, rows, rule, mid_max, C, c_type, dw->g.N, EPI_PLAIN,
+                            nullptr, s);
+    return rc;
 }
 
 }  // namespace hm
@@ -683,8 +770,8 @@ static int run_host(Workspace* ws, const Weights* w, const float* A, float* C, i
     if (hipMemcpyAsync(ws->a_f32, A, (size_t)M * K * 4, hipMemcpyHostToDevice, ws->stream) != hipSuccess)
         return RK_NPU_ERR_DEVICE;
     const double t1 = now_us();
-    int rc = enqueue_quant(ws, ws->a_f32, DT_F32, K, M, QUANT_DENSE, nullptr, nullptr, ws->stream);
-    if (rc == RK_NPU_OK) rc = enqueue_linear(ws, w, ws->c_f32, DT_F32, width, M, epi, nullptr, ws->stream);
+    int rc = enqueue_linear(ws, w, ws->a_f32, DT_F32, K, M, QUANT_DENSE, RowMax{nullptr, 0}, ws->c_f32, DT_F32,
+                            width, epi, nullptr, ws->stream);
     if (rc != RK_NPU_OK) {
         (void)hipStreamSynchronize(ws->stream);
         return rc;
@@ -788,18 +875,9 @@ int rk_npu_w4a8_run_f32(rk_npu_w4a8_workspace* workspace, const rk_npu_w4a8_weig
 
 int rk_npu_w4a8_run_swiglu_f32(rk_npu_w4a8_workspace* workspace, const rk_npu_w4a8_weights* weights,
                                const float* A, float* C, rk_npu_w4a8_timings* timings) {
-    return run_host(as_ws(workspace, 4), as_w(weights, 4), A, C, EPI_SWIGLU, timings);
-}
-
-// Fused FFN enqueue shared by the host and device entry points.
-static int enqueue_ffn(Workspace* gws, const Weights* gw, Workspace* dws, const Weights* dw, const void* A,
-                       int a_type, void* C, int c_type, int rows, hipStream_t s) {
-    const int F = gw->g.N / 2;
-    int rc = enqueue_quant(gws, A, a_type, gw->g.K, rows, QUANT_DENSE, nullptr, gws->rowmax, s);
-    if (rc == RK_NPU_OK) rc = enqueue_linear(gws, gw, gws->c_f32, DT_F32, F, rows, EPI_SWIGLU_MAX, gws->rowmax, s);
-    if (rc == RK_NPU_OK) rc = enqueue_quant(dws, gws->c_f32, DT_F32, F, rows, QUANT_DENSE, gws->rowmax, nullptr, s);
-    if (rc == RK_NPU_OK) rc = enqueue_linear(dws, dw, C, c_type, dw->g.N, rows, EPI_PLAIN, nullptr, s);
-    return rc;
+    // The SwiGLU+max epilogue also records the middle's row maxima in the
+    // workspace; the outputs are identical to the plain SwiGLU epilogue.
+    return run_host(as_ws(workspace, 4), as_w(weights, 4), A, C, EPI_SWIGLU_MAX, timings);
 }
 
 static int check_ffn(Workspace* gws, const Weights* gw, Workspace* dws, const Weights* dw, int rows) {
@@ -833,7 +911,7 @@ int rk_npu_w4a8_run_ffn_f32(rk_npu_w4a8_workspace* gate_up_workspace, const rk_n
     if (hipMemcpyAsync(gws->a_f32, A, (size_t)M * H * 4, hipMemcpyHostToDevice, s) != hipSuccess)
         return RK_NPU_ERR_DEVICE;
     const double t1 = now_us();
-    rc = enqueue_ffn(gws, gw, dws, dw, gws->a_f32, DT_F32, dws->c_f32, DT_F32, M, s);
+    rc = enqueue_ffn(gws, gw, dws, dw, gws->a_f32, DT_F32, dws->c_f32, DT_F32, M, QUANT_DENSE, s);
     if (rc != RK_NPU_OK) {
         (void)hipStreamSynchronize(s);
         return rc;
@@ -931,16 +1009,15 @@ int rk_npu_hip_linear_run(void* workspace, const void* weights, int bits, const 
     if ((a_type != DT_F32 && a_type != DT_F16) || (c_type != DT_F32 && c_type != DT_F16)) return RK_NPU_ERR_PARAM;
     if (ws->g.K != w->g.K || ws->g.N != w->g.N || rows < 1 || rows > ws->M) return RK_NPU_ERR_PARAM;
     if (epilogue != RK_NPU_HIP_PLAIN && epilogue != RK_NPU_HIP_SWIGLU) return RK_NPU_ERR_PARAM;
-    const int epi = epilogue == RK_NPU_HIP_SWIGLU ? EPI_SWIGLU : EPI_PLAIN;
+    const int epi = epilogue == RK_NPU_HIP_SWIGLU ? EPI_SWIGLU_MAX : EPI_PLAIN;
     if (epi != EPI_PLAIN && !w->g.half) return RK_NPU_ERR_PARAM;
     BusyGuard guard(ws->busy);
     if (!guard.ok) return RK_NPU_ERR_BUSY;
     if (hipSetDevice(device_of(ws->domain)) != hipSuccess) return RK_NPU_ERR_DEVICE;
     hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ws->stream;
     const int width = epi == EPI_PLAIN ? w->g.N : w->g.N / 2;
-    int rc = enqueue_quant(ws, A, a_type, w->g.K, rows, QUANT_DENSE, nullptr, nullptr, s);
-    if (rc == RK_NPU_OK) rc = enqueue_linear(ws, w, C, c_type, width, rows, epi, nullptr, s);
-    return rc;
+    return enqueue_linear(ws, w, A, a_type, w->g.K, rows, QUANT_DENSE, RowMax{nullptr, 0}, C, c_type, width, epi,
+                          nullptr, s);
 }
 
 int rk_npu_hip_ffn_run(void* gate_up_workspace, const void* gate_up, int gu_bits, void* down_workspace,
@@ -960,7 +1037,7 @@ int rk_npu_hip_ffn_run(void* gate_up_workspace, const void* gate_up, int gu_bits
     if (!g2.ok) return RK_NPU_ERR_BUSY;
     if (hipSetDevice(device_of(gws->domain)) != hipSuccess) return RK_NPU_ERR_DEVICE;
     hipStream_t s = stream ? static_cast<hipStream_t>(stream) : gws->stream;
-    return enqueue_ffn(gws, gw, dws, dw, A, a_type, C, c_type, rows, s);
+    return enqueue_ffn(gws, gw, dws, dw, A, a_type, C, c_type, rows, QUANT_DENSE, s);
 }
 
 rk_npu_f32i8f32_weights* rk_npu_hip_f32i8f32_weights_create_device(rk_npu_iommu_domain* domain,
@@ -1003,6 +1080,61 @@ int rk_npu_hip_workspace_codes(void* workspace, int bits, int rows, int8_t* code
         return RK_NPU_ERR_DEVICE;
     if (rowsums && hipMemcpy(rowsums, ws->rowsum, (size_t)rows * 4, hipMemcpyDeviceToHost) != hipSuccess)
         return RK_NPU_ERR_DEVICE;
+    return RK_NPU_OK;
+}
+
+int rk_npu_hip_profile_begin(int max_launches) {
+    if (max_launches < 1 || max_launches > (1 << 20)) return RK_NPU_ERR_PARAM;
+    std::lock_guard<std::mutex> lock(g_prof_mu);
+    for (hipEvent_t e : g_prof_events) (void)hipEventDestroy(e);
+    g_prof_events.assign(2 * (size_t)max_launches, nullptr);
+    for (hipEvent_t& e : g_prof_events)
+        if (hipEventCreate(&e) != hipSuccess) {
+            g_prof_events.clear();
+            return RK_NPU_ERR_DEVICE;
+        }
+    g_prof_records.clear();
+    g_prof_on.store(true);
+    return RK_NPU_OK;
+}
+
+int rk_npu_hip_profile_end(void) {
+    g_prof_on.store(false);
+    return RK_NPU_OK;
+}
+
+int rk_npu_hip_profile_read(rk_npu_hip_kernel_stat* stats, int capacity, int* count) {
+    if (!count || (capacity > 0 && !stats)) return RK_NPU_ERR_PARAM;
+    std::lock_guard<std::mutex> lock(g_prof_mu);
+    if (hipDeviceSynchronize() != hipSuccess) return RK_NPU_ERR_DEVICE;
+    std::map<std::tuple<int, int, int, int, int, int>, rk_npu_hip_kernel_stat> agg;
+    for (size_t i = 0; i < g_prof_records.size(); ++i) {
+        const ProfRecord& r = g_prof_records[i];
+        float ms = 0.0f;
+        if (hipEventElapsedTime(&ms, g_prof_events[2 * i], g_prof_events[2 * i + 1]) != hipSuccess)
+            return RK_NPU_ERR_DEVICE;
+        auto key = std::make_tuple(r.kind, r.bits, r.epi, r.rows, r.K, r.N);
+        auto it = agg.find(key);
+        if (it == agg.end()) {
+            rk_npu_hip_kernel_stat st{};
+            st.kind = r.kind;
+            st.bits = r.bits;
+            st.epilogue = r.epi;
+            st.rows = r.rows;
+            st.K = r.K;
+            st.N = r.N;
+            std::snprintf(st.name, sizeof(st.name), "%s", r.name.c_str());
+            it = agg.emplace(key, st).first;
+        }
+        it->second.launches += 1;
+        it->second.total_ms += ms;
+    }
+    int n = 0;
+    for (auto& kv : agg) {
+        if (n < capacity) stats[n] = kv.second;
+        ++n;
+    }
+    *count = n;
     return RK_NPU_OK;
 }
 

@@ -3,12 +3,16 @@
 // Device data layouts (all chosen so every global access is a coalesced
 // 16-byte-per-lane load and every LDS fragment read is conflict free):
 //   activation codes  A8 : [K_pad/16][M_alloc][16]  int8   ("k16 planes")
-//   W8 weights           : [K_pad/16][N_pad][16]    int8
-//   W4 weights           : [K_pad/32][N_pad][16]    bytes, two offset-binary
-//                          nibbles (u = code + 8) per byte. Entry j of column
-//                          p holds, with g = j/2 and h = j%2, the codes
-//                          k = 64g + 16h + b in the low nibble of byte b and
-//                          k = 64g + 32 + 16h + b in the high nibble.
+//   weights              : 8-column tiles, [N_pad/8][planes][8][16] bytes,
+//                          so one tile's whole K is one contiguous stream
+//                          (decode) and a K step of a tile is a 512-byte
+//                          (W8) or 256-byte (W4) contiguous run (prefill).
+//   W8 plane             : 16 k of one column (planes = K_pad/16)
+//   W4 plane j           : two offset-binary nibbles (u = code + 8) per byte;
+//                          with g = j/2 and h = j%2 byte b holds
+//                          k = 64g + 16h + b in the low nibble and
+//                          k = 64g + 32 + 16h + b in the high nibble
+//                          (planes = K_pad/32).
 //   column order         : when N % 64 == 0 the packed column p maps to the
 //                          original column orig_col(p): 32 gate columns then
 //                          the 32 matching up columns (N/2 + ...), so a
@@ -111,7 +115,8 @@ struct QuantParams {
     int8_t* codes;
     float* rowscale;
     int* rowsum;
-    const unsigned* rowmax_in;
+    const float* part_in;    // optional precomputed row maxima: max over part_in[r*part_count + i]
+    int part_count;
     unsigned* rowmax_clear;  // zeroed for the block's rows (next middle's max)
     const int* rows_dev;     // optional device-side row count (<= rows)
 };
@@ -152,8 +157,10 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantParams P) {
         const int lr = wave * 4 + i, r = r0 + lr;
         float m = 0.0f;
         if (r < rows) {
-            if (P.rowmax_in) {
-                m = __uint_as_float(P.rowmax_in[r]);
+            if (P.part_in) {
+                const float* pr = P.part_in + (size_t)r * P.part_count;
+                for (int i = lane; i < P.part_count; i += 64) m = fmaxf(m, pr[i]);
+                m = wave_max(m);
             } else {
                 const T* xr = x + (size_t)r * P.lda;
                 for (int k = lane; k < P.K; k += 64) m = fmaxf(m, fabsf(to_f32(xr[k])));
@@ -225,27 +232,33 @@ struct PackParams {
     unsigned* bad;  // set when a W4 code lies outside [-8, 7]
 };
 
+// Thread i handles plane pl of packed column p (consecutive threads walk
+// consecutive columns of one plane, so the [K][N] reads are contiguous) and
+// stores that 16-byte entry at its tile position.
 static __global__ __launch_bounds__(256) void pack_w8_kernel(PackParams P) {
     const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
-    const size_t total = (size_t)(P.K_pad / 16) * P.N_pad;
+    const int planes = P.K_pad / 16;
+    const size_t total = (size_t)planes * P.N_pad;
     if (idx >= total) return;
-    const int p = (int)(idx % P.N_pad), kg = (int)(idx / P.N_pad);
+    const int p = (int)(idx % P.N_pad), pl = (int)(idx / P.N_pad);
     const int n = p < P.N ? orig_col(p, P.half) : -1;
     unsigned w[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
     for (int b = 0; b < 16; ++b) {
-        const int k = kg * 16 + b;
+        const int k = pl * 16 + b;
         unsigned v = (n >= 0 && k < P.K) ? (unsigned)(uint8_t)P.codes[(size_t)k * P.N + n] : 0u;
         w[b >> 2] |= v << ((b & 3) * 8);
     }
     v4u out = {w[0], w[1], w[2], w[3]};
-    *reinterpret_cast<v4u*>(P.out + idx * 16) = out;
-    if (kg == 0) P.colscale[p] = n >= 0 ? P.scales[n] : 0.0f;
+    const size_t dst = (((size_t)(p >> 3) * planes + pl) * 8 + (p & 7)) * 16;
+    *reinterpret_cast<v4u*>(P.out + dst) = out;
+    if (pl == 0) P.colscale[p] = n >= 0 ? P.scales[n] : 0.0f;
 }
 
 static __global__ __launch_bounds__(256) void pack_w4_kernel(PackParams P) {
     const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
-    const size_t total = (size_t)(P.K_pad / 32) * P.N_pad;
+    const int planes = P.K_pad / 32;
+    const size_t total = (size_t)planes * P.N_pad;
     if (idx >= total) return;
     const int p = (int)(idx % P.N_pad), j = (int)(idx / P.N_pad);
     const int n = p < P.N ? orig_col(p, P.half) : -1;
@@ -262,7 +275,8 @@ static __global__ __launch_bounds__(256) void pack_w4_kernel(PackParams P) {
         w[b >> 2] |= byte << ((b & 3) * 8);
     }
     v4u out = {w[0], w[1], w[2], w[3]};
-    *reinterpret_cast<v4u*>(P.out + idx * 16) = out;
+    const size_t dst = (((size_t)(p >> 3) * planes + j) * 8 + (p & 7)) * 16;
+    *reinterpret_cast<v4u*>(P.out + dst) = out;
     if (j == 0) P.colscale[p] = n >= 0 ? P.scales[n] : 0.0f;
     if (bad) atomicOr(P.bad, 1u);
 }
@@ -311,7 +325,7 @@ struct TileCfg {
 template <int BM, int BN, int WGM, int WGN, int BITS>
 __device__ __forceinline__ void gemm_mainloop(uint8_t* smem, const int8_t* __restrict__ ga, size_t a_plane,
                                               const size_t (&a_off)[TileCfg<BM, BN, WGM, WGN, BITS>::A_LOADS],
-                                              const uint8_t* __restrict__ gb, int N_pad, int n0, int KT,
+                                              const uint8_t* __restrict__ gb, int K_pad, int n0, int KT,
                                               v16i (&acc)[TileCfg<BM, BN, WGM, WGN, BITS>::FM]
                                                          [TileCfg<BM, BN, WGM, WGN, BITS>::FN]) {
     using C = TileCfg<BM, BN, WGM, WGN, BITS>;
@@ -321,18 +335,28 @@ __device__ __forceinline__ void gemm_mainloop(uint8_t* smem, const int8_t* __res
     const int wm = wave / WGN, wn = wave % WGN;
     const int half_id = lane >> 5, l32 = lane & 31;
 
+    // B stage: BN/8 column tiles x PPS planes x 8 columns. Chunk c -> tile
+    // c/(8*PPS), plane (c/8)%PPS, column c%8: every 8*PPS lanes read one
+    // contiguous run of a tile; LDS keeps the [plane][BN][16] fragment order.
+    constexpr int PPS = (BITS == 8) ? 4 : 2;
+    const int planes = (BITS == 8) ? K_pad / 16 : K_pad / 32;
+    size_t b_src[B_LOADS];
+    int b_dst[B_LOADS];
+#pragma unroll
+    for (int i = 0; i < B_LOADS; ++i) {
+        const int c = tid + i * NT;
+        const int t = c / (8 * PPS), pl = (c / 8) % PPS, c8 = c % 8;
+        b_src[i] = (((size_t)(n0 / 8 + t) * planes + pl) * 8 + c8) * 16;
+        b_dst[i] = (pl * BN + t * 8 + c8) * 16;
+    }
     v4i ra[A_LOADS], rb[B_LOADS];
     auto gload = [&](int kt) {
 #pragma unroll
         for (int i = 0; i < A_LOADS; ++i)
             ra[i] = *reinterpret_cast<const v4i*>(ga + ((size_t)kt * 4 * a_plane + a_off[i]) * 16);
 #pragma unroll
-        for (int i = 0; i < B_LOADS; ++i) {
-            const int c = tid + i * NT;
-            const int kg = c / BN, col = c % BN;
-            const int plane = (BITS == 8) ? kt * 4 + kg : kt * 2 + kg;
-            rb[i] = *reinterpret_cast<const v4i*>(gb + ((size_t)plane * N_pad + n0 + col) * 16);
-        }
+        for (int i = 0; i < B_LOADS; ++i)
+            rb[i] = *reinterpret_cast<const v4i*>(gb + b_src[i] + (size_t)kt * (PPS * 128));
     };
     auto sstore = [&](int buf) {
         uint8_t* sa = smem + buf * STAGE;
@@ -340,7 +364,7 @@ __device__ __forceinline__ void gemm_mainloop(uint8_t* smem, const int8_t* __res
 #pragma unroll
         for (int i = 0; i < A_LOADS; ++i) *reinterpret_cast<v4i*>(sa + (tid + i * NT) * 16) = ra[i];
 #pragma unroll
-        for (int i = 0; i < B_LOADS; ++i) *reinterpret_cast<v4i*>(sb + (tid + i * NT) * 16) = rb[i];
+        for (int i = 0; i < B_LOADS; ++i) *reinterpret_cast<v4i*>(sb + b_dst[i]) = rb[i];
     };
 
     gload(0);
@@ -478,7 +502,7 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_kernel(GemmParams P) {
         for (int j = 0; j < C::FN; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
-    gemm_mainloop<BM, BN, WGM, WGN, BITS>(smem, P.a, (size_t)P.M_alloc, a_off, P.b, P.N_pad, n0, P.K_pad >> 6, acc);
+    gemm_mainloop<BM, BN, WGM, WGN, BITS>(smem, P.a, (size_t)P.M_alloc, a_off, P.b, P.K_pad, n0, P.K_pad >> 6, acc);
     const int M = P.M;
     gemm_epilogue<BM, BN, WGM, WGN, BITS, EPI>(acc, n0, P.rowscale, P.rowsum, P.colscale, P.N, P.half, P.c, P.ldc,
                                                P.c_type, P.rowmax, [&](int local, int& out_row, int& src_row) {
@@ -490,180 +514,341 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_kernel(GemmParams P) {
 }
 
 // ---------------------------------------------------------------------------
-// Decode GEMV / skinny GEMM (M <= 8) without MFMA: bandwidth bound.
-// Block = 4 waves over 64 packed columns and one K split; lane = column, so a
-// wave's weight load is 64 x 16 contiguous bytes. The block's activation codes
-// sit in LDS and are read as broadcasts. Dot products use v_dot4_i32_i8.
-// With several K splits the int32 partials are added atomically into a
-// per-workspace buffer; the last block of a column group (arrival counter)
-// finishes the epilogue and resets buffer and counter for the next call.
+// Decode GEMV / skinny GEMM (M <= 8) without MFMA: bandwidth bound, one launch.
+// A block owns one 8-column weight tile (two for SwiGLU: a gate tile and its
+// up tile) for the whole K, so no reduction crosses blocks. Its 4 waves split
+// the tile's planes; within a wave, lane (s, c8) = (lane/8, lane%8) reads
+// plane p0 + s + 8i of column c8, so each wave load is 1 KB contiguous.
+// The block first issues its first weight loads, then quantizes the
+// activation rows itself (row max from x or from precomputed partial maxima,
+// the dense or MoE rule) into LDS while those loads are in flight. Dot
+// products use v_dot4_i32_i8; partials reduce over s with cross-lane shuffles
+// and over waves through LDS. SwiGLU+max writes one partial max per block.
 // ---------------------------------------------------------------------------
 struct GemvParams {
-    const int8_t* a;
+    const void* x;
+    long lda;
+    int rule;             // QUANT_DENSE or QUANT_MOE
+    int vec;              // rows are 16-element aligned and K % 16 == 0
+    const float* part_in; // optional row maxima as partials [row][part_count]
+    int part_count;
+    float* part_out;      // SwiGLU+max: per-block max |out|, [row][gridDim.x]
     const uint8_t* b;
-    const float* rowscale;
-    const int* rowsum;
     const float* colscale;
     void* c;
     long ldc;
     int c_type;
-    int M, N, K_pad, M_alloc, N_pad, half;
-    unsigned* rowmax;
-    int ksplit, kg_per_split;  // kg = 64-k groups
-    int* acc;                  // [8][N_pad] int32, zero between calls
-    unsigned* counters;        // [N_pad/64], zero between calls
+    int M, K, N, K_pad, N_pad, half;
+    int8_t* diag_codes;   // block 0 leaves the quantized rows here ([K_pad/16][M_alloc][16])
+    float* diag_scale;
+    int* diag_rowsum;
+    int M_alloc;
 };
 
-constexpr int GEMV_LDS_BYTES = 16384;
+__device__ __forceinline__ int wave_sum(int v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    return v;
+}
 
-template <int MR, int BITS, int EPI>
+template <typename T, int MR, int BITS, int EPI>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
-    __shared__ __attribute__((aligned(16))) int8_t sa[GEMV_LDS_BYTES];
-    __shared__ int red[4][MR][64];
-    __shared__ int s_last;
+    extern __shared__ __attribute__((aligned(16))) int8_t sa[];  // [K_pad/16][MR][16]
+    constexpr int TPB = (EPI == EPI_PLAIN) ? 1 : 2;
+    constexpr int WMAX = (TPB == 1) ? 12 : 6;  // weight planes per lane held in registers
+    constexpr int XMAX = 3;                    // 16-element activation chunks per thread in registers
+    __shared__ float s_red[4][MR];
+    __shared__ int s_isum[4][MR];
+    __shared__ int red[2][4][TPB][MR][8];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int ncg = P.N_pad >> 6;
-    const int cg = blockIdx.x % ncg, split = blockIdx.x / ncg;
-    const int n0 = cg * 64, p = n0 + lane;
-    const int KG = P.K_pad >> 6;
-    const int kg_begin = split * P.kg_per_split;
-    const int kg_end = min(KG, kg_begin + P.kg_per_split);
+    const int c8 = lane & 7, s = lane >> 3;
+    const int KG16 = P.K_pad >> 4;
+    const int PL = (BITS == 8) ? KG16 : (P.K_pad >> 5);
+    const int PW = (((PL + 3) >> 2) + 7) & ~7;
+    const int p_begin = wave * PW, p_end = min(PL, p_begin + PW);
+    const int groups = (TPB == 1) ? (P.N_pad >> 3) : (P.N_pad >> 4);
 
-    // Activation codes of this K split, [kg16 - 4*kg_begin][MR][16].
-    const int chunks = (kg_end - kg_begin) * 4 * MR;
-    for (int c = tid; c < chunks; c += 256) {
-        const int kgl = c / MR, m = c % MR;
-        *reinterpret_cast<v4i*>(sa + c * 16) =
-            *reinterpret_cast<const v4i*>(P.a + ((size_t)(4 * kg_begin + kgl) * P.M_alloc + m) * 16);
+    // Tile group g: one 8-column tile, or (SwiGLU) a gate tile and its up tile.
+    auto tiles_of = [&](int g, int (&tile)[TPB]) {
+        if (TPB == 1) {
+            tile[0] = g;
+        } else {
+            tile[0] = 8 * (g >> 2) + (g & 3);
+            tile[TPB - 1] = tile[0] + 4;
+        }
+    };
+    auto load_group = [&](int g, v4u (&w)[WMAX][TPB], float (&cs)[TPB]) {
+        int tile[TPB];
+        tiles_of(g, tile);
+#pragma unroll
+        for (int t = 0; t < TPB; ++t) {
+            const uint8_t* base = P.b + ((size_t)tile[t] * PL * 8 + c8) * 16;
+#pragma unroll
+            for (int u = 0; u < WMAX; ++u) {
+                const int pl = p_begin + s + 8 * u;
+                w[u][t] = pl < p_end ? *reinterpret_cast<const v4u*>(base + (size_t)pl * 128) : v4u{0u, 0u, 0u, 0u};
+            }
+            cs[t] = P.colscale[8 * tile[t] + c8];
+        }
+    };
+
+    // 1. First group's weights and column scales, this thread's activation
+    // chunks and the row maxima are all requested before anything waits.
+    int g = blockIdx.x;
+    v4u wcur[WMAX][TPB];
+    float cscur[TPB];
+    load_group(g, wcur, cscur);
+    const T* x = static_cast<const T*>(P.x);
+    const int chunks = KG16 * MR;
+    const bool x_in_regs = chunks <= 256 * XMAX;
+    float xv[XMAX][16];
+    float mx[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) mx[m] = 0.0f;
+    auto load_chunk = [&](int c, float (&v)[16]) {
+        const int kg = c / MR, m = c % MR;
+        if (m < P.M) {
+            const T* xr = x + (size_t)m * P.lda + kg * 16;
+            if (P.vec && kg * 16 + 16 <= P.K) {
+                load16(xr, v);
+            } else {
+#pragma unroll
+                for (int b = 0; b < 16; ++b) v[b] = (kg * 16 + b < P.K) ? to_f32(xr[b]) : 0.0f;
+            }
+        } else {
+#pragma unroll
+            for (int b = 0; b < 16; ++b) v[b] = 0.0f;
+        }
+    };
+    if (x_in_regs) {
+#pragma unroll
+        for (int j = 0; j < XMAX; ++j) {
+            const int c = tid + 256 * j;
+            if (c < chunks) {
+                load_chunk(c, xv[j]);
+                if (!P.part_in) {
+                    const int m = c % MR;
+                    float lm = 0.0f;
+#pragma unroll
+                    for (int b = 0; b < 16; ++b) lm = fmaxf(lm, fabsf(xv[j][b]));
+#pragma unroll
+                    for (int r = 0; r < MR; ++r) mx[r] = (r == m) ? fmaxf(mx[r], lm) : mx[r];
+                }
+            }
+        }
+    } else if (!P.part_in) {
+#pragma unroll
+        for (int m = 0; m < MR; ++m)
+            if (m < P.M) {
+                const T* xr = x + (size_t)m * P.lda;
+                for (int k = tid; k < P.K; k += 256) mx[m] = fmaxf(mx[m], fabsf(to_f32(xr[k])));
+            }
+    }
+    if (P.part_in) {
+#pragma unroll
+        for (int m = 0; m < MR; ++m)
+            if (m < P.M)
+                for (int i = tid; i < P.part_count; i += 256) mx[m] = fmaxf(mx[m], P.part_in[(size_t)m * P.part_count + i]);
+    }
+
+    // 2. Row scales: block max through LDS (every wave reads all partials).
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+        const float v = wave_max(mx[m]);
+        if (lane == 0) s_red[wave][m] = v;
     }
     __syncthreads();
-
-    int acc[MR];
+    float scale[MR], inv[MR];
 #pragma unroll
-    for (int m = 0; m < MR; ++m) acc[m] = 0;
-    const uint8_t* __restrict__ gb = P.b;
+    for (int m = 0; m < MR; ++m) {
+        const float v = fmaxf(fmaxf(s_red[0][m], s_red[1][m]), fmaxf(s_red[2][m], s_red[3][m]));
+        if (P.rule == QUANT_DENSE)
+            scale[m] = (v == 0.0f) ? 1.0f : fmaxf(v / 127.0f, FLT_MIN);
+        else
+            scale[m] = (v == 0.0f) ? 1.0f : v / 127.0f;
+        inv[m] = 1.0f / scale[m];
+    }
 
-    if (BITS == 8) {
-        const int e_begin = 4 * kg_begin, e_end = 4 * kg_end;
-        auto consume = [&](const v4i w, int e) {
-            const int8_t* ab = sa + (e - e_begin) * MR * 16;
+    // 3. Quantize into LDS, chunk c = (k16 group, row); once per block.
+    int psum[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) psum[m] = 0;
+    auto quantize_chunk = [&](int c, const float (&v)[16]) {
+        const int m = c % MR;
+        float iv = inv[0];
+#pragma unroll
+        for (int r = 1; r < MR; ++r) iv = (r == m) ? inv[r] : iv;
+        unsigned packed[4] = {0u, 0u, 0u, 0u};
+        int sum = 0;
+#pragma unroll
+        for (int b = 0; b < 16; ++b) {
+            float q = v[b] * iv;
+            q = (P.rule == QUANT_DENSE) ? roundf(q) : __builtin_rintf(q);
+            q = fminf(fmaxf(q, -127.0f), 127.0f);
+            const int qi = (int)q;
+            sum += qi;
+            packed[b >> 2] |= ((unsigned)qi & 0xffu) << ((b & 3) * 8);
+        }
+#pragma unroll
+        for (int r = 0; r < MR; ++r) psum[r] += (r == m) ? sum : 0;
+        *reinterpret_cast<v4u*>(sa + c * 16) = v4u{packed[0], packed[1], packed[2], packed[3]};
+    };
+    if (x_in_regs) {
+#pragma unroll
+        for (int j = 0; j < XMAX; ++j) {
+            const int c = tid + 256 * j;
+            if (c < chunks) quantize_chunk(c, xv[j]);
+        }
+    } else {
+        for (int c = tid; c < chunks; c += 256) {
+            float v[16];
+            load_chunk(c, v);
+            quantize_chunk(c, v);
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+        const int v = wave_sum(psum[m]);
+        if (lane == 0) s_isum[wave][m] = v;
+    }
+    __syncthreads();
+    int corr[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+        corr[m] = (BITS == 4) ? 8 * (s_isum[0][m] + s_isum[1][m] + s_isum[2][m] + s_isum[3][m]) : 0;
+    if (blockIdx.x == 0 && P.diag_codes) {
+        for (int c = tid; c < chunks; c += 256)
+            *reinterpret_cast<v4u*>(P.diag_codes + ((size_t)(c / MR) * P.M_alloc + c % MR) * 16) =
+                *reinterpret_cast<const v4u*>(sa + c * 16);
+        if (tid < MR && tid < P.M) {
+            P.diag_scale[tid] = scale[tid];
+            P.diag_rowsum[tid] = s_isum[0][tid] + s_isum[1][tid] + s_isum[2][tid] + s_isum[3][tid];
+        }
+    }
+
+    // 4. Tile groups: while the dots of group g run, group g + gridDim.x is loading.
+    auto consume = [&](int (&acc)[TPB][MR], const v4u (&w)[TPB], int pl) {
+        if (BITS == 8) {
+            const int8_t* ab = sa + pl * MR * 16;
 #pragma unroll
             for (int m = 0; m < MR; ++m) {
                 const v4i a = *reinterpret_cast<const v4i*>(ab + m * 16);
-                int t = acc[m];
-                t = __builtin_amdgcn_sdot4(a.x, w.x, t, false);
-                t = __builtin_amdgcn_sdot4(a.y, w.y, t, false);
-                t = __builtin_amdgcn_sdot4(a.z, w.z, t, false);
-                t = __builtin_amdgcn_sdot4(a.w, w.w, t, false);
-                acc[m] = t;
+#pragma unroll
+                for (int t = 0; t < TPB; ++t) {
+                    int v = acc[t][m];
+                    v = __builtin_amdgcn_sdot4(a.x, (int)w[t].x, v, false);
+                    v = __builtin_amdgcn_sdot4(a.y, (int)w[t].y, v, false);
+                    v = __builtin_amdgcn_sdot4(a.z, (int)w[t].z, v, false);
+                    v = __builtin_amdgcn_sdot4(a.w, (int)w[t].w, v, false);
+                    acc[t][m] = v;
+                }
             }
-        };
-        int e = e_begin + wave;
-        for (; e + 12 < e_end; e += 16) {
-            const v4i w0 = *reinterpret_cast<const v4i*>(gb + ((size_t)e * P.N_pad + p) * 16);
-            const v4i w1 = *reinterpret_cast<const v4i*>(gb + ((size_t)(e + 4) * P.N_pad + p) * 16);
-            const v4i w2 = *reinterpret_cast<const v4i*>(gb + ((size_t)(e + 8) * P.N_pad + p) * 16);
-            const v4i w3 = *reinterpret_cast<const v4i*>(gb + ((size_t)(e + 12) * P.N_pad + p) * 16);
-            consume(w0, e);
-            consume(w1, e + 4);
-            consume(w2, e + 8);
-            consume(w3, e + 12);
-        }
-        for (; e < e_end; e += 4) consume(*reinterpret_cast<const v4i*>(gb + ((size_t)e * P.N_pad + p) * 16), e);
-    } else {
-        const int j_begin = 2 * kg_begin, j_end = 2 * kg_end;
-        auto consume = [&](const v4u w, int j) {
-            const v4i lo = __builtin_bit_cast(v4i, w & 0x0F0F0F0Fu);
-            const v4i hi = __builtin_bit_cast(v4i, (w >> 4) & 0x0F0F0F0Fu);
-            const int kga = 4 * ((j >> 1) - kg_begin) + (j & 1);
+        } else {
+            const int kga = 4 * (pl >> 1) + (pl & 1);
             const int8_t* aa = sa + kga * MR * 16;
             const int8_t* ab = sa + (kga + 2) * MR * 16;
+            v4u lo[TPB], hi[TPB];
+#pragma unroll
+            for (int t = 0; t < TPB; ++t) {
+                lo[t] = w[t] & 0x0F0F0F0Fu;
+                hi[t] = (w[t] >> 4) & 0x0F0F0F0Fu;
+            }
 #pragma unroll
             for (int m = 0; m < MR; ++m) {
                 const v4i x0 = *reinterpret_cast<const v4i*>(aa + m * 16);
                 const v4i x1 = *reinterpret_cast<const v4i*>(ab + m * 16);
-                int t = acc[m];
-                t = __builtin_amdgcn_sdot4(x0.x, lo.x, t, false);
-                t = __builtin_amdgcn_sdot4(x0.y, lo.y, t, false);
-                t = __builtin_amdgcn_sdot4(x0.z, lo.z, t, false);
-                t = __builtin_amdgcn_sdot4(x0.w, lo.w, t, false);
-                t = __builtin_amdgcn_sdot4(x1.x, hi.x, t, false);
-                t = __builtin_amdgcn_sdot4(x1.y, hi.y, t, false);
-                t = __builtin_amdgcn_sdot4(x1.z, hi.z, t, false);
-                t = __builtin_amdgcn_sdot4(x1.w, hi.w, t, false);
-                acc[m] = t;
+#pragma unroll
+                for (int t = 0; t < TPB; ++t) {
+                    int v = acc[t][m];
+                    v = __builtin_amdgcn_sdot4(x0.x, (int)lo[t].x, v, false);
+                    v = __builtin_amdgcn_sdot4(x0.y, (int)lo[t].y, v, false);
+                    v = __builtin_amdgcn_sdot4(x0.z, (int)lo[t].z, v, false);
+                    v = __builtin_amdgcn_sdot4(x0.w, (int)lo[t].w, v, false);
+                    v = __builtin_amdgcn_sdot4(x1.x, (int)hi[t].x, v, false);
+                    v = __builtin_amdgcn_sdot4(x1.y, (int)hi[t].y, v, false);
+                    v = __builtin_amdgcn_sdot4(x1.z, (int)hi[t].z, v, false);
+                    v = __builtin_amdgcn_sdot4(x1.w, (int)hi[t].w, v, false);
+                    acc[t][m] = v;
+                }
             }
-        };
-        int j = j_begin + wave;
-        for (; j + 12 < j_end; j += 16) {
-            const v4u w0 = *reinterpret_cast<const v4u*>(gb + ((size_t)j * P.N_pad + p) * 16);
-            const v4u w1 = *reinterpret_cast<const v4u*>(gb + ((size_t)(j + 4) * P.N_pad + p) * 16);
-            const v4u w2 = *reinterpret_cast<const v4u*>(gb + ((size_t)(j + 8) * P.N_pad + p) * 16);
-            const v4u w3 = *reinterpret_cast<const v4u*>(gb + ((size_t)(j + 12) * P.N_pad + p) * 16);
-            consume(w0, j);
-            consume(w1, j + 4);
-            consume(w2, j + 8);
-            consume(w3, j + 12);
         }
-        for (; j < j_end; j += 4) consume(*reinterpret_cast<const v4u*>(gb + ((size_t)j * P.N_pad + p) * 16), j);
-    }
+    };
 
+    for (int it = 0; g < groups; ++it) {
+        const int gn = g + gridDim.x;
+        v4u wnext[WMAX][TPB];
+        float csnext[TPB];
+        if (gn < groups) load_group(gn, wnext, csnext);
+        int tile[TPB];
+        tiles_of(g, tile);
+        int acc[TPB][MR];
 #pragma unroll
-    for (int m = 0; m < MR; ++m) red[wave][m][lane] = acc[m];
-    __syncthreads();
-    // Wave w finishes rows w and w + 4 (every lane holds one column).
-    constexpr int RPW = (MR + 3) / 4;
-    int total[RPW];
+        for (int t = 0; t < TPB; ++t)
 #pragma unroll
-    for (int i = 0; i < RPW; ++i) {
-        const int m = wave + 4 * i;
-        total[i] = (m < MR) ? red[0][m][lane] + red[1][m][lane] + red[2][m][lane] + red[3][m][lane] : 0;
-    }
-    if (P.ksplit > 1) {
+            for (int m = 0; m < MR; ++m) acc[t][m] = 0;
 #pragma unroll
-        for (int i = 0; i < RPW; ++i) {
-            const int m = wave + 4 * i;
-            if (m < MR)
-                __hip_atomic_fetch_add(P.acc + (size_t)m * P.N_pad + p, total[i], __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
+        for (int u = 0; u < WMAX; ++u) {
+            const int pl = p_begin + s + 8 * u;
+            if (pl < p_end) consume(acc, wcur[u], pl);
         }
-        __threadfence();
-        __syncthreads();
-        if (tid == 0) {
-            const unsigned prev =
-                __hip_atomic_fetch_add(P.counters + cg, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-            s_last = (prev == (unsigned)(P.ksplit - 1));
-        }
-        __syncthreads();
-        if (!s_last) return;
-        __threadfence();
+        // planes beyond the register window (long K)
+        for (int pl = p_begin + s + 8 * WMAX; pl < p_end; pl += 8) {
+            v4u w[TPB];
 #pragma unroll
-        for (int i = 0; i < RPW; ++i) {
-            const int m = wave + 4 * i;
-            if (m < MR)
-                total[i] = __hip_atomic_exchange(P.acc + (size_t)m * P.N_pad + p, 0, __ATOMIC_RELAXED,
-                                                 __HIP_MEMORY_SCOPE_AGENT);
+            for (int t = 0; t < TPB; ++t)
+                w[t] = *reinterpret_cast<const v4u*>(P.b + ((size_t)tile[t] * PL * 8 + c8) * 16 + (size_t)pl * 128);
+            consume(acc, w, pl);
         }
-        if (tid == 0) __hip_atomic_store(P.counters + cg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+        // reduce over s (shuffles) and waves (LDS, double-buffered); wave 0 stores
+        const int rb = it & 1;
 #pragma unroll
-    for (int i = 0; i < RPW; ++i) {
-        const int m = wave + 4 * i;
-        if (m >= MR) break;  // wave-uniform
-        const bool row_ok = m < P.M;
-        const int corr = (BITS == 4 && row_ok) ? 8 * P.rowsum[m] : 0;
-        const float y = ((float)(total[i] - corr) * P.rowscale[m]) * P.colscale[p];
-        if (EPI == EPI_PLAIN) {
-            if (row_ok && p < P.N) store_out(P.c, P.c_type, (size_t)m * P.ldc + orig_col(p, P.half), y);
-        } else {
-            const float u = __shfl_xor(y, 32);
-            const float o = hm_swiglu(y, u);
-            if (lane < 32 && row_ok && p < P.N) store_out(P.c, P.c_type, (size_t)m * P.ldc + (n0 >> 1) + lane, o);
-            if (EPI == EPI_SWIGLU_MAX) {
-                float mx = lane < 32 ? fabsf(o) : 0.0f;
-                mx = wave_max(mx);
-                if (lane == 0 && row_ok) atomicMax(P.rowmax + m, __float_as_uint(mx));
+        for (int t = 0; t < TPB; ++t)
+#pragma unroll
+            for (int m = 0; m < MR; ++m) {
+                int v = acc[t][m];
+                v += __shfl_xor(v, 8);
+                v += __shfl_xor(v, 16);
+                v += __shfl_xor(v, 32);
+                if (s == 0) red[rb][wave][t][m][c8] = v;
             }
+        __syncthreads();
+        if (wave == 0) {
+#pragma unroll
+            for (int m = 0; m < MR; ++m) {
+                const bool row_ok = m < P.M;
+                float y[TPB];
+#pragma unroll
+                for (int t = 0; t < TPB; ++t) {
+                    const int tot =
+                        red[rb][0][t][m][c8] + red[rb][1][t][m][c8] + red[rb][2][t][m][c8] + red[rb][3][t][m][c8];
+                    y[t] = ((float)(tot - corr[m]) * scale[m]) * cscur[t];
+                }
+                const int p = 8 * tile[0] + c8;
+                if (EPI == EPI_PLAIN) {
+                    if (lane < 8 && row_ok && p < P.N)
+                        store_out(P.c, P.c_type, (size_t)m * P.ldc + orig_col(p, P.half), y[0]);
+                } else {
+                    const float o = hm_swiglu(y[0], y[TPB - 1]);
+                    if (lane < 8 && row_ok && p < P.N)
+                        store_out(P.c, P.c_type, (size_t)m * P.ldc + ((p >> 6) << 5) + (p & 31), o);
+                    if (EPI == EPI_SWIGLU_MAX) {
+                        float mxo = (lane < 8 && p < P.N) ? fabsf(o) : 0.0f;
+                        mxo = fmaxf(mxo, __shfl_xor(mxo, 1));
+                        mxo = fmaxf(mxo, __shfl_xor(mxo, 2));
+                        mxo = fmaxf(mxo, __shfl_xor(mxo, 4));
+                        if (lane == 0) P.part_out[(size_t)m * groups + g] = row_ok ? mxo : 0.0f;
+                    }
+                }
+            }
+        }
+        g = gn;
+        if (g < groups) {
+#pragma unroll
+            for (int u = 0; u < WMAX; ++u)
+#pragma unroll
+                for (int t = 0; t < TPB; ++t) wcur[u][t] = wnext[u][t];
+#pragma unroll
+            for (int t = 0; t < TPB; ++t) cscur[t] = csnext[t];
         }
     }
 }

@@ -58,6 +58,7 @@ struct MoeWork {
     std::atomic<bool> busy;
     Workspace* xws;   // token rows: input staging, quantized input, shared middle
     Workspace* mws;   // slots: middle f32, requantized middle, contributions
+    Workspace* sgws;  // shared expert gate_up (nullable)
     Workspace* sdws;  // shared expert down (nullable)
     int* ids;
     float* routes;
@@ -204,20 +205,23 @@ static MoeWork* work_create(Domain* d, const rk_npu_moe_w8_config* cfg) {
     ws->domain = d;
     ws->busy.store(false);
     ws->stream = nullptr;
-    ws->xws = ws->mws = ws->sdws = nullptr;
+    ws->xws = ws->mws = ws->sgws = ws->sdws = nullptr;
     ws->ids = nullptr;
     ws->host_error = nullptr;
     const int A = cfg->max_rows * cfg->top;
     ws->xws = workspace_create(d, 8, cfg->max_rows, w.hidden, 2 * w.intermediate);
     ws->mws = workspace_create(d, 8, A, w.intermediate, w.hidden);
-    if (ws->shared) ws->sdws = workspace_create(d, 8, cfg->max_rows, w.intermediate, w.hidden);
+    if (ws->shared) {
+        ws->sgws = workspace_create(d, 8, cfg->max_rows, w.hidden, 2 * w.intermediate);
+        ws->sdws = workspace_create(d, 8, cfg->max_rows, w.intermediate, w.hidden);
+    }
     // ids | routes | pos | perm | tiles | counts | error | out
     const size_t sz_a = round_up_z((size_t)A * 4, 256);
     const size_t sz_tiles = round_up_z((size_t)A * 16, 256);
     const size_t sz_out = round_up_z((size_t)cfg->max_rows * w.hidden * 4, 256);
     const size_t total = 4 * sz_a + sz_tiles + 256 + 256 + sz_out;
     uint8_t* base = static_cast<uint8_t*>(domain_alloc(d, total));
-    bool ok = ws->xws && ws->mws && (!ws->shared || ws->sdws) && base;
+    bool ok = ws->xws && ws->mws && (!ws->shared || (ws->sgws && ws->sdws)) && base;
     if (base) {
         size_t off = 0;
         ws->ids = reinterpret_cast<int*>(base + off);
@@ -238,7 +242,7 @@ static MoeWork* work_create(Domain* d, const rk_npu_moe_w8_config* cfg) {
         ok = ok && hipMemset(base, 0, total) == hipSuccess;
     }
     ws->bytes = total + (ws->xws ? ws->xws->bytes : 0) + (ws->mws ? ws->mws->bytes : 0) +
-                (ws->sdws ? ws->sdws->bytes : 0);
+                (ws->sgws ? ws->sgws->bytes : 0) + (ws->sdws ? ws->sdws->bytes : 0);
     ok = ok && hipHostMalloc(reinterpret_cast<void**>(&ws->host_error), 4, hipHostMallocDefault) == hipSuccess;
     ok = ok && hipStreamCreateWithFlags(&ws->stream, hipStreamNonBlocking) == hipSuccess;
     ok = ok && hipDeviceSynchronize() == hipSuccess;
@@ -247,6 +251,7 @@ static MoeWork* work_create(Domain* d, const rk_npu_moe_w8_config* cfg) {
         ws->ids = nullptr;
         workspace_destroy(ws->xws);
         workspace_destroy(ws->mws);
+        workspace_destroy(ws->sgws);
         workspace_destroy(ws->sdws);
         if (ws->host_error) (void)hipHostFree(ws->host_error);
         if (ws->stream) (void)hipStreamDestroy(ws->stream);
@@ -272,14 +277,17 @@ static void work_destroy(MoeWork* ws) {
     if (ws->ids) domain_free(ws->domain, ws->ids, work_table_bytes(ws));
     workspace_destroy(ws->xws);
     workspace_destroy(ws->mws);
+    workspace_destroy(ws->sgws);
     workspace_destroy(ws->sdws);
     if (ws->host_error) (void)hipHostFree(ws->host_error);
     delete static_cast<rk_npu_moe_w8_workspace*>(ws);
 }
 
 template <int BITS, int EPI>
-static void launch_moe_gemm(const MoeGemmParams& G, int grid, hipStream_t s) {
+static void launch_moe_gemm(const MoeGemmParams& G, int grid, hipStream_t s, int rows) {
+    const int slot = prof_begin(s, 3, BITS, EPI, rows, G.K_pad, G.N, EPI == EPI_PLAIN ? "moe_gemm<down>" : "moe_gemm<gate_up>");
     hipLaunchKernelGGL((moe_gemm_kernel<MOE_BM, MOE_BN, 1, 2, BITS, EPI>), dim3(grid), dim3(128), 0, s, G);
+    prof_end(slot, s);
 }
 
 // Enqueues the whole routed FFN (plus shared expert) for `rows` token rows
@@ -287,7 +295,7 @@ static void launch_moe_gemm(const MoeGemmParams& G, int grid, hipStream_t s) {
 static int enqueue_moe(MoeWork* ws, const MoeBank* b, int rows, const float* input, const int* ids,
                        const float* routes, float* out, hipStream_t s) {
     const int A = rows * ws->top;
-    int rc = enqueue_quant(ws->xws, input, DT_F32, ws->h, rows, QUANT_MOE, nullptr, ws->xws->rowmax, s);
+    int rc = enqueue_quant(ws->xws, input, DT_F32, ws->h, rows, QUANT_MOE, RowMax{nullptr, 0}, nullptr, s);
     if (rc != RK_NPU_OK) return rc;
     RouteParams R;
     R.ids = ids;
@@ -328,10 +336,10 @@ static int enqueue_moe(MoeWork* ws, const MoeBank* b, int rows, const float* inp
     G.N_pad = b->ggu.N_pad;
     G.half = b->ggu.half;
     G.tiles_n = b->ggu.N_pad / MOE_BN;
-    launch_moe_gemm<4, EPI_SWIGLU_MAX>(G, max_tiles * G.tiles_n, s);
+    launch_moe_gemm<4, EPI_SWIGLU_MAX>(G, max_tiles * G.tiles_n, s, A);
 
-    rc = enqueue_quant(ws->mws, ws->mws->a_f32, DT_F32, ws->inter, A, QUANT_MOE, ws->mws->rowmax, nullptr, s,
-                       ws->counts);
+    rc = enqueue_quant(ws->mws, ws->mws->a_f32, DT_F32, ws->inter, A, QUANT_MOE,
+                       RowMax{reinterpret_cast<const float*>(ws->mws->rowmax), 1}, nullptr, s, ws->counts);
     if (rc != RK_NPU_OK) return rc;
 
     G.a = ws->mws->codes;
@@ -350,20 +358,16 @@ static int enqueue_moe(MoeWork* ws, const MoeBank* b, int rows, const float* inp
     G.half = b->gdn.half;
     G.tiles_n = b->gdn.N_pad / MOE_BN;
     if (b->dn_bits == 8)
-        launch_moe_gemm<8, EPI_PLAIN>(G, max_tiles * G.tiles_n, s);
+        launch_moe_gemm<8, EPI_PLAIN>(G, max_tiles * G.tiles_n, s, A);
     else
-        launch_moe_gemm<4, EPI_PLAIN>(G, max_tiles * G.tiles_n, s);
+        launch_moe_gemm<4, EPI_PLAIN>(G, max_tiles * G.tiles_n, s, A);
     if (hipGetLastError() != hipSuccess) return RK_NPU_ERR_DEVICE;
 
     const float* shared = nullptr;
     if (b->shared) {
-        rc = enqueue_linear(ws->xws, b->shared_gu, ws->xws->c_f32, DT_F32, ws->inter, rows, EPI_SWIGLU_MAX,
-                            ws->xws->rowmax, s);
-        if (rc == RK_NPU_OK)
-            rc = enqueue_quant(ws->sdws, ws->xws->c_f32, DT_F32, ws->inter, rows, QUANT_MOE, ws->xws->rowmax,
-                               nullptr, s);
-        if (rc == RK_NPU_OK)
-            rc = enqueue_linear(ws->sdws, b->shared_dn, ws->sdws->c_f32, DT_F32, ws->h, rows, EPI_PLAIN, nullptr, s);
+        // The shared expert is an ordinary fused FFN with the MoE rounding rule.
+        rc = enqueue_ffn(ws->sgws, b->shared_gu, ws->sdws, b->shared_dn, input, DT_F32, ws->sdws->c_f32, DT_F32,
+                         rows, QUANT_MOE, s);
         if (rc != RK_NPU_OK) return rc;
         shared = ws->sdws->c_f32;
     }

@@ -132,7 +132,7 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void moe_gemm_kernel(MoeGemmParam
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
     const int n0 = tn * BN;
-    gemm_mainloop<BM, BN, WGM, WGN, BITS>(smem, P.a, (size_t)P.a_alloc, a_off, P.b_tab[e], P.N_pad, n0, P.K_pad >> 6,
+    gemm_mainloop<BM, BN, WGM, WGN, BITS>(smem, P.a, (size_t)P.a_alloc, a_off, P.b_tab[e], P.K_pad, n0, P.K_pad >> 6,
                                           acc);
     gemm_epilogue<BM, BN, WGM, WGN, BITS, EPI>(acc, n0, P.rowscale, P.rowsum, P.s_tab[e], P.N, P.half, P.c, P.ldc,
                                                P.c_type, P.rowmax, [&](int local, int& out_row, int& src_row) {

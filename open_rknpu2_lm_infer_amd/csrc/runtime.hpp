@@ -82,8 +82,7 @@ struct Workspace {
     int* rowsum;      // [M_alloc]
     unsigned* rowmax; // [M_alloc]  max|middle| of a fused SwiGLU output
     float* c_f32;     // [M][N]   output staging / fused middle
-    int* gemv_acc;    // [8][N_pad]
-    unsigned* gemv_counters;  // [N_pad/64]
+    float* partmax;   // [8][N_pad/8] per-block max|middle| of a GEMV SwiGLU
 };
 
 size_t workspace_bytes(const Geometry& g, int M);
@@ -98,18 +97,29 @@ struct Plan {
     int kind;  // 0 GEMV, 1 GEMM
     int bm, bn;
     int mr;
-    int ksplit, kg_per_split;
+    int ksplit;
     int grid;
     int variant;
 };
 Plan plan_linear(int rows, const Geometry& g);
 
+// Row maxima as partials: the max of row r is max_i p[r * count + i].
+struct RowMax {
+    const float* p;
+    int count;
+};
+
 // Enqueue helpers (no synchronization).
-int enqueue_quant(Workspace* ws, const void* x, int x_type, long lda, int rows, int rule,
-                  const unsigned* rowmax_in, unsigned* rowmax_clear, hipStream_t s,
-                  const int* rows_dev = nullptr);
-int enqueue_linear(Workspace* ws, const Weights* w, void* c, int c_type, long ldc, int rows, int epi,
-                   unsigned* rowmax, hipStream_t s);
+int enqueue_quant(Workspace* ws, const void* x, int x_type, long lda, int rows, int rule, RowMax in_max,
+                  unsigned* rowmax_clear, hipStream_t s, const int* rows_dev = nullptr);
+// A full dynamic-int8 linear from activations x: the GEMV quantizes inside
+// its blocks; the GEMM path quantizes with a separate kernel first. With a
+// SwiGLU+max epilogue, *out_max tells where the middle's row maxima are.
+int enqueue_linear(Workspace* ws, const Weights* w, const void* x, int x_type, long lda, int rows, int rule,
+                   RowMax in_max, void* c, int c_type, long ldc, int epi, RowMax* out_max, hipStream_t s);
+// gate_up (SwiGLU + row max) -> requant of the middle (same rule) -> down.
+int enqueue_ffn(Workspace* gws, const Weights* gw, Workspace* dws, const Weights* dw, const void* A, int a_type,
+                void* C, int c_type, int rows, int rule, hipStream_t s);
 
 int device_of(Domain* d);
 struct BusyGuard {
@@ -125,6 +135,11 @@ struct BusyGuard {
 };
 
 double now_us();
+
+// Launch profiling (rk_npu_hip_profile_*): returns a slot index to pass to
+// prof_end, or -1 when profiling is off or the event pool is exhausted.
+int prof_begin(hipStream_t s, int kind, int bits, int epi, int rows, int K, int N, const char* name);
+void prof_end(int slot, hipStream_t s);
 
 }  // namespace hm
 

@@ -1,0 +1,98 @@
+"""Device-resident entry points (rk_npu_hip.h): fp16/fp32 activations in HBM,
+results identical to the host-buffer ABI, and HIP-graph replays identical to
+eager runs (checked on every replay, with eager work in between)."""
+import numpy as np
+import pytest
+
+from oracle import oracle
+from open_rknpu2_lm_infer_amd import device as D
+from open_rknpu2_lm_infer_amd import npu
+from tests import refdata as R
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    return D.DeviceContext(3)
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("rows", [1, 3, 8, 40, 300])
+def test_device_linear_matches_oracle_f32_and_f16(ctx, bits, rows):
+    k, n = 640, 768
+    codes, scales = R.weights(5, f"dl{bits}", bits, k, n)
+    w = ctx.weights(bits, dev(codes), dev(scales))
+    x = R.activations(5, f"dl-x{rows}", rows, k)  # fp16-representable values
+    ref = oracle.linear(codes, scales, x)
+    y32 = torch.empty(rows, n, dtype=torch.float32, device="cuda")
+    D.linear(ctx, w, dev(x), y32, rows)
+    torch.cuda.synchronize()
+    assert np.array_equal(y32.cpu().numpy(), ref)
+    # fp16 activations carry the same values; fp16 output is the f32 result rounded
+    y16 = torch.empty(rows, n, dtype=torch.float16, device="cuda")
+    D.linear(ctx, w, dev(x).half(), y16, rows)
+    torch.cuda.synchronize()
+    assert np.array_equal(y16.cpu().numpy(), ref.astype(np.float16))
+
+
+@pytest.mark.parametrize("rows", [1, 4, 64])
+def test_device_ffn_matches_oracle(ctx, rows):
+    h, f = 512, 768
+    gc, gs = R.weights(5, "dffn-g", 4, h, 2 * f)
+    dc, ds = R.weights(5, "dffn-d", 8, f, h)
+    gu = ctx.weights(4, dev(gc), dev(gs))
+    dn = ctx.weights(8, dev(dc), dev(ds))
+    x = R.activations(5, f"dffn-x{rows}", rows, h)
+    y = torch.empty(rows, h, dtype=torch.float32, device="cuda")
+    D.ffn(ctx, gu, dn, dev(x), y, rows)
+    torch.cuda.synchronize()
+    assert np.array_equal(y.cpu().numpy(), oracle.ffn(gc, gs, dc, ds, x))
+
+
+@pytest.mark.parametrize("rows", [1, 4, 96])
+def test_graph_replay_matches_eager(ctx, rows):
+    h, f = 512, 768
+    gc, gs = R.weights(6, "g-g", 4, h, 2 * f)
+    dc, ds = R.weights(6, "g-d", 4, f, h)
+    qc, qs = R.weights(6, "g-q", 8, h, 384)
+    gu = ctx.weights(4, dev(gc), dev(gs))
+    dn = ctx.weights(4, dev(dc), dev(ds))
+    q = ctx.weights(8, dev(qc), dev(qs))
+    x = dev(R.activations(6, f"g-x{rows}", rows, h)).half()
+    y1 = torch.empty(rows, h, dtype=torch.float16, device="cuda")
+    y2 = torch.empty(rows, 384, dtype=torch.float16, device="cuda")
+
+    def step():
+        D.ffn(ctx, gu, dn, x, y1, rows)
+        D.linear(ctx, q, x, y2, rows)
+
+    step()
+    torch.cuda.synchronize()
+    e1, e2 = y1.clone(), y2.clone()
+    xf = x.float().cpu().numpy()
+    assert np.array_equal(e1.cpu().numpy(), oracle.ffn(gc, gs, dc, ds, xf).astype(np.float16))
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=s):
+            step()
+    torch.cuda.synchronize()
+    for _ in range(4):
+        y1.zero_()
+        y2.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y1, e1) and torch.equal(y2, e2)
+        step()  # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(y1, e1) and torch.equal(y2, e2)
