@@ -6,8 +6,9 @@
  * the host-buffer entry points, so their results are bit-identical.
  *
  * All A/C/ids/routes pointers are DEVICE pointers on the context's GPU.
- * `stream` is a hipStream_t (NULL = the workspace's own stream); the call
- * only enqueues work and returns without synchronizing. The workspace stays
+ * `stream` is the hipStream_t the work is enqueued on, used as given (NULL is
+ * the HIP null stream, so work stays ordered with a caller that uses it); the
+ * call only enqueues work and returns without synchronizing. The workspace stays
  * busy until that work completes on the stream: the caller must not issue a
  * second call on the same workspace from another stream before that.
  */

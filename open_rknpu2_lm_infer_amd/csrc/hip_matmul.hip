@@ -400,7 +400,7 @@ template <int BITS, int EPI>
 static void launch_gemm(int v, const GemmParams& G, int grid, hipStream_t s) {
     switch (v) {
         case V256x256:
-            hipLaunchKernelGGL((gemm_kernel<256, 256, 2, 2, BITS, EPI>), dim3(grid), dim3(256), 0, s, G);
+            hipLaunchKernelGGL((gemm_kernel<256, 256, 2, 4, BITS, EPI>), dim3(grid), dim3(512), 0, s, G);
             break;
         case V256x128:
             hipLaunchKernelGGL((gemm_kernel<256, 128, 2, 2, BITS, EPI>), dim3(grid), dim3(256), 0, s, G);
@@ -1014,7 +1014,7 @@ int rk_npu_hip_linear_run(void* workspace, const void* weights, int bits, const 
     BusyGuard guard(ws->busy);
     if (!guard.ok) return RK_NPU_ERR_BUSY;
     if (hipSetDevice(device_of(ws->domain)) != hipSuccess) return RK_NPU_ERR_DEVICE;
-    hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ws->stream;
+    hipStream_t s = static_cast<hipStream_t>(stream);
     const int width = epi == EPI_PLAIN ? w->g.N : w->g.N / 2;
     return enqueue_linear(ws, w, A, a_type, w->g.K, rows, QUANT_DENSE, RowMax{nullptr, 0}, C, c_type, width, epi,
                           nullptr, s);
@@ -1036,7 +1036,7 @@ int rk_npu_hip_ffn_run(void* gate_up_workspace, const void* gate_up, int gu_bits
     BusyGuard g2(dws->busy);
     if (!g2.ok) return RK_NPU_ERR_BUSY;
     if (hipSetDevice(device_of(gws->domain)) != hipSuccess) return RK_NPU_ERR_DEVICE;
-    hipStream_t s = stream ? static_cast<hipStream_t>(stream) : gws->stream;
+    hipStream_t s = static_cast<hipStream_t>(stream);
     return enqueue_ffn(gws, gw, dws, dw, A, a_type, C, c_type, rows, QUANT_DENSE, s);
 }
 

@@ -309,6 +309,17 @@ struct GemmParams {
 // (BM x BN) tile whose A rows are given per thread by a_off (the plane-0 chunk
 // index of each of the thread's A loads) and whose B panel starts at column n0
 // of gb. acc must be zero on entry.
+//
+// Pipeline: STAGES LDS buffers filled by direct global->LDS loads
+// (global_load_lds_dwordx4: each lane's 16 bytes land at base + 16*lane, no
+// staging registers), STAGES-1 of them in flight while one stage is
+// multiplied. Each wave waits only for its own loads of the next stage (vmcnt
+// counts the later stages still in flight) and one barrier per stage makes
+// every wave's loads visible. Fragments are double-buffered in registers: the
+// next stage is read from LDS while the MFMAs of the current one run. LDS
+// keeps the fragment order A [k16 plane][BM][16] and B [plane][BN][16], so
+// every fragment read is 16 consecutive bytes per lane for 32 consecutive
+// lanes.
 template <int BM, int BN, int WGM, int WGN, int BITS>
 struct TileCfg {
     static constexpr int NT = WGM * WGN * 64;
@@ -319,8 +330,31 @@ struct TileCfg {
     static constexpr int STAGE = A_STAGE + B_STAGE;
     static constexpr int A_LOADS = A_STAGE / 16 / NT;
     static constexpr int B_LOADS = B_STAGE / 16 / NT;
+    static constexpr int LPS = A_LOADS + B_LOADS;
+    // as many stages as fit in 128 KB of LDS, at most 4
+    static constexpr int STAGES = (4 * STAGE <= 131072) ? 4 : (3 * STAGE <= 131072 ? 3 : 2);
+    static constexpr int LDS = STAGES * STAGE;
     static_assert(A_STAGE % (16 * NT) == 0 && B_STAGE % (16 * NT) == 0, "tile/thread mismatch");
+    static_assert(BN % 64 == 0, "a wave's B loads must cover one plane");
+    static_assert(LPS * (STAGES - 1) <= 63, "vmcnt range");
 };
+
+// 16-byte direct global->LDS load: lane l's bytes land at lds + 16*l.
+__device__ __forceinline__ void lds_dma16(const void* g, void* lds) {
+    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
+
+// s_waitcnt through the builtin (not inline asm) so that the compiler's own
+// wait insertion sees it. gfx9 encoding: vmcnt[3:0] bits 3:0, expcnt bits 6:4,
+// lgkmcnt bits 11:8, vmcnt[5:4] bits 15:14; a field at its maximum waits for
+// nothing.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N <= 63, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+__device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4)); }
 
 template <int BM, int BN, int WGM, int WGN, int BITS>
 __device__ __forceinline__ void gemm_mainloop(uint8_t* smem, const int8_t* __restrict__ ga, size_t a_plane,
@@ -331,90 +365,119 @@ __device__ __forceinline__ void gemm_mainloop(uint8_t* smem, const int8_t* __res
     using C = TileCfg<BM, BN, WGM, WGN, BITS>;
     constexpr int NT = C::NT, TM = C::TM, TN = C::TN, FM = C::FM, FN = C::FN;
     constexpr int A_STAGE = C::A_STAGE, STAGE = C::STAGE, A_LOADS = C::A_LOADS, B_LOADS = C::B_LOADS;
+    constexpr int S = C::STAGES, LPS = C::LPS;
+    constexpr int PPS = (BITS == 8) ? 4 : 2;  // weight planes per 64-k step
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave / WGN, wn = wave % WGN;
     const int half_id = lane >> 5, l32 = lane & 31;
-
-    // B stage: BN/8 column tiles x PPS planes x 8 columns. Chunk c -> tile
-    // c/(8*PPS), plane (c/8)%PPS, column c%8: every 8*PPS lanes read one
-    // contiguous run of a tile; LDS keeps the [plane][BN][16] fragment order.
-    constexpr int PPS = (BITS == 8) ? 4 : 2;
     const int planes = (BITS == 8) ? K_pad / 16 : K_pad / 32;
+
+    // B chunk c (LDS order [plane][BN][16]) of this thread's i-th load.
     size_t b_src[B_LOADS];
-    int b_dst[B_LOADS];
 #pragma unroll
     for (int i = 0; i < B_LOADS; ++i) {
         const int c = tid + i * NT;
-        const int t = c / (8 * PPS), pl = (c / 8) % PPS, c8 = c % 8;
-        b_src[i] = (((size_t)(n0 / 8 + t) * planes + pl) * 8 + c8) * 16;
-        b_dst[i] = (pl * BN + t * 8 + c8) * 16;
+        const int pl = c / BN, n = c % BN;
+        b_src[i] = ((size_t)(n0 / 8 + n / 8) * planes + pl) * 128 + (n % 8) * 16;
     }
-    v4i ra[A_LOADS], rb[B_LOADS];
-    auto gload = [&](int kt) {
-#pragma unroll
-        for (int i = 0; i < A_LOADS; ++i)
-            ra[i] = *reinterpret_cast<const v4i*>(ga + ((size_t)kt * 4 * a_plane + a_off[i]) * 16);
-#pragma unroll
-        for (int i = 0; i < B_LOADS; ++i)
-            rb[i] = *reinterpret_cast<const v4i*>(gb + b_src[i] + (size_t)kt * (PPS * 128));
-    };
-    auto sstore = [&](int buf) {
+
+    // Fragment registers of one stage, flattened: f < 2*FM is A[s][i] (32-k
+    // half s, row block i); then B[h][j] for both halves (W8) or the packed
+    // plane whose two nibbles give both halves (W4).
+    constexpr int BH = (BITS == 8) ? 2 : 1;
+    constexpr int NF = 2 * FM + BH * FN;
+    constexpr int T = 2 * FM * FN;           // MFMAs per stage
+    constexpr int G = T >= 4 ? T / 4 : 1;    // issue groups per stage
+    const int a_lane = (half_id * BM + wm * TM + l32) * 16;
+    const int b_lane = (half_id * BN + wn * TN + l32) * 16;
+
+    // Load d of a stage (A loads first), fragment read f, MFMA t: all indices
+    // are compile-time constants after unrolling.
+    auto issue1 = [&](int d, int kt_, int buf) {
         uint8_t* sa = smem + buf * STAGE;
-        uint8_t* sb = sa + A_STAGE;
-#pragma unroll
-        for (int i = 0; i < A_LOADS; ++i) *reinterpret_cast<v4i*>(sa + (tid + i * NT) * 16) = ra[i];
-#pragma unroll
-        for (int i = 0; i < B_LOADS; ++i) *reinterpret_cast<v4i*>(sb + b_dst[i]) = rb[i];
+        if (d < A_LOADS)
+            lds_dma16(ga + ((size_t)kt_ * 4 * a_plane + a_off[d]) * 16, sa + (d * NT + wave * 64) * 16);
+        else
+            lds_dma16(gb + b_src[d - A_LOADS] + (size_t)kt_ * (PPS * 128),
+                      sa + A_STAGE + ((d - A_LOADS) * NT + wave * 64) * 16);
+    };
+    auto read1 = [&](int f, int buf) -> v4i {
+        const uint8_t* r = smem + buf * STAGE;
+        if (f < 2 * FM) return *reinterpret_cast<const v4i*>(r + a_lane + (2 * (f / FM) * BM + (f % FM) * 32) * 16);
+        const int h = (f - 2 * FM) / FN, j = (f - 2 * FM) % FN;
+        return *reinterpret_cast<const v4i*>(r + A_STAGE + b_lane + (2 * h * BN + j * 32) * 16);
+    };
+    auto mfma1 = [&](int t, const v4i(&c)[NF]) {
+        const int s2 = t / (FM * FN), i = (t / FN) % FM, j = t % FN;
+        v4i bf;
+        if (BITS == 8) {
+            bf = c[2 * FM + s2 * FN + j];
+        } else {
+            const v4u raw = __builtin_bit_cast(v4u, c[2 * FM + j]);
+            bf = __builtin_bit_cast(v4i, s2 == 0 ? (raw & 0x0F0F0F0Fu) : ((raw >> 4) & 0x0F0F0F0Fu));
+        }
+        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(c[s2 * FM + i], bf, acc[i][j], 0, 0, 0);
     };
 
-    gload(0);
-    sstore(0);
-    __syncthreads();
-    for (int kt = 0; kt < KT; ++kt) {
-        const int cur = kt & 1;
-        if (kt + 1 < KT) gload(kt + 1);
-        const uint8_t* sa = smem + cur * STAGE;
-        const uint8_t* sb = sa + A_STAGE;
-        if (BITS == 8) {
+    // Prologue: stages 0..S-1 in flight, stage 0 read into registers.
 #pragma unroll
-            for (int s = 0; s < 2; ++s) {
-                v4i af[FM], bf[FN];
+    for (int st = 0; st < S; ++st)
+        if (st < KT)
 #pragma unroll
-                for (int i = 0; i < FM; ++i)
-                    af[i] = *reinterpret_cast<const v4i*>(sa + ((2 * s + half_id) * BM + wm * TM + i * 32 + l32) * 16);
+            for (int d = 0; d < LPS; ++d) issue1(d, st, st);
+    if (KT >= S)
+        wait_vmcnt<LPS * (S - 1)>();
+    else
+        wait_vmcnt<0>();
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    v4i cur[NF], nxt[NF];
 #pragma unroll
-                for (int j = 0; j < FN; ++j)
-                    bf[j] = *reinterpret_cast<const v4i*>(sb + ((2 * s + half_id) * BN + wn * TN + j * 32 + l32) * 16);
-#pragma unroll
-                for (int i = 0; i < FM; ++i)
-#pragma unroll
-                    for (int j = 0; j < FN; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
-            }
-        } else {
-            v4u bw[FN];
-#pragma unroll
-            for (int j = 0; j < FN; ++j)
-                bw[j] = *reinterpret_cast<const v4u*>(sb + (half_id * BN + wn * TN + j * 32 + l32) * 16);
-#pragma unroll
-            for (int s = 0; s < 2; ++s) {
-                v4i af[FM];
-#pragma unroll
-                for (int i = 0; i < FM; ++i)
-                    af[i] = *reinterpret_cast<const v4i*>(sa + ((2 * s + half_id) * BM + wm * TM + i * 32 + l32) * 16);
-#pragma unroll
-                for (int j = 0; j < FN; ++j) {
-                    const v4u nib = (s == 0) ? (bw[j] & 0x0F0F0F0Fu) : ((bw[j] >> 4) & 0x0F0F0F0Fu);
-                    const v4i bf = __builtin_bit_cast(v4i, nib);
-#pragma unroll
-                    for (int i = 0; i < FM; ++i)
-                        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf, acc[i][j], 0, 0, 0);
-                }
-            }
-        }
-        if (kt + 1 < KT) sstore(cur ^ 1);
-        __syncthreads();
+    for (int f = 0; f < NF; ++f) cur[f] = read1(f, 0);
+
+    // Iteration kt: stage kt is in registers (or arriving). Once every wave
+    // holds its fragments and its own loads of stage kt+1 have landed, one
+    // barrier frees buffer kt%S for stage kt+S and publishes stage kt+1. The
+    // loads of stage kt+S and the fragment reads of stage kt+1 (into the other
+    // register set) are then spread over G groups of the stage's MFMAs, so
+    // the load path and the LDS stay busy while the matrix cores run. Past the
+    // last stage the read is stale and unused.
+#define HM_STAGE(kt_, C_, N_)                                                                     \
+    do {                                                                                          \
+        wait_lgkmcnt0();                                                                          \
+        if ((kt_) + 1 < KT) {                                                                     \
+            if ((kt_) + S - 1 < KT)                                                               \
+                wait_vmcnt<LPS * (S - 2)>();                                                      \
+            else                                                                                  \
+                wait_vmcnt<0>();                                                                  \
+        }                                                                                         \
+        __builtin_amdgcn_s_barrier();                                                             \
+        asm volatile("" ::: "memory");                                                            \
+        const bool iss_ = (kt_) + S < KT;                                                         \
+        const int nbuf_ = ((kt_) + 1) % S, ibuf_ = (kt_) % S;                                     \
+        _Pragma("unroll") for (int g = 0; g < G; ++g) {                                           \
+            __builtin_amdgcn_sched_barrier(0);                                                    \
+            if (iss_)                                                                             \
+                _Pragma("unroll") for (int d = g * LPS / G; d < (g + 1) * LPS / G; ++d)           \
+                    issue1(d, (kt_) + S, ibuf_);                                                  \
+            _Pragma("unroll") for (int f = g * NF / G; f < (g + 1) * NF / G; ++f)                 \
+                N_[f] = read1(f, nbuf_);                                                          \
+            __builtin_amdgcn_sched_barrier(0);                                                    \
+            _Pragma("unroll") for (int t = g * T / G; t < (g + 1) * T / G; ++t) mfma1(t, C_);     \
+        }                                                                                         \
+        __builtin_amdgcn_sched_barrier(0);                                                        \
+    } while (0)
+
+    // Pairs of stages ping-pong between the two register sets; an odd last
+    // stage runs after the loop (a conditional second stage inside the loop
+    // makes the compiler spill the accumulators).
+    int kt = 0;
+    for (; kt + 1 < KT; kt += 2) {
+        HM_STAGE(kt, cur, nxt);
+        HM_STAGE(kt + 1, nxt, cur);
     }
+    if (kt < KT) HM_STAGE(kt, cur, nxt);
+#undef HM_STAGE
 }
 
 // Epilogue of a finished tile. Fragment (i, j) register r holds row
@@ -424,46 +487,102 @@ template <int BM, int BN, int WGM, int WGN, int BITS, int EPI, typename RowMap>
 __device__ __forceinline__ void gemm_epilogue(
     const v16i (&acc)[TileCfg<BM, BN, WGM, WGN, BITS>::FM][TileCfg<BM, BN, WGM, WGN, BITS>::FN], int n0,
     const float* __restrict__ rowscale, const int* __restrict__ rowsum, const float* __restrict__ colscale, int N,
-    int half, void* c, long ldc, int c_type, unsigned* rowmax, RowMap row_of) {
+    int half, void* c, long ldc, int c_type, unsigned* rowmax, RowMap row_of, uint8_t* smem) {
     using C = TileCfg<BM, BN, WGM, WGN, BITS>;
-    constexpr int TM = C::TM, TN = C::TN, FM = C::FM, FN = C::FN;
+    constexpr int TM = C::TM, TN = C::TN, FM = C::FM, FN = C::FN, NW = WGM * WGN;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave / WGN, wn = wave % WGN;
     const int half_id = lane >> 5, l32 = lane & 31;
+    const int esz = c_type == DT_F32 ? 4 : 2;
+    // Output columns this wave owns (SwiGLU: TN/2, contiguous from out0).
+    constexpr int OUTC = (EPI == EPI_PLAIN) ? TN : TN / 2;
+
+    // Rows are staged through LDS and written as 16-byte runs when the output
+    // allows it (16-byte aligned base and row pitch); otherwise each lane
+    // stores its own elements. Values and rounding are identical either way.
+    const bool staged = ((reinterpret_cast<uintptr_t>(c) & 15) == 0) && ((((size_t)ldc * esz) & 15) == 0);
+    constexpr int WAVE_LDS = C::LDS / NW;
+    constexpr int FIT = WAVE_LDS / (32 * (OUTC * 4 + 16));
+    static_assert(FIT >= 1, "epilogue staging does not fit in LDS");
+    constexpr int FPI = FIT >= FM ? FM : ((FIT >= 2 && FM % 2 == 0) ? 2 : 1);
+    const int pitch = OUTC * esz + 16;
+    uint8_t* wl = smem + wave * WAVE_LDS;
+    if (staged) __syncthreads();
+
 #pragma unroll
-    for (int i = 0; i < FM; ++i) {
+    for (int i0 = 0; i0 < FM; i0 += FPI) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int local = wm * TM + i * 32 + (r >> 2) * 8 + half_id * 4 + (r & 3);
-            int out_row, src_row;
-            const bool row_ok = row_of(local, out_row, src_row);
-            const float s_row = rowscale[src_row];
-            const int corr = (BITS == 4) ? 8 * rowsum[src_row] : 0;
-            if (EPI == EPI_PLAIN) {
+        for (int ii = 0; ii < FPI; ++ii) {
+            const int i = i0 + ii;
 #pragma unroll
-                for (int j = 0; j < FN; ++j) {
-                    const int p = n0 + wn * TN + j * 32 + l32;
-                    const float y = ((float)(acc[i][j][r] - corr) * s_row) * colscale[p];
-                    if (row_ok && p < N) store_out(c, c_type, (size_t)out_row * ldc + orig_col(p, half), y);
-                }
-            } else {
-                float mx = 0.0f;
+            for (int r = 0; r < 16; ++r) {
+                const int rr = (r >> 2) * 8 + half_id * 4 + (r & 3);
+                const int local = wm * TM + i * 32 + rr;
+                uint8_t* lrow = wl + (ii * 32 + rr) * pitch;
+                int out_row, src_row;
+                const bool row_ok = row_of(local, out_row, src_row);
+                const float s_row = rowscale[src_row];
+                const int corr = (BITS == 4) ? 8 * rowsum[src_row] : 0;
+                if (EPI == EPI_PLAIN) {
 #pragma unroll
-                for (int j = 0; j < FN; j += 2) {
-                    const int p = n0 + wn * TN + j * 32 + l32;
-                    const float g = ((float)(acc[i][j][r] - corr) * s_row) * colscale[p];
-                    const float u = ((float)(acc[i][j + 1][r] - corr) * s_row) * colscale[p + 32];
-                    const float o = hm_swiglu(g, u);
-                    mx = fmaxf(mx, fabsf(o));
-                    if (row_ok && p < N) store_out(c, c_type, (size_t)out_row * ldc + ((p >> 6) << 5) + l32, o);
-                }
-                if (EPI == EPI_SWIGLU_MAX) {
+                    for (int j = 0; j < FN; ++j) {
+                        const int p = n0 + wn * TN + j * 32 + l32;
+                        const float y = ((float)(acc[i][j][r] - corr) * s_row) * colscale[p];
+                        if (staged)
+                            store_out(lrow, c_type, j * 32 + l32, y);
+                        else if (row_ok && p < N)
+                            store_out(c, c_type, (size_t)out_row * ldc + orig_col(p, half), y);
+                    }
+                } else {
+                    float mx = 0.0f;
 #pragma unroll
-                    for (int off = 16; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-                    if (l32 == 0 && row_ok) atomicMax(rowmax + out_row, __float_as_uint(mx));
+                    for (int j = 0; j < FN; j += 2) {
+                        const int p = n0 + wn * TN + j * 32 + l32;
+                        const float g = ((float)(acc[i][j][r] - corr) * s_row) * colscale[p];
+                        const float u = ((float)(acc[i][j + 1][r] - corr) * s_row) * colscale[p + 32];
+                        const float o = hm_swiglu(g, u);
+                        mx = fmaxf(mx, fabsf(o));
+                        if (staged)
+                            store_out(lrow, c_type, (j >> 1) * 32 + l32, o);
+                        else if (row_ok && p < N)
+                            store_out(c, c_type, (size_t)out_row * ldc + ((p >> 6) << 5) + l32, o);
+                    }
+                    if (EPI == EPI_SWIGLU_MAX) {
+#pragma unroll
+                        for (int off = 16; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+                        if (l32 == 0 && row_ok) atomicMax(rowmax + out_row, __float_as_uint(mx));
+                    }
                 }
             }
         }
+        if (!staged) continue;
+        __syncthreads();
+        // 16-byte runs: chunk q of the staged rows -> (row, 16/esz columns).
+        const int per = 16 / esz, cpr = OUTC / per;
+        const int n_out = (EPI == EPI_PLAIN) ? N : N / 2;
+        for (int q = lane; q < FPI * 32 * cpr; q += 64) {
+            const int lr = q / cpr, cc = (q - lr * cpr) * per;
+            int out_row, src_row;
+            if (!row_of(wm * TM + i0 * 32 + lr, out_row, src_row)) continue;
+            int col, valid;
+            if (EPI == EPI_PLAIN) {
+                const int p = n0 + wn * TN + cc;
+                col = orig_col(p, half);
+                valid = N - p;
+            } else {
+                col = ((n0 + wn * TN) >> 1) + cc;
+                valid = n_out - col;
+            }
+            const uint8_t* src = wl + lr * pitch + cc * esz;
+            uint8_t* dst = static_cast<uint8_t*>(c) + ((size_t)out_row * ldc + col) * esz;
+            if (valid >= per) {
+                *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(src);
+            } else {
+                for (int t = 0; t < valid; ++t)
+                    for (int bb = 0; bb < esz; ++bb) dst[t * esz + bb] = src[t * esz + bb];
+            }
+        }
+        __syncthreads();
     }
 }
 
@@ -471,7 +590,7 @@ template <int BM, int BN, int WGM, int WGN, int BITS, int EPI>
 __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_kernel(GemmParams P) {
     using C = TileCfg<BM, BN, WGM, WGN, BITS>;
     static_assert(EPI == EPI_PLAIN || C::FN % 2 == 0, "SwiGLU pairs need an even fragment count");
-    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * C::STAGE];
+    __shared__ __attribute__((aligned(16))) uint8_t smem[C::LDS];
 
     // Block -> tile: give each of the 8 XCDs (blocks are dealt round-robin)
     // a contiguous range of tile ids, then walk groups of 8 M-tiles so that
@@ -510,7 +629,7 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_kernel(GemmParams P) {
                                                    out_row = row;
                                                    src_row = row < M ? row : 0;
                                                    return row < M;
-                                               });
+                                               }, smem);
 }
 
 // ---------------------------------------------------------------------------

@@ -541,7 +541,7 @@ int rk_npu_hip_moe_run(rk_npu_moe_w8_workspace* workspace, const rk_npu_moe_w8_w
     BusyGuard guard(ws->busy);
     if (!guard.ok) return RK_NPU_ERR_BUSY;
     if (hipSetDevice(device_of(ws->domain)) != hipSuccess) return RK_NPU_ERR_DEVICE;
-    hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ws->stream;
+    hipStream_t s = static_cast<hipStream_t>(stream);
     return enqueue_moe(ws, weights, rows, input, ids, routes, output, s);
 }
 

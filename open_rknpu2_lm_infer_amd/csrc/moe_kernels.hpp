@@ -107,7 +107,7 @@ struct MoeGemmParams {
 template <int BM, int BN, int WGM, int WGN, int BITS, int EPI>
 __global__ __launch_bounds__(WGM* WGN * 64, 1) void moe_gemm_kernel(MoeGemmParams P) {
     using C = TileCfg<BM, BN, WGM, WGN, BITS>;
-    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * C::STAGE];
+    __shared__ __attribute__((aligned(16))) uint8_t smem[C::LDS];
     __shared__ int s_rows[BM];
     const int t = blockIdx.x / P.tiles_n, tn = blockIdx.x % P.tiles_n;
     if (t >= P.counts[1]) return;
@@ -139,7 +139,7 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void moe_gemm_kernel(MoeGemmParam
                                                    out_row = begin + local;
                                                    src_row = s_rows[local];
                                                    return begin + local < end;
-                                               });
+                                               }, smem);
 }
 
 // ---------------------------------------------------------------------------

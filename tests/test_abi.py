@@ -99,8 +99,14 @@ def test_queries_and_config_init_without_a_device():
 def test_plans():
     L = F.lib()
     plan = F.rk_npu_hip_plan()
+    # decode rows run the GEMV on 8-column weight tiles
     assert L.rk_npu_hip_linear_plan(1, 2560, 19456, 4, ctypes.byref(plan)) == 0
-    assert plan.kind == 0 and plan.block_n == 64 and plan.k_splits >= 1
+    assert (plan.kind, plan.block_m, plan.block_n, plan.k_splits, plan.grid) == (0, 1, 8, 1, 19456 // 8)
+    assert L.rk_npu_hip_linear_plan(8, 2560, 6144, 8, ctypes.byref(plan)) == 0
+    assert (plan.kind, plan.block_m) == (0, 8)
+    # a K too long for the GEMV's quantized rows in LDS (8 x 9728 bytes) takes the GEMM
+    assert L.rk_npu_hip_linear_plan(8, 9728, 2560, 8, ctypes.byref(plan)) == 0
+    assert (plan.kind, plan.block_m, plan.block_n) == (1, 32, 128)
     assert L.rk_npu_hip_linear_plan(4096, 2560, 9728, 8, ctypes.byref(plan)) == 0
     assert plan.kind == 1 and plan.block_m == 256 and plan.block_n == 256
     assert L.rk_npu_hip_linear_plan(0, 2560, 9728, 8, ctypes.byref(plan)) == F.RK_NPU_ERR_PARAM
