@@ -417,30 +417,9 @@ static void launch_gemm(int v, const GemmParams& G, int grid, hipStream_t s) {
     }
 }
 
-// Resident blocks of a GEMV instantiation on this device (persistent grid).
-template <typename T, int MR, int BITS, int EPI>
-static int gemv_capacity(size_t lds) {
-    static std::mutex mu;
-    static std::map<size_t, int> cache;
-    std::lock_guard<std::mutex> lock(mu);
-    auto it = cache.find(lds);
-    if (it != cache.end()) return it->second;
-    int per_cu = 0, dev = 0, cus = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gemv_kernel<T, MR, BITS, EPI>, 256, lds) != hipSuccess ||
-        per_cu < 1)
-        per_cu = 1;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
-        cus = 256;
-    const int cap = per_cu * cus * std::max(1, env_int("HM_GEMV_WAVES_PER_SLOT", 1));
-    cache[lds] = cap;
-    return cap;
-}
-
 template <typename T, int MR, int BITS, int EPI>
 static void launch_gemv_mr(const GemvParams& V, int groups, size_t lds, hipStream_t s) {
-    const int grid = std::min(groups, gemv_capacity<T, MR, BITS, EPI>(lds));
-    hipLaunchKernelGGL((gemv_kernel<T, MR, BITS, EPI>), dim3(grid), dim3(256), lds, s, V);
+    hipLaunchKernelGGL((gemv_kernel<T, MR, BITS, EPI>), dim3(groups), dim3(256), lds, s, V);
 }
 
 template <typename T, int BITS, int EPI>

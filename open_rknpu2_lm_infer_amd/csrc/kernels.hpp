@@ -143,6 +143,24 @@ __device__ __forceinline__ void load16(const __half* p, float (&v)[16]) {
         }
     }
 }
+// 16 activations as raw 16-byte words (2 for fp16, 4 for f32), so a load can
+// be issued now and converted later without waiting on anything else.
+template <typename T>
+__device__ __forceinline__ void load16_raw(const T* p, v4u (&r)[4]) {
+#pragma unroll
+    for (int q = 0; q < (int)(16 * sizeof(T) / 16); ++q) r[q] = reinterpret_cast<const v4u*>(p)[q];
+}
+__device__ __forceinline__ void cvt16_raw(const v4u (&r)[4], float (&v)[16], float) {
+#pragma unroll
+    for (int b = 0; b < 16; ++b) v[b] = __uint_as_float(r[b >> 2][b & 3]);
+}
+__device__ __forceinline__ void cvt16_raw(const v4u (&r)[4], float (&v)[16], __half) {
+#pragma unroll
+    for (int b = 0; b < 16; ++b) {
+        const unsigned bits = r[b >> 3][(b >> 1) & 3];
+        v[b] = __half2float(__ushort_as_half((unsigned short)((b & 1) ? (bits >> 16) : (bits & 0xffffu))));
+    }
+}
 
 template <typename T, int RULE>
 __global__ __launch_bounds__(256) void quant_rows_kernel(QuantParams P) {
@@ -634,15 +652,19 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_kernel(GemmParams P) {
 
 // ---------------------------------------------------------------------------
 // Decode GEMV / skinny GEMM (M <= 8) without MFMA: bandwidth bound, one launch.
-// A block owns one 8-column weight tile (two for SwiGLU: a gate tile and its
-// up tile) for the whole K, so no reduction crosses blocks. Its 4 waves split
-// the tile's planes; within a wave, lane (s, c8) = (lane/8, lane%8) reads
-// plane p0 + s + 8i of column c8, so each wave load is 1 KB contiguous.
-// The block first issues its first weight loads, then quantizes the
-// activation rows itself (row max from x or from precomputed partial maxima,
-// the dense or MoE rule) into LDS while those loads are in flight. Dot
-// products use v_dot4_i32_i8; partials reduce over s with cross-lane shuffles
-// and over waves through LDS. SwiGLU+max writes one partial max per block.
+// A block owns one tile group for the whole K: one 8-column weight tile, or
+// (SwiGLU) a gate tile and its up tile, so no reduction crosses blocks and
+// one block is launched per group (enough blocks are resident that every
+// weight byte of a decode-sized matrix is requested at once). The group's
+// bytes are a flat stream of 16-byte chunks (chunk q = plane q/8, column q%8
+// of its tile); thread tid takes chunks tid + 256r, so every wave load is
+// 1 KB contiguous and the column of a thread is fixed (tid % 8). All chunks
+// (up to two windows of RW rounds) are requested first; the block then
+// quantizes the activation rows itself (row max from x or from precomputed
+// partial maxima, the dense or MoE rule) into LDS while they are in flight.
+// Dot products use v_dot4_i32_i8; partials reduce over threads of the same
+// column with cross-lane shuffles and over waves through LDS. SwiGLU+max
+// writes one partial max per block.
 // ---------------------------------------------------------------------------
 struct GemvParams {
     const void* x;
@@ -674,66 +696,99 @@ template <typename T, int MR, int BITS, int EPI>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
     extern __shared__ __attribute__((aligned(16))) int8_t sa[];  // [K_pad/16][MR][16]
     constexpr int TPB = (EPI == EPI_PLAIN) ? 1 : 2;
-    constexpr int WMAX = (TPB == 1) ? 12 : 6;  // weight planes per lane held in registers
-    constexpr int XMAX = 3;                    // 16-element activation chunks per thread in registers
+    constexpr int RW = 8;     // rounds (16-byte chunks per thread) per window
+    constexpr int XMAX = 3;   // 16-element activation chunks per thread in registers
+    constexpr int PV = 5;     // precomputed row-max partials per thread in registers
     __shared__ float s_red[4][MR];
     __shared__ int s_isum[4][MR];
-    __shared__ int red[2][4][TPB][MR][8];
+    __shared__ int red[4][TPB][MR][8];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int c8 = lane & 7, s = lane >> 3;
+    const int c8 = tid & 7;
     const int KG16 = P.K_pad >> 4;
     const int PL = (BITS == 8) ? KG16 : (P.K_pad >> 5);
-    const int PW = (((PL + 3) >> 2) + 7) & ~7;
-    const int p_begin = wave * PW, p_end = min(PL, p_begin + PW);
-    const int groups = (TPB == 1) ? (P.N_pad >> 3) : (P.N_pad >> 4);
+    const int CPT = PL * 8;                  // chunks per tile
+    const int CPG = CPT * TPB;               // chunks per group
+    const int NWIN = (CPG + 256 * RW - 1) / (256 * RW);
+    const int g = blockIdx.x;
+    const int groups = gridDim.x;
 
     // Tile group g: one 8-column tile, or (SwiGLU) a gate tile and its up tile.
-    auto tiles_of = [&](int g, int (&tile)[TPB]) {
-        if (TPB == 1) {
-            tile[0] = g;
-        } else {
-            tile[0] = 8 * (g >> 2) + (g & 3);
-            tile[TPB - 1] = tile[0] + 4;
-        }
-    };
-    auto load_group = [&](int g, v4u (&w)[WMAX][TPB], float (&cs)[TPB]) {
-        int tile[TPB];
-        tiles_of(g, tile);
+    int tile[TPB];
+    if (TPB == 1) {
+        tile[0] = g;
+    } else {
+        tile[0] = 8 * (g >> 2) + (g & 3);
+        tile[TPB - 1] = tile[0] + 4;
+    }
+    const uint8_t* tb0 = P.b + (size_t)tile[0] * CPT * 16;
+    const uint8_t* tb1 = P.b + (size_t)tile[TPB - 1] * CPT * 16;
+    // Loads are unconditional (a chunk past the group re-reads its last one
+    // and is skipped by the dots), so the compiler's wait counts are exact:
+    // a load under a branch makes every later wait assume it may be missing.
+    auto load_window = [&](int w, v4u (&buf)[RW]) {
 #pragma unroll
-        for (int t = 0; t < TPB; ++t) {
-            const uint8_t* base = P.b + ((size_t)tile[t] * PL * 8 + c8) * 16;
-#pragma unroll
-            for (int u = 0; u < WMAX; ++u) {
-                const int pl = p_begin + s + 8 * u;
-                w[u][t] = pl < p_end ? *reinterpret_cast<const v4u*>(base + (size_t)pl * 128) : v4u{0u, 0u, 0u, 0u};
-            }
-            cs[t] = P.colscale[8 * tile[t] + c8];
+        for (int i = 0; i < RW; ++i) {
+            const int q = min(tid + 256 * (w * RW + i), CPG - 1);
+            const bool second = TPB == 2 && q >= CPT;
+            buf[i] = *reinterpret_cast<const v4u*>((second ? tb1 : tb0) + (size_t)(second ? q - CPT : q) * 16);
         }
     };
 
-    // 1. First group's weights and column scales, this thread's activation
-    // chunks and the row maxima are all requested before anything waits.
-    int g = blockIdx.x;
-    v4u wcur[WMAX][TPB];
-    float cscur[TPB];
-    load_group(g, wcur, cscur);
+    // 1. Requests go out in the order they are needed, because a wait for a
+    // load also waits for every load issued before it: this thread's
+    // activation chunks (raw) and precomputed row maxima first, then every
+    // weight chunk of the group (up to two windows) and the column scales.
     const T* x = static_cast<const T*>(P.x);
     const int chunks = KG16 * MR;
     const bool x_in_regs = chunks <= 256 * XMAX;
+    auto fast_chunk = [&](int c) {
+        const int kg = c / MR, m = c % MR;
+        return m < P.M && P.vec && kg * 16 + 16 <= P.K;
+    };
+    // (unconditional as well: a chunk this thread does not convert from
+    // registers reads the first bytes of the weights instead)
+    // No branches around these loads either: a register written on only one
+    // side of a branch makes the compiler wait for all loads at the join.
+    v4u xraw[XMAX][4];
+#pragma unroll
+    for (int j = 0; j < XMAX; ++j) {
+        const int c = tid + 256 * j;
+        const bool ok = x_in_regs && c < chunks && fast_chunk(c);
+        load16_raw(ok ? x + (size_t)(c % MR) * P.lda + (c / MR) * 16 : reinterpret_cast<const T*>(P.b), xraw[j]);
+    }
+    float pv[MR][PV];
+    const float* pin = P.part_in ? P.part_in : P.colscale;
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+#pragma unroll
+        for (int i = 0; i < PV; ++i) {
+            const int idx = tid + 256 * i;
+            const bool ok = P.part_in && m < P.M && idx < P.part_count;
+            pv[m][i] = pin[ok ? (size_t)m * P.part_count + idx : 0];  // masked at use
+        }
+    // (the empty asm statements keep the compiler from sinking these loads
+    // to their first use, which would put them behind the weight stream)
+    asm volatile("" ::: "memory");
+    v4u wa[RW], wb[RW];
+    load_window(0, wa);
+    if (NWIN > 1) load_window(1, wb);
+    float cs[TPB];
+#pragma unroll
+    for (int t = 0; t < TPB; ++t) cs[t] = P.colscale[8 * tile[t] + c8];
+    asm volatile("" ::: "memory");
+
     float xv[XMAX][16];
     float mx[MR];
 #pragma unroll
     for (int m = 0; m < MR; ++m) mx[m] = 0.0f;
     auto load_chunk = [&](int c, float (&v)[16]) {
         const int kg = c / MR, m = c % MR;
-        if (m < P.M) {
+        if (fast_chunk(c)) {
+            load16(x + (size_t)m * P.lda + kg * 16, v);
+        } else if (m < P.M) {
             const T* xr = x + (size_t)m * P.lda + kg * 16;
-            if (P.vec && kg * 16 + 16 <= P.K) {
-                load16(xr, v);
-            } else {
 #pragma unroll
-                for (int b = 0; b < 16; ++b) v[b] = (kg * 16 + b < P.K) ? to_f32(xr[b]) : 0.0f;
-            }
+            for (int b = 0; b < 16; ++b) v[b] = (kg * 16 + b < P.K) ? to_f32(xr[b]) : 0.0f;
         } else {
 #pragma unroll
             for (int b = 0; b < 16; ++b) v[b] = 0.0f;
@@ -744,7 +799,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
         for (int j = 0; j < XMAX; ++j) {
             const int c = tid + 256 * j;
             if (c < chunks) {
-                load_chunk(c, xv[j]);
+                if (fast_chunk(c))
+                    cvt16_raw(xraw[j], xv[j], T());
+                else
+                    load_chunk(c, xv[j]);  // ragged K, unaligned rows or padding rows
                 if (!P.part_in) {
                     const int m = c % MR;
                     float lm = 0.0f;
@@ -765,9 +823,14 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
     }
     if (P.part_in) {
 #pragma unroll
-        for (int m = 0; m < MR; ++m)
+        for (int m = 0; m < MR; ++m) {
+#pragma unroll
+            for (int i = 0; i < PV; ++i)
+                if (m < P.M && tid + 256 * i < P.part_count) mx[m] = fmaxf(mx[m], pv[m][i]);
             if (m < P.M)
-                for (int i = tid; i < P.part_count; i += 256) mx[m] = fmaxf(mx[m], P.part_in[(size_t)m * P.part_count + i]);
+                for (int i = tid + 256 * PV; i < P.part_count; i += 256)
+                    mx[m] = fmaxf(mx[m], P.part_in[(size_t)m * P.part_count + i]);
+        }
     }
 
     // 2. Row scales: block max through LDS (every wave reads all partials).
@@ -845,129 +908,108 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
         }
     }
 
-    // 4. Tile groups: while the dots of group g run, group g + gridDim.x is loading.
-    auto consume = [&](int (&acc)[TPB][MR], const v4u (&w)[TPB], int pl) {
-        if (BITS == 8) {
-            const int8_t* ab = sa + pl * MR * 16;
+    // 4. Dots: chunk q = tid + 256r of the group's stream.
+    int acc[TPB][MR];
 #pragma unroll
-            for (int m = 0; m < MR; ++m) {
-                const v4i a = *reinterpret_cast<const v4i*>(ab + m * 16);
+    for (int t = 0; t < TPB; ++t)
 #pragma unroll
-                for (int t = 0; t < TPB; ++t) {
-                    int v = acc[t][m];
-                    v = __builtin_amdgcn_sdot4(a.x, (int)w[t].x, v, false);
-                    v = __builtin_amdgcn_sdot4(a.y, (int)w[t].y, v, false);
-                    v = __builtin_amdgcn_sdot4(a.z, (int)w[t].z, v, false);
-                    v = __builtin_amdgcn_sdot4(a.w, (int)w[t].w, v, false);
-                    acc[t][m] = v;
+        for (int m = 0; m < MR; ++m) acc[t][m] = 0;
+    auto consume = [&](int w, const v4u (&buf)[RW]) {
+#pragma unroll
+        for (int i = 0; i < RW; ++i) {
+            const int q = tid + 256 * (w * RW + i);
+            if (q >= CPG) continue;
+            const bool second = TPB == 2 && q >= CPT;
+            const int pl = (second ? q - CPT : q) >> 3;
+            const v4u wv = buf[i];
+            int d[MR];
+            if (BITS == 8) {
+                const int8_t* ab = sa + pl * MR * 16;
+#pragma unroll
+                for (int m = 0; m < MR; ++m) {
+                    const v4i a = *reinterpret_cast<const v4i*>(ab + m * 16);
+                    int v = __builtin_amdgcn_sdot4(a.x, (int)wv.x, 0, false);
+                    v = __builtin_amdgcn_sdot4(a.y, (int)wv.y, v, false);
+                    v = __builtin_amdgcn_sdot4(a.z, (int)wv.z, v, false);
+                    d[m] = __builtin_amdgcn_sdot4(a.w, (int)wv.w, v, false);
+                }
+            } else {
+                const int kga = 4 * (pl >> 1) + (pl & 1);
+                const int8_t* aa = sa + kga * MR * 16;
+                const int8_t* ab = sa + (kga + 2) * MR * 16;
+                const v4u lo = wv & 0x0F0F0F0Fu, hi = (wv >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+                for (int m = 0; m < MR; ++m) {
+                    const v4i x0 = *reinterpret_cast<const v4i*>(aa + m * 16);
+                    const v4i x1 = *reinterpret_cast<const v4i*>(ab + m * 16);
+                    int v = __builtin_amdgcn_sdot4(x0.x, (int)lo.x, 0, false);
+                    v = __builtin_amdgcn_sdot4(x0.y, (int)lo.y, v, false);
+                    v = __builtin_amdgcn_sdot4(x0.z, (int)lo.z, v, false);
+                    v = __builtin_amdgcn_sdot4(x0.w, (int)lo.w, v, false);
+                    v = __builtin_amdgcn_sdot4(x1.x, (int)hi.x, v, false);
+                    v = __builtin_amdgcn_sdot4(x1.y, (int)hi.y, v, false);
+                    v = __builtin_amdgcn_sdot4(x1.z, (int)hi.z, v, false);
+                    d[m] = __builtin_amdgcn_sdot4(x1.w, (int)hi.w, v, false);
                 }
             }
-        } else {
-            const int kga = 4 * (pl >> 1) + (pl & 1);
-            const int8_t* aa = sa + kga * MR * 16;
-            const int8_t* ab = sa + (kga + 2) * MR * 16;
-            v4u lo[TPB], hi[TPB];
-#pragma unroll
-            for (int t = 0; t < TPB; ++t) {
-                lo[t] = w[t] & 0x0F0F0F0Fu;
-                hi[t] = (w[t] >> 4) & 0x0F0F0F0Fu;
-            }
 #pragma unroll
             for (int m = 0; m < MR; ++m) {
-                const v4i x0 = *reinterpret_cast<const v4i*>(aa + m * 16);
-                const v4i x1 = *reinterpret_cast<const v4i*>(ab + m * 16);
-#pragma unroll
-                for (int t = 0; t < TPB; ++t) {
-                    int v = acc[t][m];
-                    v = __builtin_amdgcn_sdot4(x0.x, (int)lo[t].x, v, false);
-                    v = __builtin_amdgcn_sdot4(x0.y, (int)lo[t].y, v, false);
-                    v = __builtin_amdgcn_sdot4(x0.z, (int)lo[t].z, v, false);
-                    v = __builtin_amdgcn_sdot4(x0.w, (int)lo[t].w, v, false);
-                    v = __builtin_amdgcn_sdot4(x1.x, (int)hi[t].x, v, false);
-                    v = __builtin_amdgcn_sdot4(x1.y, (int)hi[t].y, v, false);
-                    v = __builtin_amdgcn_sdot4(x1.z, (int)hi[t].z, v, false);
-                    v = __builtin_amdgcn_sdot4(x1.w, (int)hi[t].w, v, false);
-                    acc[t][m] = v;
-                }
+                if (second)
+                    acc[TPB - 1][m] += d[m];
+                else
+                    acc[0][m] += d[m];
             }
         }
     };
+    // Windows ping-pong between the two register sets (longer K only).
+    for (int w = 0; w < NWIN; w += 2) {
+        consume(w, wa);
+        if (w + 2 < NWIN) load_window(w + 2, wa);
+        if (w + 1 < NWIN) {
+            consume(w + 1, wb);
+            if (w + 3 < NWIN) load_window(w + 3, wb);
+        }
+    }
 
-    for (int it = 0; g < groups; ++it) {
-        const int gn = g + gridDim.x;
-        v4u wnext[WMAX][TPB];
-        float csnext[TPB];
-        if (gn < groups) load_group(gn, wnext, csnext);
-        int tile[TPB];
-        tiles_of(g, tile);
-        int acc[TPB][MR];
+    // 5. Reduce over threads of the same column: shuffles within a wave, LDS
+    // across waves; wave 0 finishes the 8 columns.
 #pragma unroll
-        for (int t = 0; t < TPB; ++t)
+    for (int t = 0; t < TPB; ++t)
 #pragma unroll
-            for (int m = 0; m < MR; ++m) acc[t][m] = 0;
-#pragma unroll
-        for (int u = 0; u < WMAX; ++u) {
-            const int pl = p_begin + s + 8 * u;
-            if (pl < p_end) consume(acc, wcur[u], pl);
+        for (int m = 0; m < MR; ++m) {
+            int v = acc[t][m];
+            v += __shfl_xor(v, 8);
+            v += __shfl_xor(v, 16);
+            v += __shfl_xor(v, 32);
+            if (lane < 8) red[wave][t][m][c8] = v;
         }
-        // planes beyond the register window (long K)
-        for (int pl = p_begin + s + 8 * WMAX; pl < p_end; pl += 8) {
-            v4u w[TPB];
+    __syncthreads();
+    if (wave == 0) {
 #pragma unroll
-            for (int t = 0; t < TPB; ++t)
-                w[t] = *reinterpret_cast<const v4u*>(P.b + ((size_t)tile[t] * PL * 8 + c8) * 16 + (size_t)pl * 128);
-            consume(acc, w, pl);
-        }
-        // reduce over s (shuffles) and waves (LDS, double-buffered); wave 0 stores
-        const int rb = it & 1;
+        for (int m = 0; m < MR; ++m) {
+            const bool row_ok = m < P.M;
+            float y[TPB];
 #pragma unroll
-        for (int t = 0; t < TPB; ++t)
-#pragma unroll
-            for (int m = 0; m < MR; ++m) {
-                int v = acc[t][m];
-                v += __shfl_xor(v, 8);
-                v += __shfl_xor(v, 16);
-                v += __shfl_xor(v, 32);
-                if (s == 0) red[rb][wave][t][m][c8] = v;
+            for (int t = 0; t < TPB; ++t) {
+                const int tot = red[0][t][m][c8] + red[1][t][m][c8] + red[2][t][m][c8] + red[3][t][m][c8];
+                y[t] = ((float)(tot - corr[m]) * scale[m]) * cs[t];
             }
-        __syncthreads();
-        if (wave == 0) {
-#pragma unroll
-            for (int m = 0; m < MR; ++m) {
-                const bool row_ok = m < P.M;
-                float y[TPB];
-#pragma unroll
-                for (int t = 0; t < TPB; ++t) {
-                    const int tot =
-                        red[rb][0][t][m][c8] + red[rb][1][t][m][c8] + red[rb][2][t][m][c8] + red[rb][3][t][m][c8];
-                    y[t] = ((float)(tot - corr[m]) * scale[m]) * cscur[t];
-                }
-                const int p = 8 * tile[0] + c8;
-                if (EPI == EPI_PLAIN) {
-                    if (lane < 8 && row_ok && p < P.N)
-                        store_out(P.c, P.c_type, (size_t)m * P.ldc + orig_col(p, P.half), y[0]);
-                } else {
-                    const float o = hm_swiglu(y[0], y[TPB - 1]);
-                    if (lane < 8 && row_ok && p < P.N)
-                        store_out(P.c, P.c_type, (size_t)m * P.ldc + ((p >> 6) << 5) + (p & 31), o);
-                    if (EPI == EPI_SWIGLU_MAX) {
-                        float mxo = (lane < 8 && p < P.N) ? fabsf(o) : 0.0f;
-                        mxo = fmaxf(mxo, __shfl_xor(mxo, 1));
-                        mxo = fmaxf(mxo, __shfl_xor(mxo, 2));
-                        mxo = fmaxf(mxo, __shfl_xor(mxo, 4));
-                        if (lane == 0) P.part_out[(size_t)m * groups + g] = row_ok ? mxo : 0.0f;
-                    }
+            const int p = 8 * tile[0] + c8;
+            if (EPI == EPI_PLAIN) {
+                if (lane < 8 && row_ok && p < P.N)
+                    store_out(P.c, P.c_type, (size_t)m * P.ldc + orig_col(p, P.half), y[0]);
+            } else {
+                const float o = hm_swiglu(y[0], y[TPB - 1]);
+                if (lane < 8 && row_ok && p < P.N)
+                    store_out(P.c, P.c_type, (size_t)m * P.ldc + ((p >> 6) << 5) + (p & 31), o);
+                if (EPI == EPI_SWIGLU_MAX) {
+                    float mxo = (lane < 8 && p < P.N) ? fabsf(o) : 0.0f;
+                    mxo = fmaxf(mxo, __shfl_xor(mxo, 1));
+                    mxo = fmaxf(mxo, __shfl_xor(mxo, 2));
+                    mxo = fmaxf(mxo, __shfl_xor(mxo, 4));
+                    if (lane == 0) P.part_out[(size_t)m * groups + g] = row_ok ? mxo : 0.0f;
                 }
             }
-        }
-        g = gn;
-        if (g < groups) {
-#pragma unroll
-            for (int u = 0; u < WMAX; ++u)
-#pragma unroll
-                for (int t = 0; t < TPB; ++t) wcur[u][t] = wnext[u][t];
-#pragma unroll
-            for (int t = 0; t < TPB; ++t) cscur[t] = csnext[t];
         }
     }
 }
