@@ -417,35 +417,54 @@ static void launch_gemm(int v, const GemmParams& G, int grid, hipStream_t s) {
     }
 }
 
+template <typename T, int MR, int BITS, int EPI, bool PREQ>
+static void launch_gemv_w(const GemvParams& V, int groups, size_t lds, hipStream_t s) {
+    // Register windows sized to the group (rounds of 256 16-byte chunks), so
+    // no registers hold chunks past its end: fewer registers, more resident blocks.
+    const int planes = BITS == 8 ? V.K_pad / 16 : V.K_pad / 32;
+    const int rounds = (planes * 8 * (EPI == EPI_PLAIN ? 1 : 2) + 255) / 256;
+    if (rounds <= 4)
+        hipLaunchKernelGGL((gemv_kernel<T, MR, BITS, EPI, 4, 1, PREQ>), dim3(groups), dim3(256), lds, s, V);
+    else if (rounds <= 6)
+        hipLaunchKernelGGL((gemv_kernel<T, MR, BITS, EPI, 6, 1, PREQ>), dim3(groups), dim3(256), lds, s, V);
+    else if (rounds <= 8)
+        hipLaunchKernelGGL((gemv_kernel<T, MR, BITS, EPI, 8, 1, PREQ>), dim3(groups), dim3(256), lds, s, V);
+    else
+        hipLaunchKernelGGL((gemv_kernel<T, MR, BITS, EPI, 8, 2, PREQ>), dim3(groups), dim3(256), lds, s, V);
+}
+
 template <typename T, int MR, int BITS, int EPI>
-static void launch_gemv_mr(const GemvParams& V, int groups, size_t lds, hipStream_t s) {
-    hipLaunchKernelGGL((gemv_kernel<T, MR, BITS, EPI>), dim3(groups), dim3(256), lds, s, V);
+static void launch_gemv_mr(const GemvParams& V, int groups, size_t lds, hipStream_t s, bool preq) {
+    if (preq)
+        launch_gemv_w<float, MR, BITS, EPI, true>(V, groups, lds, s);  // activations unused
+    else
+        launch_gemv_w<T, MR, BITS, EPI, false>(V, groups, lds, s);
 }
 
 template <typename T, int BITS, int EPI>
-static void launch_gemv(int mr, const GemvParams& V, int grid, size_t lds, hipStream_t s) {
+static void launch_gemv(int mr, const GemvParams& V, int grid, size_t lds, hipStream_t s, bool preq) {
     switch (mr) {
         case 1:
-            launch_gemv_mr<T, 1, BITS, EPI>(V, grid, lds, s);
+            launch_gemv_mr<T, 1, BITS, EPI>(V, grid, lds, s, preq);
             break;
         case 2:
-            launch_gemv_mr<T, 2, BITS, EPI>(V, grid, lds, s);
+            launch_gemv_mr<T, 2, BITS, EPI>(V, grid, lds, s, preq);
             break;
         case 4:
-            launch_gemv_mr<T, 4, BITS, EPI>(V, grid, lds, s);
+            launch_gemv_mr<T, 4, BITS, EPI>(V, grid, lds, s, preq);
             break;
         default:
-            launch_gemv_mr<T, 8, BITS, EPI>(V, grid, lds, s);
+            launch_gemv_mr<T, 8, BITS, EPI>(V, grid, lds, s, preq);
             break;
     }
 }
 
 template <typename T, int BITS>
-static void launch_gemv_epi(int epi, int mr, const GemvParams& V, int grid, size_t lds, hipStream_t s) {
+static void launch_gemv_epi(int epi, int mr, const GemvParams& V, int grid, size_t lds, hipStream_t s, bool preq) {
     if (epi == EPI_PLAIN)
-        launch_gemv<T, BITS, EPI_PLAIN>(mr, V, grid, lds, s);
+        launch_gemv<T, BITS, EPI_PLAIN>(mr, V, grid, lds, s, preq);
     else
-        launch_gemv<T, BITS, EPI_SWIGLU_MAX>(mr, V, grid, lds, s);
+        launch_gemv<T, BITS, EPI_SWIGLU_MAX>(mr, V, grid, lds, s, preq);
 }
 
 int enqueue_linear(Workspace* ws, const Weights* w, const void* x, int x_type, long lda, int rows, int rule,
@@ -479,19 +498,26 @@ int enqueue_linear(Workspace* ws, const Weights* w, const void* x, int x_type, l
         V.M_alloc = ws->M_alloc;
         const int grid = epi == EPI_PLAIN ? g.N_pad / 8 : g.N_pad / 16;
         const size_t lds = (size_t)g.K_pad * p.mr;
+        // Rows the kernel cannot quantize from registers (unaligned or ragged
+        // rows, or more than GEMV_XMAX chunks per thread) are quantized first.
+        const bool preq = !V.vec || (g.K_pad / 16) * p.mr > 256 * GEMV_XMAX;
+        if (preq) {
+            int rc = enqueue_quant(ws, x, x_type, lda, rows, rule, in_max, nullptr, s);
+            if (rc != RK_NPU_OK) return rc;
+        }
         char name[64];
         std::snprintf(name, sizeof(name), "gemv<mr=%d,w%d,epi=%d>", p.mr, g.bits, epi);
         const int slot = prof_begin(s, 0, g.bits, epi, rows, g.K, g.N, name);
         if (x_type == DT_F32) {
             if (g.bits == 8)
-                launch_gemv_epi<float, 8>(epi, p.mr, V, grid, lds, s);
+                launch_gemv_epi<float, 8>(epi, p.mr, V, grid, lds, s, preq);
             else
-                launch_gemv_epi<float, 4>(epi, p.mr, V, grid, lds, s);
+                launch_gemv_epi<float, 4>(epi, p.mr, V, grid, lds, s, preq);
         } else {
             if (g.bits == 8)
-                launch_gemv_epi<__half, 8>(epi, p.mr, V, grid, lds, s);
+                launch_gemv_epi<__half, 8>(epi, p.mr, V, grid, lds, s, preq);
             else
-                launch_gemv_epi<__half, 4>(epi, p.mr, V, grid, lds, s);
+                launch_gemv_epi<__half, 4>(epi, p.mr, V, grid, lds, s, preq);
         }
         prof_end(slot, s);
         if (out_max) *out_max = RowMax{ws->partmax, grid};

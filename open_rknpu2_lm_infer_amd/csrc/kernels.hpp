@@ -659,13 +659,17 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_kernel(GemmParams P) {
 // bytes are a flat stream of 16-byte chunks (chunk q = plane q/8, column q%8
 // of its tile); thread tid takes chunks tid + 256r, so every wave load is
 // 1 KB contiguous and the column of a thread is fixed (tid % 8). All chunks
-// (up to two windows of RW rounds) are requested first; the block then
+// (up to NW register windows of RW rounds each) are requested first; the block then
 // quantizes the activation rows itself (row max from x or from precomputed
 // partial maxima, the dense or MoE rule) into LDS while they are in flight.
 // Dot products use v_dot4_i32_i8; partials reduce over threads of the same
 // column with cross-lane shuffles and over waves through LDS. SwiGLU+max
 // writes one partial max per block.
 // ---------------------------------------------------------------------------
+// Activation chunks (16 elements) each GEMV thread quantizes from registers;
+// rows with K_pad/16 * rows above 256 * GEMV_XMAX are quantized beforehand.
+constexpr int GEMV_XMAX = 3;
+
 struct GemvParams {
     const void* x;
     long lda;
@@ -680,7 +684,10 @@ struct GemvParams {
     long ldc;
     int c_type;
     int M, K, N, K_pad, N_pad, half;
-    int8_t* diag_codes;   // block 0 leaves the quantized rows here ([K_pad/16][M_alloc][16])
+    // Quantized rows [K_pad/16][M_alloc][16] with their scales and code sums:
+    // written by block 0 when the kernel quantizes (diagnostics), read when
+    // the rows were quantized beforehand (PREQ).
+    int8_t* diag_codes;
     float* diag_scale;
     int* diag_rowsum;
     int M_alloc;
@@ -692,13 +699,12 @@ __device__ __forceinline__ int wave_sum(int v) {
     return v;
 }
 
-template <typename T, int MR, int BITS, int EPI>
+template <typename T, int MR, int BITS, int EPI, int RW, int NW, bool PREQ>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
     extern __shared__ __attribute__((aligned(16))) int8_t sa[];  // [K_pad/16][MR][16]
     constexpr int TPB = (EPI == EPI_PLAIN) ? 1 : 2;
-    constexpr int RW = 8;     // rounds (16-byte chunks per thread) per window
-    constexpr int XMAX = 3;   // 16-element activation chunks per thread in registers
-    constexpr int PV = 5;     // precomputed row-max partials per thread in registers
+    constexpr int XMAX = GEMV_XMAX;  // 16-element activation chunks per thread
+    constexpr int PV = 5;            // precomputed row-max partials per thread
     __shared__ float s_red[4][MR];
     __shared__ int s_isum[4][MR];
     __shared__ int red[4][TPB][MR][8];
@@ -709,6 +715,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
     const int CPT = PL * 8;                  // chunks per tile
     const int CPG = CPT * TPB;               // chunks per group
     const int NWIN = (CPG + 256 * RW - 1) / (256 * RW);
+    const int chunks = KG16 * MR;            // activation chunks (<= 256 * XMAX unless PREQ)
     const int g = blockIdx.x;
     const int groups = gridDim.x;
 
@@ -722,189 +729,187 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
     }
     const uint8_t* tb0 = P.b + (size_t)tile[0] * CPT * 16;
     const uint8_t* tb1 = P.b + (size_t)tile[TPB - 1] * CPT * 16;
-    // Loads are unconditional (a chunk past the group re-reads its last one
-    // and is skipped by the dots), so the compiler's wait counts are exact:
-    // a load under a branch makes every later wait assume it may be missing.
-    auto load_window = [&](int w, v4u (&buf)[RW]) {
+
+    // 1. Requests go out in the order they are needed, because a wait for a
+    // load also waits for every load issued before it: this thread's
+    // activation chunks (raw) or code chunks and the precomputed row maxima
+    // first, then every weight chunk of the group (up to NW windows) and the
+    // column scales. No load sits under a branch (addresses are clamped and
+    // results masked at use): a load that may be skipped makes every later
+    // wait of the compiler assume it was, and a register written on only one
+    // side of a branch makes it wait for everything at the join.
+    // A masked-off load reads bytes this thread loads anyway (its first
+    // weight chunk or its column scale), never one shared address: thousands
+    // of requests to one line would queue on one cache channel.
+    const uint8_t* own = tb0 + (size_t)min(tid, CPT - 4) * 16;  // 64 readable bytes (CPT >= 16)
+    v4u xraw[XMAX][4];
+    const T* x = static_cast<const T*>(P.x);
+#pragma unroll
+    for (int j = 0; j < XMAX; ++j) {
+        const int c = tid + 256 * j, kg = c / MR, m = c % MR;
+        if (PREQ) {
+            const bool ok = c < chunks && m < P.M;
+            xraw[j][0] = *reinterpret_cast<const v4u*>(ok ? P.diag_codes + ((size_t)kg * P.M_alloc + m) * 16
+                                                          : reinterpret_cast<const int8_t*>(own));
+        } else {
+            const bool ok = c < chunks && m < P.M && kg * 16 < P.K;
+            load16_raw(ok ? x + (size_t)m * P.lda + kg * 16 : reinterpret_cast<const T*>(own), xraw[j]);
+        }
+    }
+    float pv[MR][PV];
+    const float* own_cs = P.colscale + 8 * tile[0] + c8;
+    if (!PREQ) {
+#pragma unroll
+        for (int m = 0; m < MR; ++m)
+#pragma unroll
+            for (int i = 0; i < PV; ++i) {
+                const int idx = tid + 256 * i;
+                const bool ok = P.part_in && m < P.M && idx < P.part_count;
+                pv[m][i] = *(ok ? P.part_in + (size_t)m * P.part_count + idx : own_cs);  // masked at use
+            }
+    }
+    // (the empty asm statements keep the compiler from sinking these loads
+    // to their first use, which would put them behind the weight stream)
+    asm volatile("" ::: "memory");
+    auto load_window = [&](int w, auto& buf) {
 #pragma unroll
         for (int i = 0; i < RW; ++i) {
-            const int q = min(tid + 256 * (w * RW + i), CPG - 1);
+            const int q = (tid + 256 * (w * RW + i)) % CPG;  // past the group: a re-read, skipped
             const bool second = TPB == 2 && q >= CPT;
             buf[i] = *reinterpret_cast<const v4u*>((second ? tb1 : tb0) + (size_t)(second ? q - CPT : q) * 16);
         }
     };
-
-    // 1. Requests go out in the order they are needed, because a wait for a
-    // load also waits for every load issued before it: this thread's
-    // activation chunks (raw) and precomputed row maxima first, then every
-    // weight chunk of the group (up to two windows) and the column scales.
-    const T* x = static_cast<const T*>(P.x);
-    const int chunks = KG16 * MR;
-    const bool x_in_regs = chunks <= 256 * XMAX;
-    auto fast_chunk = [&](int c) {
-        const int kg = c / MR, m = c % MR;
-        return m < P.M && P.vec && kg * 16 + 16 <= P.K;
-    };
-    // (unconditional as well: a chunk this thread does not convert from
-    // registers reads the first bytes of the weights instead)
-    // No branches around these loads either: a register written on only one
-    // side of a branch makes the compiler wait for all loads at the join.
-    v4u xraw[XMAX][4];
-#pragma unroll
-    for (int j = 0; j < XMAX; ++j) {
-        const int c = tid + 256 * j;
-        const bool ok = x_in_regs && c < chunks && fast_chunk(c);
-        load16_raw(ok ? x + (size_t)(c % MR) * P.lda + (c / MR) * 16 : reinterpret_cast<const T*>(P.b), xraw[j]);
-    }
-    float pv[MR][PV];
-    const float* pin = P.part_in ? P.part_in : P.colscale;
-#pragma unroll
-    for (int m = 0; m < MR; ++m)
-#pragma unroll
-        for (int i = 0; i < PV; ++i) {
-            const int idx = tid + 256 * i;
-            const bool ok = P.part_in && m < P.M && idx < P.part_count;
-            pv[m][i] = pin[ok ? (size_t)m * P.part_count + idx : 0];  // masked at use
-        }
-    // (the empty asm statements keep the compiler from sinking these loads
-    // to their first use, which would put them behind the weight stream)
-    asm volatile("" ::: "memory");
-    v4u wa[RW], wb[RW];
+    v4u wa[RW], wb[NW == 2 ? RW : 1];
     load_window(0, wa);
-    if (NWIN > 1) load_window(1, wb);
+    if (NW == 2 && NWIN > 1) load_window(1, wb);
     float cs[TPB];
 #pragma unroll
     for (int t = 0; t < TPB; ++t) cs[t] = P.colscale[8 * tile[t] + c8];
     asm volatile("" ::: "memory");
 
-    float xv[XMAX][16];
-    float mx[MR];
-#pragma unroll
-    for (int m = 0; m < MR; ++m) mx[m] = 0.0f;
-    auto load_chunk = [&](int c, float (&v)[16]) {
-        const int kg = c / MR, m = c % MR;
-        if (fast_chunk(c)) {
-            load16(x + (size_t)m * P.lda + kg * 16, v);
-        } else if (m < P.M) {
-            const T* xr = x + (size_t)m * P.lda + kg * 16;
-#pragma unroll
-            for (int b = 0; b < 16; ++b) v[b] = (kg * 16 + b < P.K) ? to_f32(xr[b]) : 0.0f;
-        } else {
-#pragma unroll
-            for (int b = 0; b < 16; ++b) v[b] = 0.0f;
-        }
-    };
-    if (x_in_regs) {
+    float scale[MR];
+    int corr[MR];
+    if (PREQ) {
+        // 2-3. Rows quantized beforehand: codes to LDS, scales and sums from HBM.
 #pragma unroll
         for (int j = 0; j < XMAX; ++j) {
-            const int c = tid + 256 * j;
-            if (c < chunks) {
-                if (fast_chunk(c))
-                    cvt16_raw(xraw[j], xv[j], T());
-                else
-                    load_chunk(c, xv[j]);  // ragged K, unaligned rows or padding rows
-                if (!P.part_in) {
-                    const int m = c % MR;
-                    float lm = 0.0f;
-#pragma unroll
-                    for (int b = 0; b < 16; ++b) lm = fmaxf(lm, fabsf(xv[j][b]));
-#pragma unroll
-                    for (int r = 0; r < MR; ++r) mx[r] = (r == m) ? fmaxf(mx[r], lm) : mx[r];
-                }
-            }
+            const int c = tid + 256 * j, m = c % MR;
+            if (c < chunks) *reinterpret_cast<v4u*>(sa + c * 16) = (m < P.M) ? xraw[j][0] : v4u{0u, 0u, 0u, 0u};
         }
-    } else if (!P.part_in) {
-#pragma unroll
-        for (int m = 0; m < MR; ++m)
-            if (m < P.M) {
-                const T* xr = x + (size_t)m * P.lda;
-                for (int k = tid; k < P.K; k += 256) mx[m] = fmaxf(mx[m], fabsf(to_f32(xr[k])));
-            }
-    }
-    if (P.part_in) {
+        for (int c = tid + 256 * XMAX; c < chunks; c += 256) {  // long rows: after the weights
+            const int m = c % MR;
+            *reinterpret_cast<v4u*>(sa + c * 16) =
+                (m < P.M) ? *reinterpret_cast<const v4u*>(P.diag_codes + ((size_t)(c / MR) * P.M_alloc + m) * 16)
+                          : v4u{0u, 0u, 0u, 0u};
+        }
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
-#pragma unroll
-            for (int i = 0; i < PV; ++i)
-                if (m < P.M && tid + 256 * i < P.part_count) mx[m] = fmaxf(mx[m], pv[m][i]);
-            if (m < P.M)
-                for (int i = tid + 256 * PV; i < P.part_count; i += 256)
-                    mx[m] = fmaxf(mx[m], P.part_in[(size_t)m * P.part_count + i]);
+            scale[m] = m < P.M ? P.diag_scale[m] : 1.0f;
+            corr[m] = (BITS == 4 && m < P.M) ? 8 * P.diag_rowsum[m] : 0;
         }
-    }
-
-    // 2. Row scales: block max through LDS (every wave reads all partials).
+        wait_lgkmcnt0();
+        __builtin_amdgcn_s_barrier();
+    } else {
+        // 2. Row maxima (from the activations or the precomputed partials),
+        // block max through LDS, row scales.
+        float mx[MR];
 #pragma unroll
-    for (int m = 0; m < MR; ++m) {
-        const float v = wave_max(mx[m]);
-        if (lane == 0) s_red[wave][m] = v;
-    }
-    __syncthreads();
-    float scale[MR], inv[MR];
+        for (int m = 0; m < MR; ++m) mx[m] = 0.0f;
+        auto chunk_vals = [&](int j, float (&v)[16]) {
+            const int c = tid + 256 * j, kg = c / MR, m = c % MR;
+            const bool ok = c < chunks && m < P.M && kg * 16 < P.K;
+            cvt16_raw(xraw[j], v, T());
 #pragma unroll
-    for (int m = 0; m < MR; ++m) {
-        const float v = fmaxf(fmaxf(s_red[0][m], s_red[1][m]), fmaxf(s_red[2][m], s_red[3][m]));
-        if (P.rule == QUANT_DENSE)
-            scale[m] = (v == 0.0f) ? 1.0f : fmaxf(v / 127.0f, FLT_MIN);
-        else
-            scale[m] = (v == 0.0f) ? 1.0f : v / 127.0f;
-        inv[m] = 1.0f / scale[m];
-    }
-
-    // 3. Quantize into LDS, chunk c = (k16 group, row); once per block.
-    int psum[MR];
+            for (int b = 0; b < 16; ++b) v[b] = ok ? v[b] : 0.0f;
+        };
+        if (P.part_in) {
 #pragma unroll
-    for (int m = 0; m < MR; ++m) psum[m] = 0;
-    auto quantize_chunk = [&](int c, const float (&v)[16]) {
-        const int m = c % MR;
-        float iv = inv[0];
+            for (int m = 0; m < MR; ++m) {
 #pragma unroll
-        for (int r = 1; r < MR; ++r) iv = (r == m) ? inv[r] : iv;
-        unsigned packed[4] = {0u, 0u, 0u, 0u};
-        int sum = 0;
+                for (int i = 0; i < PV; ++i)
+                    if (m < P.M && tid + 256 * i < P.part_count) mx[m] = fmaxf(mx[m], pv[m][i]);
+                if (m < P.M)
+                    for (int i = tid + 256 * PV; i < P.part_count; i += 256)
+                        mx[m] = fmaxf(mx[m], P.part_in[(size_t)m * P.part_count + i]);
+            }
+        } else {
 #pragma unroll
-        for (int b = 0; b < 16; ++b) {
-            float q = v[b] * iv;
-            q = (P.rule == QUANT_DENSE) ? roundf(q) : __builtin_rintf(q);
-            q = fminf(fmaxf(q, -127.0f), 127.0f);
-            const int qi = (int)q;
-            sum += qi;
-            packed[b >> 2] |= ((unsigned)qi & 0xffu) << ((b & 3) * 8);
+            for (int j = 0; j < XMAX; ++j) {
+                if (tid + 256 * j >= chunks) continue;  // (pure arithmetic: no load under the branch)
+                float v[16];
+                chunk_vals(j, v);
+                float lm = 0.0f;
+#pragma unroll
+                for (int b = 0; b < 16; ++b) lm = fmaxf(lm, fabsf(v[b]));
+                const int m = (tid + 256 * j) % MR;
+#pragma unroll
+                for (int r = 0; r < MR; ++r) mx[r] = (r == m) ? fmaxf(mx[r], lm) : mx[r];
+            }
         }
 #pragma unroll
-        for (int r = 0; r < MR; ++r) psum[r] += (r == m) ? sum : 0;
-        *reinterpret_cast<v4u*>(sa + c * 16) = v4u{packed[0], packed[1], packed[2], packed[3]};
-    };
-    if (x_in_regs) {
+        for (int m = 0; m < MR; ++m) {
+            const float v = wave_max(mx[m]);
+            if (lane == 0) s_red[wave][m] = v;
+        }
+        wait_lgkmcnt0();
+        __builtin_amdgcn_s_barrier();
+        float inv[MR];
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            const float v = fmaxf(fmaxf(s_red[0][m], s_red[1][m]), fmaxf(s_red[2][m], s_red[3][m]));
+            if (P.rule == QUANT_DENSE)
+                scale[m] = (v == 0.0f) ? 1.0f : fmaxf(v / 127.0f, FLT_MIN);
+            else
+                scale[m] = (v == 0.0f) ? 1.0f : v / 127.0f;
+            inv[m] = 1.0f / scale[m];
+        }
+
+        // 3. Quantize this thread's chunks into LDS, chunk c = (k16 group, row).
+        int psum[MR];
+#pragma unroll
+        for (int m = 0; m < MR; ++m) psum[m] = 0;
 #pragma unroll
         for (int j = 0; j < XMAX; ++j) {
-            const int c = tid + 256 * j;
-            if (c < chunks) quantize_chunk(c, xv[j]);
-        }
-    } else {
-        for (int c = tid; c < chunks; c += 256) {
+            const int c = tid + 256 * j, m = c % MR;
+            if (c >= chunks) continue;
             float v[16];
-            load_chunk(c, v);
-            quantize_chunk(c, v);
+            chunk_vals(j, v);
+            float iv = inv[0];
+#pragma unroll
+            for (int r = 1; r < MR; ++r) iv = (r == m) ? inv[r] : iv;
+            unsigned packed[4] = {0u, 0u, 0u, 0u};
+            int sum = 0;
+#pragma unroll
+            for (int b = 0; b < 16; ++b) {
+                float q = v[b] * iv;
+                q = (P.rule == QUANT_DENSE) ? roundf(q) : __builtin_rintf(q);
+                q = fminf(fmaxf(q, -127.0f), 127.0f);
+                const int qi = (int)q;
+                sum += qi;
+                packed[b >> 2] |= ((unsigned)qi & 0xffu) << ((b & 3) * 8);
+            }
+#pragma unroll
+            for (int r = 0; r < MR; ++r) psum[r] += (r == m) ? sum : 0;
+            *reinterpret_cast<v4u*>(sa + c * 16) = v4u{packed[0], packed[1], packed[2], packed[3]};
         }
-    }
 #pragma unroll
-    for (int m = 0; m < MR; ++m) {
-        const int v = wave_sum(psum[m]);
-        if (lane == 0) s_isum[wave][m] = v;
-    }
-    __syncthreads();
-    int corr[MR];
+        for (int m = 0; m < MR; ++m) {
+            const int v = wave_sum(psum[m]);
+            if (lane == 0) s_isum[wave][m] = v;
+        }
+        wait_lgkmcnt0();
+        __builtin_amdgcn_s_barrier();
 #pragma unroll
-    for (int m = 0; m < MR; ++m)
-        corr[m] = (BITS == 4) ? 8 * (s_isum[0][m] + s_isum[1][m] + s_isum[2][m] + s_isum[3][m]) : 0;
-    if (blockIdx.x == 0 && P.diag_codes) {
-        for (int c = tid; c < chunks; c += 256)
-            *reinterpret_cast<v4u*>(P.diag_codes + ((size_t)(c / MR) * P.M_alloc + c % MR) * 16) =
-                *reinterpret_cast<const v4u*>(sa + c * 16);
-        if (tid < MR && tid < P.M) {
-            P.diag_scale[tid] = scale[tid];
-            P.diag_rowsum[tid] = s_isum[0][tid] + s_isum[1][tid] + s_isum[2][tid] + s_isum[3][tid];
+        for (int m = 0; m < MR; ++m)
+            corr[m] = (BITS == 4) ? 8 * (s_isum[0][m] + s_isum[1][m] + s_isum[2][m] + s_isum[3][m]) : 0;
+        if (blockIdx.x == 0 && P.diag_codes) {
+            for (int c = tid; c < chunks; c += 256)
+                *reinterpret_cast<v4u*>(P.diag_codes + ((size_t)(c / MR) * P.M_alloc + c % MR) * 16) =
+                    *reinterpret_cast<const v4u*>(sa + c * 16);
+            if (tid < MR && tid < P.M) {
+                P.diag_scale[tid] = scale[tid];
+                P.diag_rowsum[tid] = s_isum[0][tid] + s_isum[1][tid] + s_isum[2][tid] + s_isum[3][tid];
+            }
         }
     }
 
@@ -914,7 +919,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
     for (int t = 0; t < TPB; ++t)
 #pragma unroll
         for (int m = 0; m < MR; ++m) acc[t][m] = 0;
-    auto consume = [&](int w, const v4u (&buf)[RW]) {
+    auto consume = [&](int w, const auto& buf) {
 #pragma unroll
         for (int i = 0; i < RW; ++i) {
             const int q = tid + 256 * (w * RW + i);
@@ -961,13 +966,21 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
             }
         }
     };
-    // Windows ping-pong between the two register sets (longer K only).
-    for (int w = 0; w < NWIN; w += 2) {
-        consume(w, wa);
-        if (w + 2 < NWIN) load_window(w + 2, wa);
-        if (w + 1 < NWIN) {
-            consume(w + 1, wb);
-            if (w + 3 < NWIN) load_window(w + 3, wb);
+    // Windows ping-pong between the two register sets (longer K only); with
+    // one set, a further window is requested after the previous one is used.
+    if constexpr (NW == 2) {
+        for (int w = 0; w < NWIN; w += 2) {
+            consume(w, wa);
+            if (w + 2 < NWIN) load_window(w + 2, wa);
+            if (w + 1 < NWIN) {
+                consume(w + 1, wb);
+                if (w + 3 < NWIN) load_window(w + 3, wb);
+            }
+        }
+    } else {
+        for (int w = 0; w < NWIN; ++w) {
+            if (w > 0) load_window(w, wa);
+            consume(w, wa);
         }
     }
 
@@ -983,7 +996,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
             v += __shfl_xor(v, 32);
             if (lane < 8) red[wave][t][m][c8] = v;
         }
-    __syncthreads();
+    wait_lgkmcnt0();
+    __builtin_amdgcn_s_barrier();
     if (wave == 0) {
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
