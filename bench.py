@@ -298,7 +298,7 @@ def run_prefill(torch, ctx, rows, steps, warmup):
            "value": round(ops / (ms * 1e-3) / 1e12, 2), "unit": "TOPS", "ms_per_step": round(ms, 3),
            "frac_of_int8_peak": round(ops / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4),
            "roofline": roofline(work / (per_us * 1e-6) / 1e12, "mfma",
-                                f"gemm_kernel<256,256,2,2,W4,SwiGLU> gate_up 2560x19456, M={rows}", per_us, work,
+                                f"gemm_kernel<256,256,2,4,W4,SwiGLU> gate_up 2560x19456, M={rows}", per_us, work,
                                 len(gu), "graph of 36 back-to-back launches, HIP events on the replay stream")}
     log(f"[bench] prefill: {res['value']} TOPS ({ms:.2f} ms/step)")
     del t, head
@@ -421,6 +421,28 @@ def run_moe(torch, ctx, steps, warmup, tokens_list=(512, 1)):
     return results
 
 
+def traffic_probe(torch, ctx, rows=1, reps=3):
+    """Workload for the HBM-traffic counter runs (no timing): a plain 256 MiB
+    device copy (known bytes: the calibration of FETCH_SIZE / WRITE_SIZE) and
+    the decode gate_up GEMV on 36 layers' distinct weights."""
+    from open_rknpu2_lm_infer_amd import device as D
+    src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda").random_(0, 256)
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    gen = Gen(torch, 1)
+    t = DenseLayers(torch, ctx, gen, rows, (4, 4, 4, 4), tag=f"dec{rows}")
+    mid = torch.empty(rows, F, dtype=torch.float16, device="cuda")
+    for _ in range(reps):
+        for mats in t.w:
+            D.linear(ctx, mats["gate_up"], t.x_ffn, mid, rows, swiglu=True, ws=t.ws["gate_up"])
+    torch.cuda.synchronize()
+    log(f"[bench] traffic probe: copy 268435456 B x{reps}, gate_up GEMV x{reps * LAYERS} "
+        f"({lin_bytes(4, H, 2 * F, rows)} algorithmic B each)")
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -428,6 +450,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--primary-only", action="store_true", help="skip the secondary workloads")
+    ap.add_argument("--decode-rows", type=int, default=1,
+                    help="rows of the primary decode line (1 is the metric's configuration)")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="only run the workload of the FETCH_SIZE / WRITE_SIZE counter runs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path "
@@ -436,7 +462,10 @@ def main():
     torch = torch_setup()
     from open_rknpu2_lm_infer_amd import device as D
     ctx = D.DeviceContext(0)
-    primary = run_decode(torch, ctx, 1, args.steps, args.warmup, not args.no_cpu_baseline)
+    if args.traffic_probe:
+        traffic_probe(torch, ctx)
+        return
+    primary = run_decode(torch, ctx, args.decode_rows, args.steps, args.warmup, not args.no_cpu_baseline)
     secondary = []
     if not args.primary_only:
         m4 = run_decode(torch, ctx, 4, args.steps, args.warmup, False, want_roofline=True)
@@ -469,8 +498,8 @@ def main():
         "dtype": "int8",
         "data": "synthetic (seeded random W4 codes in [-8,7], f32 scales U(0.001,0.01), fp16 N(0,1) activations)",
         "config": {"workload": "decode: Qwen3-4B-shaped W4A8 projection set (qkv 2560x6144, o 4096x2560, "
-                               "gate_up 2560x19456 + SwiGLU -> down 9728x2560), M=1, 36 layers",
-                   "rows": 1, "layers": 36, "weight_bits": 4, "activations": "fp16 in/out, per-token dynamic int8",
+                               f"gate_up 2560x19456 + SwiGLU -> down 9728x2560), M={args.decode_rows}, 36 layers",
+                   "rows": args.decode_rows, "layers": 36, "weight_bits": 4, "activations": "fp16 in/out, per-token dynamic int8",
                    "bytes_per_step": primary["bytes_per_step"], "parallelism": "single GPU",
                    "timing": "faster of eager launches and HIP graph replay of the same step "
                              "(replay checked bit-exact vs eager)", **config_extra},

@@ -379,7 +379,7 @@ int enqueue_quant(Workspace* ws, const void* x, int x_type, long lda, int rows, 
     P.part_count = in_max.count;
     P.rowmax_clear = rowmax_clear;
     P.rows_dev = rows_dev;
-    const dim3 grid((rows + 15) / 16), block(256);
+    const dim3 grid(rows), block(256);  // one block per row
     const int slot = prof_begin(s, 2, 8, rule, rows, ws->g.K, 0, rule == QUANT_DENSE ? "quant_rows<dense>" : "quant_rows<moe>");
     if (x_type == DT_F32) {
         if (rule == QUANT_DENSE)

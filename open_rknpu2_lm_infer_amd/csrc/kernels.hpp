@@ -93,6 +93,12 @@ __device__ __forceinline__ float to_f32<__half>(__half v) {
     return __half2float(v);
 }
 
+__device__ __forceinline__ int wave_sum(int v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    return v;
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
@@ -100,12 +106,16 @@ __device__ __forceinline__ float wave_max(float v) {
 }
 
 // ---------------------------------------------------------------------------
-// Per-row dynamic int8 quantization.
-// 16 rows per 256-thread block. Phase 1: one wave per row computes max|x| with
-// a wave reduction (or takes a precomputed max from rowmax_in). Phase 2: each
-// thread quantizes 16 consecutive k of one row and writes them as one 16-byte
-// chunk of the k16-plane layout; 16 consecutive threads cover one 256-byte run.
+// Per-row dynamic int8 quantization: one 256-thread block per row. Thread t
+// owns the 16-element chunks kg = t + 256j of the row; every chunk load (and
+// every precomputed row-max partial) is issued before the first wait, the
+// row max reduces over the block (wave shuffles, then LDS), and each chunk is
+// quantized from registers into one 16-byte entry of the k16-plane layout.
 // ---------------------------------------------------------------------------
+// 16-element chunks per thread the quantization kernel keeps in registers
+// (rows up to 256 * 16 * QUANT_CHUNKS elements take no second pass).
+constexpr int QUANT_CHUNKS = 3;
+
 struct QuantParams {
     const void* x;
     int x_type;
@@ -164,76 +174,116 @@ __device__ __forceinline__ void cvt16_raw(const v4u (&r)[4], float (&v)[16], __h
 
 template <typename T, int RULE>
 __global__ __launch_bounds__(256) void quant_rows_kernel(QuantParams P) {
-    __shared__ float s_inv[16];
-    __shared__ int s_sum[4][16];
+    constexpr int J = QUANT_CHUNKS;  // chunks per thread held in registers
+    constexpr int PV = 8;            // row-max partials per thread held in registers
+    __shared__ float s_max[4];
+    __shared__ int s_sum[4];
     const T* x = static_cast<const T*>(P.x);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int r0 = blockIdx.x * 16;
+    const int r = blockIdx.x;
     const int rows = P.rows_dev ? min(P.rows, *P.rows_dev) : P.rows;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int lr = wave * 4 + i, r = r0 + lr;
-        float m = 0.0f;
-        if (r < rows) {
-            if (P.part_in) {
-                const float* pr = P.part_in + (size_t)r * P.part_count;
-                for (int i = lane; i < P.part_count; i += 64) m = fmaxf(m, pr[i]);
-                m = wave_max(m);
-            } else {
-                const T* xr = x + (size_t)r * P.lda;
-                for (int k = lane; k < P.K; k += 64) m = fmaxf(m, fabsf(to_f32(xr[k])));
-                m = wave_max(m);
-            }
-        }
-        if (lane == 0) {
-            float s;
-            if (RULE == QUANT_DENSE)
-                s = (m == 0.0f) ? 1.0f : fmaxf(m / 127.0f, FLT_MIN);
-            else
-                s = (m == 0.0f) ? 1.0f : m / 127.0f;
-            s_inv[lr] = 1.0f / s;
-            if (r < rows) P.rowscale[r] = s;
-        }
-    }
-    if (P.rowmax_clear && tid < 16 && r0 + tid < P.M_alloc) P.rowmax_clear[r0 + tid] = 0u;
-    __syncthreads();
-    const int lr = tid & 15, r = r0 + lr;
-    const float inv = s_inv[lr];
+    if (P.rowmax_clear && tid == 0) P.rowmax_clear[r] = 0u;
+    if (r >= rows) return;  // whole block: uniform
     const int KG = P.K_pad >> 4;
-    int sum = 0;
-    for (int kg = tid >> 4; kg < KG; kg += 16) {
-        float v[16];
-        if (r < rows) {
-            const T* xr = x + (size_t)r * P.lda + kg * 16;
-            if (P.vec && kg * 16 + 16 <= P.K) {
-                load16(xr, v);
-            } else {
+    const T* xr = x + (size_t)r * P.lda;
+    // 1. Issue every load (no branches around them: masked-off lanes re-read
+    // the row start), then reduce.
+    // (a masked-off chunk re-reads the row's first chunk, which aligned rows
+    // always have; unaligned rows read a 16-byte-aligned workspace word)
+    const T* dummy = P.vec ? xr : reinterpret_cast<const T*>(P.rowscale);
+    v4u raw[J][4];
 #pragma unroll
-                for (int b = 0; b < 16; ++b) v[b] = (kg * 16 + b < P.K) ? to_f32(xr[b]) : 0.0f;
-            }
+    for (int j = 0; j < J; ++j) {
+        const int kg = tid + 256 * j;
+        const bool ok = P.vec && kg * 16 < P.K;
+        load16_raw(ok ? xr + kg * 16 : dummy, raw[j]);
+    }
+    float pv[PV];
+    const float* pr = P.part_in ? P.part_in + (size_t)r * P.part_count : P.rowscale;
+#pragma unroll
+    for (int i = 0; i < PV; ++i) {
+        const int idx = tid + 256 * i;
+        pv[i] = pr[(P.part_in && idx < P.part_count) ? idx : 0];  // masked at use
+    }
+    asm volatile("" ::: "memory");
+    // Chunk j as 16 floats (zero past K; scalar reads when rows are unaligned).
+    auto chunk = [&](int j, float (&v)[16]) {
+        const int kg = tid + 256 * j;
+        if (P.vec) {
+            cvt16_raw(raw[j], v, T());
+#pragma unroll
+            for (int b = 0; b < 16; ++b) v[b] = (kg * 16 < P.K) ? v[b] : 0.0f;
         } else {
 #pragma unroll
-            for (int b = 0; b < 16; ++b) v[b] = 0.0f;
+            for (int b = 0; b < 16; ++b) v[b] = (kg * 16 + b < P.K) ? to_f32(xr[kg * 16 + b]) : 0.0f;
         }
+    };
+    float m = 0.0f;
+    if (P.part_in) {
+#pragma unroll
+        for (int i = 0; i < PV; ++i)
+            if (tid + 256 * i < P.part_count) m = fmaxf(m, pv[i]);
+        for (int i = tid + 256 * PV; i < P.part_count; i += 256) m = fmaxf(m, pr[i]);
+    } else {
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            if (tid + 256 * j >= KG) continue;
+            float v[16];
+            chunk(j, v);
+#pragma unroll
+            for (int b = 0; b < 16; ++b) m = fmaxf(m, fabsf(v[b]));
+        }
+        for (int kg = tid + 256 * J; kg < KG; kg += 256)  // rows longer than 4096 * J elements
+#pragma unroll
+            for (int b = 0; b < 16; ++b)
+                if (kg * 16 + b < P.K) m = fmaxf(m, fabsf(to_f32(xr[kg * 16 + b])));
+    }
+    m = wave_max(m);
+    if (lane == 0) s_max[wave] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(s_max[0], s_max[1]), fmaxf(s_max[2], s_max[3]));
+    float sc;
+    if (RULE == QUANT_DENSE)
+        sc = (m == 0.0f) ? 1.0f : fmaxf(m / 127.0f, FLT_MIN);
+    else
+        sc = (m == 0.0f) ? 1.0f : m / 127.0f;
+    const float inv = 1.0f / sc;
+    if (tid == 0) P.rowscale[r] = sc;
+
+    // 2. Quantize each chunk into its 16-byte entry.
+    int sum = 0;
+    auto quantize = [&](int kg, const float (&v)[16]) {
         unsigned packed[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
         for (int b = 0; b < 16; ++b) {
             float q = v[b] * inv;
             q = (RULE == QUANT_DENSE) ? roundf(q) : __builtin_rintf(q);
             q = fminf(fmaxf(q, -127.0f), 127.0f);
-            int qi = (int)q;
+            const int qi = (int)q;
             sum += qi;
             packed[b >> 2] |= ((unsigned)qi & 0xffu) << ((b & 3) * 8);
         }
-        v4u out = {packed[0], packed[1], packed[2], packed[3]};
-        *reinterpret_cast<v4u*>(P.codes + ((size_t)kg * P.M_alloc + r0 + lr) * 16) = out;
+        *reinterpret_cast<v4u*>(P.codes + ((size_t)kg * P.M_alloc + r) * 16) =
+            v4u{packed[0], packed[1], packed[2], packed[3]};
+    };
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const int kg = tid + 256 * j;
+        if (kg >= KG) continue;
+        float v[16];
+        chunk(j, v);
+        quantize(kg, v);
     }
-    sum += __shfl_xor(sum, 16);
-    sum += __shfl_xor(sum, 32);
-    if (lane < 16) s_sum[wave][lane] = sum;
+    for (int kg = tid + 256 * J; kg < KG; kg += 256) {
+        float v[16];
+#pragma unroll
+        for (int b = 0; b < 16; ++b) v[b] = (kg * 16 + b < P.K) ? to_f32(xr[kg * 16 + b]) : 0.0f;
+        quantize(kg, v);
+    }
+    sum = wave_sum(sum);
+    if (lane == 0) s_sum[wave] = sum;
     __syncthreads();
-    if (tid < 16 && r0 + tid < rows)
-        P.rowsum[r0 + tid] = s_sum[0][tid] + s_sum[1][tid] + s_sum[2][tid] + s_sum[3][tid];
+    if (tid == 0) P.rowsum[r] = s_sum[0] + s_sum[1] + s_sum[2] + s_sum[3];
 }
 
 // ---------------------------------------------------------------------------
@@ -693,11 +743,6 @@ struct GemvParams {
     int M_alloc;
 };
 
-__device__ __forceinline__ int wave_sum(int v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-    return v;
-}
 
 template <typename T, int MR, int BITS, int EPI, int RW, int NW, bool PREQ>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
