@@ -452,6 +452,8 @@ def main():
     ap.add_argument("--primary-only", action="store_true", help="skip the secondary workloads")
     ap.add_argument("--decode-rows", type=int, default=1,
                     help="rows of the primary decode line (1 is the metric's configuration)")
+    ap.add_argument("--only", choices=["prefill", "ffn512", "up128", "moe"],
+                    help="run one secondary workload alone and print its result (for profiling)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only run the workload of the FETCH_SIZE / WRITE_SIZE counter runs")
     args = ap.parse_args()
@@ -464,6 +466,14 @@ def main():
     ctx = D.DeviceContext(0)
     if args.traffic_probe:
         traffic_probe(torch, ctx)
+        return
+    if args.only:
+        steps = max(4, args.steps // 2)
+        res = {"prefill": lambda: run_prefill(torch, ctx, 4096, steps, 2),
+               "ffn512": lambda: run_ffn512(torch, ctx, steps, 2),
+               "up128": lambda: run_up128(torch, ctx, args.steps, args.warmup),
+               "moe": lambda: run_moe(torch, ctx, steps, 2)}[args.only]()
+        print(json.dumps(res), flush=True)
         return
     primary = run_decode(torch, ctx, args.decode_rows, args.steps, args.warmup, not args.no_cpu_baseline)
     secondary = []

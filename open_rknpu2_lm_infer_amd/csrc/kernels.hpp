@@ -106,8 +106,9 @@ __device__ __forceinline__ float wave_max(float v) {
 }
 
 // ---------------------------------------------------------------------------
-// Per-row dynamic int8 quantization: one 256-thread block per row. Thread t
-// owns the 16-element chunks kg = t + 256j of the row; every chunk load (and
+// Per-row dynamic int8 quantization: a row is owned by TPR threads (the
+// whole 256-thread block, or one wave for rows of at most 64 * QUANT_CHUNKS
+// chunks). Thread t owns the 16-element chunks kg = t + TPR*j of the row; every chunk load (and
 // every precomputed row-max partial) is issued before the first wait, the
 // row max reduces over the block (wave shuffles, then LDS), and each chunk is
 // quantized from registers into one 16-byte entry of the k16-plane layout.
@@ -172,18 +173,19 @@ __device__ __forceinline__ void cvt16_raw(const v4u (&r)[4], float (&v)[16], __h
     }
 }
 
-template <typename T, int RULE>
+template <typename T, int RULE, int TPR>
 __global__ __launch_bounds__(256) void quant_rows_kernel(QuantParams P) {
     constexpr int J = QUANT_CHUNKS;  // chunks per thread held in registers
     constexpr int PV = 8;            // row-max partials per thread held in registers
     __shared__ float s_max[4];
     __shared__ int s_sum[4];
     const T* x = static_cast<const T*>(P.x);
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int r = blockIdx.x;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int tid = threadIdx.x % TPR;  // thread within its row
+    const int r = blockIdx.x * (256 / TPR) + threadIdx.x / TPR;
     const int rows = P.rows_dev ? min(P.rows, *P.rows_dev) : P.rows;
-    if (P.rowmax_clear && tid == 0) P.rowmax_clear[r] = 0u;
-    if (r >= rows) return;  // whole block: uniform
+    if (P.rowmax_clear && tid == 0 && r < P.M_alloc) P.rowmax_clear[r] = 0u;
+    if (r >= rows) return;  // uniform over the row's threads (a block or a wave)
     const int KG = P.K_pad >> 4;
     const T* xr = x + (size_t)r * P.lda;
     // 1. Issue every load (no branches around them: masked-off lanes re-read
@@ -194,7 +196,7 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantParams P) {
     v4u raw[J][4];
 #pragma unroll
     for (int j = 0; j < J; ++j) {
-        const int kg = tid + 256 * j;
+        const int kg = tid + TPR * j;
         const bool ok = P.vec && kg * 16 < P.K;
         load16_raw(ok ? xr + kg * 16 : dummy, raw[j]);
     }
@@ -202,13 +204,13 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantParams P) {
     const float* pr = P.part_in ? P.part_in + (size_t)r * P.part_count : P.rowscale;
 #pragma unroll
     for (int i = 0; i < PV; ++i) {
-        const int idx = tid + 256 * i;
+        const int idx = tid + TPR * i;
         pv[i] = pr[(P.part_in && idx < P.part_count) ? idx : 0];  // masked at use
     }
     asm volatile("" ::: "memory");
     // Chunk j as 16 floats (zero past K; scalar reads when rows are unaligned).
     auto chunk = [&](int j, float (&v)[16]) {
-        const int kg = tid + 256 * j;
+        const int kg = tid + TPR * j;
         if (P.vec) {
             cvt16_raw(raw[j], v, T());
 #pragma unroll
@@ -222,26 +224,28 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantParams P) {
     if (P.part_in) {
 #pragma unroll
         for (int i = 0; i < PV; ++i)
-            if (tid + 256 * i < P.part_count) m = fmaxf(m, pv[i]);
-        for (int i = tid + 256 * PV; i < P.part_count; i += 256) m = fmaxf(m, pr[i]);
+            if (tid + TPR * i < P.part_count) m = fmaxf(m, pv[i]);
+        for (int i = tid + TPR * PV; i < P.part_count; i += TPR) m = fmaxf(m, pr[i]);
     } else {
 #pragma unroll
         for (int j = 0; j < J; ++j) {
-            if (tid + 256 * j >= KG) continue;
+            if (tid + TPR * j >= KG) continue;
             float v[16];
             chunk(j, v);
 #pragma unroll
             for (int b = 0; b < 16; ++b) m = fmaxf(m, fabsf(v[b]));
         }
-        for (int kg = tid + 256 * J; kg < KG; kg += 256)  // rows longer than 4096 * J elements
+        for (int kg = tid + TPR * J; kg < KG; kg += TPR)  // rows longer than 16 * TPR * J elements
 #pragma unroll
             for (int b = 0; b < 16; ++b)
                 if (kg * 16 + b < P.K) m = fmaxf(m, fabsf(to_f32(xr[kg * 16 + b])));
     }
     m = wave_max(m);
-    if (lane == 0) s_max[wave] = m;
-    __syncthreads();
-    m = fmaxf(fmaxf(s_max[0], s_max[1]), fmaxf(s_max[2], s_max[3]));
+    if (TPR == 256) {
+        if (lane == 0) s_max[wave] = m;
+        __syncthreads();
+        m = fmaxf(fmaxf(s_max[0], s_max[1]), fmaxf(s_max[2], s_max[3]));
+    }
     float sc;
     if (RULE == QUANT_DENSE)
         sc = (m == 0.0f) ? 1.0f : fmaxf(m / 127.0f, FLT_MIN);
@@ -268,22 +272,25 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantParams P) {
     };
 #pragma unroll
     for (int j = 0; j < J; ++j) {
-        const int kg = tid + 256 * j;
+        const int kg = tid + TPR * j;
         if (kg >= KG) continue;
         float v[16];
         chunk(j, v);
         quantize(kg, v);
     }
-    for (int kg = tid + 256 * J; kg < KG; kg += 256) {
+    for (int kg = tid + TPR * J; kg < KG; kg += TPR) {
         float v[16];
 #pragma unroll
         for (int b = 0; b < 16; ++b) v[b] = (kg * 16 + b < P.K) ? to_f32(xr[kg * 16 + b]) : 0.0f;
         quantize(kg, v);
     }
     sum = wave_sum(sum);
-    if (lane == 0) s_sum[wave] = sum;
-    __syncthreads();
-    if (tid == 0) P.rowsum[r] = s_sum[0] + s_sum[1] + s_sum[2] + s_sum[3];
+    if (TPR == 256) {
+        if (lane == 0) s_sum[wave] = sum;
+        __syncthreads();
+        sum = s_sum[0] + s_sum[1] + s_sum[2] + s_sum[3];
+    }
+    if (tid == 0) P.rowsum[r] = sum;
 }
 
 // ---------------------------------------------------------------------------
@@ -548,34 +555,75 @@ __device__ __forceinline__ void gemm_mainloop(uint8_t* smem, const int8_t* __res
 #undef HM_STAGE
 }
 
-// Epilogue of a finished tile. Fragment (i, j) register r holds row
-// 8*(r/4) + 4*half_id + r%4 and column l32 of its 32x32 block. row_of maps the
-// tile-local row to (output row, scale row, valid).
+// Per-thread values the epilogue needs from HBM, requested before the main
+// loop so they have long arrived when it ends: the row scale and W4 code-sum
+// correction of tile row threadIdx.x, and the column scales of this lane's
+// fragment columns.
+template <int BM, int BN, int WGM, int WGN, int BITS>
+struct EpiPre {
+    float rs;
+    int rc;
+    float cs[TileCfg<BM, BN, WGM, WGN, BITS>::FN];
+};
+
+template <int BM, int BN, int WGM, int WGN, int BITS, typename RowMap>
+__device__ __forceinline__ EpiPre<BM, BN, WGM, WGN, BITS> epilogue_prefetch(const float* __restrict__ rowscale,
+                                                                         const int* __restrict__ rowsum,
+                                                                         const float* __restrict__ colscale, int n0,
+                                                                         RowMap row_of) {
+    using C = TileCfg<BM, BN, WGM, WGN, BITS>;
+    static_assert(BM <= C::NT, "one tile row per thread");
+    EpiPre<BM, BN, WGM, WGN, BITS> pre;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, wn = wave % WGN;
+    int out_row, src_row;
+    const int local = threadIdx.x < BM ? threadIdx.x : 0;
+    row_of(local, out_row, src_row);
+    pre.rs = rowscale[src_row];
+    pre.rc = (BITS == 4) ? 8 * rowsum[src_row] : 0;
+#pragma unroll
+    for (int j = 0; j < C::FN; ++j) pre.cs[j] = colscale[n0 + wn * C::TN + j * 32 + (lane & 31)];
+    return pre;
+}
+
+// Epilogue of a finished tile: dequantize (two RNE multiplies, row scale then
+// column scale), optional SwiGLU with the row max of |out| for the next
+// quantization, and the store.
 template <int BM, int BN, int WGM, int WGN, int BITS, int EPI, typename RowMap>
 __device__ __forceinline__ void gemm_epilogue(
     const v16i (&acc)[TileCfg<BM, BN, WGM, WGN, BITS>::FM][TileCfg<BM, BN, WGM, WGN, BITS>::FN], int n0,
-    const float* __restrict__ rowscale, const int* __restrict__ rowsum, const float* __restrict__ colscale, int N,
-    int half, void* c, long ldc, int c_type, unsigned* rowmax, RowMap row_of, uint8_t* smem) {
+    const EpiPre<BM, BN, WGM, WGN, BITS>& pre, int N, int half, void* c, long ldc, int c_type, unsigned* rowmax,
+    RowMap row_of, uint8_t* smem) {
     using C = TileCfg<BM, BN, WGM, WGN, BITS>;
     constexpr int TM = C::TM, TN = C::TN, FM = C::FM, FN = C::FN, NW = WGM * WGN;
+    __shared__ float s_rs[BM];
+    __shared__ int s_rc[BM];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave / WGN, wn = wave % WGN;
     const int half_id = lane >> 5, l32 = lane & 31;
     const int esz = c_type == DT_F32 ? 4 : 2;
     // Output columns this wave owns (SwiGLU: TN/2, contiguous from out0).
     constexpr int OUTC = (EPI == EPI_PLAIN) ? TN : TN / 2;
+    const int out0 = (EPI == EPI_PLAIN) ? n0 + wn * TN : (n0 + wn * TN) >> 1;
+    const int n_out = (EPI == EPI_PLAIN) ? N : N / 2;
 
-    // Rows are staged through LDS and written as 16-byte runs when the output
-    // allows it (16-byte aligned base and row pitch); otherwise each lane
-    // stores its own elements. Values and rounding are identical either way.
+    // Rows are staged through LDS (SwiGLU values in f32, so the row max is
+    // taken on exact values; plain values in the output type) and written as
+    // 16-byte runs when the output allows it (16-byte aligned base and row
+    // pitch); otherwise each lane stores its own elements. Values and
+    // rounding are identical either way.
     const bool staged = ((reinterpret_cast<uintptr_t>(c) & 15) == 0) && ((((size_t)ldc * esz) & 15) == 0);
+    const int ssz = (EPI == EPI_PLAIN) ? esz : 4;  // staged element size
     constexpr int WAVE_LDS = C::LDS / NW;
     constexpr int FIT = WAVE_LDS / (32 * (OUTC * 4 + 16));
     static_assert(FIT >= 1, "epilogue staging does not fit in LDS");
     constexpr int FPI = FIT >= FM ? FM : ((FIT >= 2 && FM % 2 == 0) ? 2 : 1);
-    const int pitch = OUTC * esz + 16;
+    const int pitch = OUTC * ssz + 16;
     uint8_t* wl = smem + wave * WAVE_LDS;
-    if (staged) __syncthreads();
+    if (threadIdx.x < BM) {
+        s_rs[threadIdx.x] = pre.rs;
+        s_rc[threadIdx.x] = pre.rc;
+    }
+    __syncthreads();
 
 #pragma unroll
     for (int i0 = 0; i0 < FM; i0 += FPI) {
@@ -587,67 +635,102 @@ __device__ __forceinline__ void gemm_epilogue(
                 const int rr = (r >> 2) * 8 + half_id * 4 + (r & 3);
                 const int local = wm * TM + i * 32 + rr;
                 uint8_t* lrow = wl + (ii * 32 + rr) * pitch;
-                int out_row, src_row;
-                const bool row_ok = row_of(local, out_row, src_row);
-                const float s_row = rowscale[src_row];
-                const int corr = (BITS == 4) ? 8 * rowsum[src_row] : 0;
+                const float s_row = s_rs[local];
+                const int corr = s_rc[local];
                 if (EPI == EPI_PLAIN) {
 #pragma unroll
                     for (int j = 0; j < FN; ++j) {
-                        const int p = n0 + wn * TN + j * 32 + l32;
-                        const float y = ((float)(acc[i][j][r] - corr) * s_row) * colscale[p];
-                        if (staged)
+                        const float y = ((float)(acc[i][j][r] - corr) * s_row) * pre.cs[j];
+                        if (staged) {
                             store_out(lrow, c_type, j * 32 + l32, y);
-                        else if (row_ok && p < N)
-                            store_out(c, c_type, (size_t)out_row * ldc + orig_col(p, half), y);
+                        } else {
+                            const int p = n0 + wn * TN + j * 32 + l32;
+                            int out_row, src_row;
+                            if (row_of(local, out_row, src_row) && p < N)
+                                store_out(c, c_type, (size_t)out_row * ldc + orig_col(p, half), y);
+                        }
                     }
                 } else {
                     float mx = 0.0f;
 #pragma unroll
                     for (int j = 0; j < FN; j += 2) {
-                        const int p = n0 + wn * TN + j * 32 + l32;
-                        const float g = ((float)(acc[i][j][r] - corr) * s_row) * colscale[p];
-                        const float u = ((float)(acc[i][j + 1][r] - corr) * s_row) * colscale[p + 32];
+                        const float g = ((float)(acc[i][j][r] - corr) * s_row) * pre.cs[j];
+                        const float u = ((float)(acc[i][j + 1][r] - corr) * s_row) * pre.cs[j + 1];
                         const float o = hm_swiglu(g, u);
-                        mx = fmaxf(mx, fabsf(o));
-                        if (staged)
-                            store_out(lrow, c_type, (j >> 1) * 32 + l32, o);
-                        else if (row_ok && p < N)
-                            store_out(c, c_type, (size_t)out_row * ldc + ((p >> 6) << 5) + l32, o);
+                        if (staged) {
+                            reinterpret_cast<float*>(lrow)[(j >> 1) * 32 + l32] = o;
+                        } else {
+                            const int p = n0 + wn * TN + j * 32 + l32;
+                            mx = fmaxf(mx, fabsf(o));
+                            int out_row, src_row;
+                            if (row_of(local, out_row, src_row) && p < N)
+                                store_out(c, c_type, (size_t)out_row * ldc + ((p >> 6) << 5) + l32, o);
+                        }
                     }
-                    if (EPI == EPI_SWIGLU_MAX) {
+                    if (EPI == EPI_SWIGLU_MAX && !staged) {
 #pragma unroll
                         for (int off = 16; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-                        if (l32 == 0 && row_ok) atomicMax(rowmax + out_row, __float_as_uint(mx));
+                        int out_row, src_row;
+                        if (l32 == 0 && row_of(local, out_row, src_row)) atomicMax(rowmax + out_row, __float_as_uint(mx));
                     }
                 }
             }
         }
         if (!staged) continue;
         __syncthreads();
-        // 16-byte runs: chunk q of the staged rows -> (row, 16/esz columns).
-        const int per = 16 / esz, cpr = OUTC / per;
-        const int n_out = (EPI == EPI_PLAIN) ? N : N / 2;
-        for (int q = lane; q < FPI * 32 * cpr; q += 64) {
-            const int lr = q / cpr, cc = (q - lr * cpr) * per;
-            int out_row, src_row;
-            if (!row_of(wm * TM + i0 * 32 + lr, out_row, src_row)) continue;
-            int col, valid;
-            if (EPI == EPI_PLAIN) {
-                const int p = n0 + wn * TN + cc;
-                col = orig_col(p, half);
-                valid = N - p;
-            } else {
-                col = ((n0 + wn * TN) >> 1) + cc;
-                valid = n_out - col;
+        if (EPI == EPI_PLAIN) {
+            // 16-byte runs: chunk q of the staged rows -> (row, 16/esz columns).
+            const int per = 16 / esz, cpr = OUTC / per;
+            for (int q = lane; q < FPI * 32 * cpr; q += 64) {
+                const int lr = q / cpr, cc = (q - lr * cpr) * per;
+                int out_row, src_row;
+                if (!row_of(wm * TM + i0 * 32 + lr, out_row, src_row)) continue;
+                const int p = out0 + cc;
+                const int col = orig_col(p, half), valid = N - p;
+                const uint8_t* src = wl + lr * pitch + cc * esz;
+                uint8_t* dst = static_cast<uint8_t*>(c) + ((size_t)out_row * ldc + col) * esz;
+                if (valid >= per) {
+                    *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(src);
+                } else {
+                    for (int t = 0; t < valid; ++t)
+                        for (int bb = 0; bb < esz; ++bb) dst[t * esz + bb] = src[t * esz + bb];
+                }
             }
-            const uint8_t* src = wl + lr * pitch + cc * esz;
-            uint8_t* dst = static_cast<uint8_t*>(c) + ((size_t)out_row * ldc + col) * esz;
-            if (valid >= per) {
-                *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(src);
-            } else {
-                for (int t = 0; t < valid; ++t)
-                    for (int bb = 0; bb < esz; ++bb) dst[t * esz + bb] = src[t * esz + bb];
+        } else {
+            // 4 staged f32 values per lane: max |o| over the row's lanes (CPR
+            // consecutive lanes), conversion to the output type, one store.
+            constexpr int CPR = OUTC / 4;
+            static_assert((FPI * 32 * CPR) % 64 == 0 && 64 % CPR == 0, "rows must not straddle waves");
+            for (int q = lane; q < FPI * 32 * CPR; q += 64) {
+                const int lr = q / CPR, cc = (q % CPR) * 4;
+                int out_row, src_row;
+                const bool row_ok = row_of(wm * TM + i0 * 32 + lr, out_row, src_row);
+                const float4 v = *reinterpret_cast<const float4*>(wl + lr * pitch + cc * 4);
+                const int col = out0 + cc, valid = row_ok ? n_out - col : 0;
+                float mx = 0.0f;
+                if (valid > 0) mx = fabsf(v.x);
+                if (valid > 1) mx = fmaxf(mx, fabsf(v.y));
+                if (valid > 2) mx = fmaxf(mx, fabsf(v.z));
+                if (valid > 3) mx = fmaxf(mx, fabsf(v.w));
+                if (valid >= 4) {
+                    if (c_type == DT_F32) {
+                        *reinterpret_cast<float4*>(static_cast<float*>(c) + (size_t)out_row * ldc + col) = v;
+                    } else {
+                        const __half2 h01 = __floats2half2_rn(v.x, v.y), h23 = __floats2half2_rn(v.z, v.w);
+                        uint2 pk;
+                        pk.x = *reinterpret_cast<const unsigned*>(&h01);
+                        pk.y = *reinterpret_cast<const unsigned*>(&h23);
+                        *reinterpret_cast<uint2*>(static_cast<__half*>(c) + (size_t)out_row * ldc + col) = pk;
+                    }
+                } else {
+                    const float vv[4] = {v.x, v.y, v.z, v.w};
+                    for (int t = 0; t < valid; ++t) store_out(c, c_type, (size_t)out_row * ldc + col + t, vv[t]);
+                }
+                if (EPI == EPI_SWIGLU_MAX) {
+#pragma unroll
+                    for (int off = 1; off < CPR; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+                    if ((lane % CPR) == 0 && row_ok) atomicMax(rowmax + out_row, __float_as_uint(mx));
+                }
             }
         }
         __syncthreads();
@@ -689,15 +772,17 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_kernel(GemmParams P) {
         for (int j = 0; j < C::FN; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
-    gemm_mainloop<BM, BN, WGM, WGN, BITS>(smem, P.a, (size_t)P.M_alloc, a_off, P.b, P.K_pad, n0, P.K_pad >> 6, acc);
     const int M = P.M;
-    gemm_epilogue<BM, BN, WGM, WGN, BITS, EPI>(acc, n0, P.rowscale, P.rowsum, P.colscale, P.N, P.half, P.c, P.ldc,
-                                               P.c_type, P.rowmax, [&](int local, int& out_row, int& src_row) {
-                                                   const int row = m0 + local;
-                                                   out_row = row;
-                                                   src_row = row < M ? row : 0;
-                                                   return row < M;
-                                               }, smem);
+    auto row_of = [&](int local, int& out_row, int& src_row) {
+        const int row = m0 + local;
+        out_row = row;
+        src_row = row < M ? row : 0;
+        return row < M;
+    };
+    const auto pre = epilogue_prefetch<BM, BN, WGM, WGN, BITS>(P.rowscale, P.rowsum, P.colscale, n0, row_of);
+    gemm_mainloop<BM, BN, WGM, WGN, BITS>(smem, P.a, (size_t)P.M_alloc, a_off, P.b, P.K_pad, n0, P.K_pad >> 6, acc);
+    gemm_epilogue<BM, BN, WGM, WGN, BITS, EPI>(acc, n0, pre, P.N, P.half, P.c, P.ldc, P.c_type, P.rowmax, row_of,
+                                               smem);
 }
 
 // ---------------------------------------------------------------------------

@@ -132,14 +132,16 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void moe_gemm_kernel(MoeGemmParam
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
     const int n0 = tn * BN;
+    auto row_of = [&](int local, int& out_row, int& src_row) {
+        out_row = begin + local;
+        src_row = s_rows[local];
+        return begin + local < end;
+    };
+    const auto pre = epilogue_prefetch<BM, BN, WGM, WGN, BITS>(P.rowscale, P.rowsum, P.s_tab[e], n0, row_of);
     gemm_mainloop<BM, BN, WGM, WGN, BITS>(smem, P.a, (size_t)P.a_alloc, a_off, P.b_tab[e], P.K_pad, n0, P.K_pad >> 6,
                                           acc);
-    gemm_epilogue<BM, BN, WGM, WGN, BITS, EPI>(acc, n0, P.rowscale, P.rowsum, P.s_tab[e], P.N, P.half, P.c, P.ldc,
-                                               P.c_type, P.rowmax, [&](int local, int& out_row, int& src_row) {
-                                                   out_row = begin + local;
-                                                   src_row = s_rows[local];
-                                                   return begin + local < end;
-                                               }, smem);
+    gemm_epilogue<BM, BN, WGM, WGN, BITS, EPI>(acc, n0, pre, P.N, P.half, P.c, P.ldc, P.c_type, P.rowmax, row_of,
+                                               smem);
 }
 
 // ---------------------------------------------------------------------------
