@@ -142,13 +142,22 @@ def graph_time(torch, fn, reps, check=None):
     return e0.elapsed_time(e1) / reps, ok
 
 
-def roofline(achieved, bound, kernel, avg_us, work, launches, method):
+# HBM bytes per launch of the dominant decode kernel (gate_up GEMV, M=1), from
+# two rocprofv3 counter runs of `bench.py --traffic-probe` (FETCH_SIZE, then
+# WRITE_SIZE, KiB per dispatch, median over 108 dispatches), each scaled by
+# what the same counter reads for a 268,435,456-byte device copy in the same
+# run: FETCH_SIZE 131,089.5 KiB (factor 2.0), WRITE_SIZE 262,144 KiB (factor 1.0).
+# Summary and commands: profiles/traffic_gemv_gate_up_m1.txt.
+TRAFFIC_GEMV_GATE_UP_M1 = int(round((12416.0 * 2.0 + 81.0625 * 1.0) * 1024))
+
+
+def roofline(achieved, bound, kernel, avg_us, work, launches, method, traffic=None):
     if bound == "hbm":
         peak, unit = HBM_PEAK_GBS, "GB/s"
     else:
         peak, unit = INT8_PEAK_TOPS, "TFLOP/s"
     return {"bound": bound, "kernel": kernel, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
-            "frac": round(achieved / peak, 4), "traffic": None, "avg_us": round(avg_us, 3),
+            "frac": round(achieved / peak, 4), "traffic": traffic, "avg_us": round(avg_us, 3),
             "work_per_launch": work, "launches": launches, "method": method}
 
 
@@ -259,7 +268,8 @@ def run_decode(torch, ctx, rows, steps, warmup, want_cpu, want_roofline=True):
         out["roofline"] = roofline(work / (per_launch_us * 1e-6) / 1e9, "hbm",
                                    f"gemv_kernel<__half,{rows if rows in (1, 2, 4) else 8},4,SwiGLU> "
                                    f"gate_up 2560x19456 W4, M={rows}", per_launch_us, work, len(gu) * steps,
-                                   "graph of 36 back-to-back launches (distinct weights), HIP events on the replay stream")
+                                   "graph of 36 back-to-back launches (distinct weights), HIP events on the replay stream",
+                                   TRAFFIC_GEMV_GATE_UP_M1 if rows == 1 else None)
         log(f"[bench] decode roofline: {out['roofline']}")
     if want_cpu:
         log("[bench] cpu baseline (oracle) on layer 0 ...")

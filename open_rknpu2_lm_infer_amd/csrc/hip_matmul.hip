@@ -779,7 +779,7 @@ static int run_host(Workspace* ws, const Weights* w, const float* A, float* C, i
     const double t0 = now_us();
     if (!ws || !w || !A || !C) return RK_NPU_ERR_PARAM;
     if (ws->g.K != w->g.K || ws->g.N != w->g.N || ws->g.bits != w->g.bits) return RK_NPU_ERR_PARAM;
-    if (epi != EPI_PLAIN && !w->g.half) return RK_NPU_ERR_PARAM;
+    if (epi != EPI_PLAIN && !w->g.half) return RK_NPU_ERR_UNSUPPORTED;  // SwiGLU needs N % 64 == 0
     BusyGuard guard(ws->busy);
     if (!guard.ok) return RK_NPU_ERR_BUSY;
     if (hipSetDevice(device_of(ws->domain)) != hipSuccess) return RK_NPU_ERR_DEVICE;
@@ -1028,7 +1028,7 @@ int rk_npu_hip_linear_run(void* workspace, const void* weights, int bits, const 
     if (ws->g.K != w->g.K || ws->g.N != w->g.N || rows < 1 || rows > ws->M) return RK_NPU_ERR_PARAM;
     if (epilogue != RK_NPU_HIP_PLAIN && epilogue != RK_NPU_HIP_SWIGLU) return RK_NPU_ERR_PARAM;
     const int epi = epilogue == RK_NPU_HIP_SWIGLU ? EPI_SWIGLU_MAX : EPI_PLAIN;
-    if (epi != EPI_PLAIN && !w->g.half) return RK_NPU_ERR_PARAM;
+    if (epi != EPI_PLAIN && !w->g.half) return RK_NPU_ERR_UNSUPPORTED;  // SwiGLU needs N % 64 == 0
     BusyGuard guard(ws->busy);
     if (!guard.ok) return RK_NPU_ERR_BUSY;
     if (hipSetDevice(device_of(ws->domain)) != hipSuccess) return RK_NPU_ERR_DEVICE;

@@ -7,7 +7,8 @@
  * load it, and only as the checker (or the timed CPU baseline). The product
  * library never links or calls it.
  *
- * Parity status per function is listed in oracle/README.md.
+ * Each function cites the reference lines it restates; tests/ pins every one
+ * of them with known answers, closed forms or brute force.
  */
 #ifndef RK_ORACLE_H
 #define RK_ORACLE_H
