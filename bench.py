@@ -11,9 +11,9 @@ W8A8/W4A8 prefill projection set x36 + lm_head (int8 TOPS), the M=512 FFN
 block x36, the M=128 W8A8 up projection, and the 35B-A3B-class MoE at T=512
 and T=1.
 
-Timing: the step runs eagerly (host launches between two synchronizations)
-and as a HIP graph replay (checked bit-exact against eager runs) between two
-HIP events; value uses the faster of the two, both are reported.
+Timing (every workload): the step runs eagerly (host launches between two
+synchronizations) and as a HIP graph replay (checked bit-exact against eager
+runs) between two HIP events; the faster valid one is used, both are reported.
 roofline: the dominant kernel's algorithmic bytes (or ops) per launch over its
 average launch time: 36 back-to-back launches of that kernel alone (distinct
 layers' weights) captured in a graph and timed with HIP events on the replay
@@ -100,6 +100,14 @@ def time_steps(torch, step, steps, warmup):
         step()
     torch.cuda.synchronize()
     return (time.perf_counter() - t0) * 1000.0 / steps
+
+
+def best_time(torch, step, steps, warmup, check):
+    """Eager launches and a HIP-graph replay of the same step (replays checked
+    bit-exact against eager runs); the faster valid one is the step time."""
+    ms_eager = time_steps(torch, step, steps, warmup)
+    ms_graph, ok = graph_time(torch, step, steps, check)
+    return (min(ms_eager, ms_graph) if ok else ms_eager), ms_eager, ms_graph, ok
 
 
 def graph_time(torch, fn, reps, check=None):
@@ -293,7 +301,8 @@ def run_prefill(torch, ctx, rows, steps, warmup):
         t.step()
         D.linear(ctx, head, t.x_qkv, y_head, rows, ws=ws_head)
 
-    ms = time_steps(torch, step, steps, warmup)
+    ms, ms_eager, ms_graph, ok = best_time(torch, step, steps, warmup,
+                                           lambda: [t.y_qkv.clone(), t.y_ffn.clone(), y_head.clone()])
     ops = t.ops_per_layer() * LAYERS + 2.0 * rows * H * VOCAB
     # dominant kernel: the W4 gate_up GEMM with fused SwiGLU, 36 launches
     gu = [mats["gate_up"] for mats in t.w]
@@ -307,6 +316,7 @@ def run_prefill(torch, ctx, rows, steps, warmup):
     res = {"workload": f"prefill M={rows}: Qwen3-4B qkv/o/down W8A8 + gate_up W4A8 (+SwiGLU) x36 + lm_head W8A8",
            "value": round(ops / (ms * 1e-3) / 1e12, 2), "unit": "TOPS", "ms_per_step": round(ms, 3),
            "frac_of_int8_peak": round(ops / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4),
+           "ms_eager": round(ms_eager, 3), "ms_graph": round(ms_graph, 3), "graph_matches_eager": ok,
            "roofline": roofline(work / (per_us * 1e-6) / 1e12, "mfma",
                                 f"gemm_kernel<256,256,2,4,W4,SwiGLU> gate_up 2560x19456, M={rows}", per_us, work,
                                 len(gu), "graph of 36 back-to-back launches, HIP events on the replay stream")}
@@ -332,11 +342,12 @@ def run_ffn512(torch, ctx, steps, warmup, rows=512):
         for gu, dn in layers:
             D.ffn(ctx, gu, dn, x, y, rows, gws=gws, dws=dws)
 
-    ms = time_steps(torch, step, steps, warmup)
+    ms, ms_eager, ms_graph, ok = best_time(torch, step, steps, warmup, lambda: [y.clone()])
     ops = LAYERS * 2.0 * rows * (H * 2 * F + F * H)
     res = {"workload": "FFN block M=512: W4A8 gate_up 2560->2x9728 + SwiGLU + requant + W8A8 down, 36 layers",
            "value": round(ops / (ms * 1e-3) / 1e12, 2), "unit": "TOPS", "ms_per_step": round(ms, 3),
-           "frac_of_int8_peak": round(ops / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4)}
+           "frac_of_int8_peak": round(ops / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4),
+           "ms_eager": round(ms_eager, 3), "ms_graph": round(ms_graph, 3), "graph_matches_eager": ok}
     log(f"[bench] ffn512: {res['value']} TOPS")
     del layers
     return res
@@ -351,7 +362,7 @@ def run_up128(torch, ctx, steps, warmup, rows=128):
     y = torch.empty(rows, F, dtype=torch.float16, device="cuda")
     ws = ctx.workspace(8, rows, H, F)
     step = lambda: D.linear(ctx, w, x, y, rows, ws=ws)
-    ms = time_steps(torch, step, steps * 10, warmup)
+    ms, _, _, _ = best_time(torch, step, steps * 10, warmup, lambda: [y.clone()])
     ops = 2.0 * rows * H * F
     return {"workload": "W8A8 linear M=128 K=2560 N=9728 (Qwen3-4B FFN up)", "value": round(ops / (ms * 1e-3) / 1e12, 2),
             "unit": "TOPS", "ms_per_step": round(ms, 4),
@@ -415,13 +426,15 @@ def run_moe(torch, ctx, steps, warmup, tokens_list=(512, 1)):
             npu.check(rc, "MoE run")
             D.ffn(ctx, sgu, sdn, xs, ys, T, gws=gws, dws=dws)
 
-        ms = time_steps(torch, step, steps * (10 if T == 1 else 1), warmup)
+        ms, ms_eager, ms_graph, ok = best_time(torch, step, steps * (10 if T == 1 else 1), warmup,
+                                               lambda: [y.clone(), ys.clone()])
         routed_ops = 2.0 * T * top * (h * 2 * inter + inter * h)
         shared_ops = 2.0 * T * (h * 2 * sh_inter + sh_inter * h)
         routed_bytes = min(experts, T * top) * (h * 2 * inter // 2 + 4 * 2 * inter + inter * h + 4 * h)
         shared_bytes = h * 2 * sh_inter + 4 * 2 * sh_inter + sh_inter * h + 4 * h
         res = {"workload": f"MoE 35B-A3B-class T={T}: h2048 E128 top8 I768 W4 gate_up + W8 down, shared W8 FFN I2048",
-               "ms_per_step": round(ms, 4)}
+               "ms_per_step": round(ms, 4), "ms_eager": round(ms_eager, 4), "ms_graph": round(ms_graph, 4),
+               "graph_matches_eager": ok}
         if T >= 64:
             res.update(value=round((routed_ops + shared_ops) / (ms * 1e-3) / 1e12, 2), unit="TOPS")
         else:

@@ -829,10 +829,11 @@ struct GemvParams {
 };
 
 
-template <typename T, int MR, int BITS, int EPI, int RW, int NW, bool PREQ>
+template <typename T, int MR, int BITS, int EPI, int RW, int NW, bool PREQ, int GPB = 1>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
     extern __shared__ __attribute__((aligned(16))) int8_t sa[];  // [K_pad/16][MR][16]
-    constexpr int TPB = (EPI == EPI_PLAIN) ? 1 : 2;
+    constexpr int TPG = (EPI == EPI_PLAIN) ? 1 : 2;  // tiles per group
+    constexpr int TPB = TPG * GPB;                   // tiles per block (GPB groups)
     constexpr int XMAX = GEMV_XMAX;  // 16-element activation chunks per thread
     constexpr int PV = 5;            // precomputed row-max partials per thread
     __shared__ float s_red[4][MR];
@@ -846,19 +847,34 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
     const int CPG = CPT * TPB;               // chunks per group
     const int NWIN = (CPG + 256 * RW - 1) / (256 * RW);
     const int chunks = KG16 * MR;            // activation chunks (<= 256 * XMAX unless PREQ)
-    const int g = blockIdx.x;
-    const int groups = gridDim.x;
+    const int g0 = blockIdx.x * GPB;  // first group of the block
+    const int groups = gridDim.x * GPB;
 
-    // Tile group g: one 8-column tile, or (SwiGLU) a gate tile and its up tile.
+    // Tile group g: one 8-column tile, or (SwiGLU) a gate tile and its up
+    // tile; the block's GPB groups are consecutive and their tiles form one
+    // stream of TPB tiles.
     int tile[TPB];
-    if (TPB == 1) {
-        tile[0] = g;
-    } else {
-        tile[0] = 8 * (g >> 2) + (g & 3);
-        tile[TPB - 1] = tile[0] + 4;
+    const uint8_t* tb[TPB];
+#pragma unroll
+    for (int gp = 0; gp < GPB; ++gp) {
+        const int g = g0 + gp;
+        if (TPG == 1) {
+            tile[gp] = g;
+        } else {
+            tile[2 * gp] = 8 * (g >> 2) + (g & 3);
+            tile[2 * gp + 1] = tile[2 * gp] + 4;
+        }
     }
-    const uint8_t* tb0 = P.b + (size_t)tile[0] * CPT * 16;
-    const uint8_t* tb1 = P.b + (size_t)tile[TPB - 1] * CPT * 16;
+#pragma unroll
+    for (int t = 0; t < TPB; ++t) tb[t] = P.b + (size_t)tile[t] * CPT * 16;
+    // Stream position q -> (tile t of the block, chunk within the tile).
+    auto locate = [&](int q, int& t, int& r) {
+        t = 0;
+#pragma unroll
+        for (int i = 1; i < TPB; ++i) t += (q >= i * CPT) ? 1 : 0;
+        r = q - t * CPT;
+    };
+    const uint8_t* tb0 = tb[0];
 
     // 1. Requests go out in the order they are needed, because a wait for a
     // load also waits for every load issued before it: this thread's
@@ -868,14 +884,20 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
     // results masked at use): a load that may be skipped makes every later
     // wait of the compiler assume it was, and a register written on only one
     // side of a branch makes it wait for everything at the join.
-    // A masked-off load reads bytes this thread loads anyway (its first
-    // weight chunk or its column scale), never one shared address: thousands
-    // of requests to one line would queue on one cache channel.
+    // Rounds of activation chunks (and of partial maxima) that hold work for
+    // some thread of the block are requested; the others are not issued at
+    // all (every vector-memory instruction costs the CU's load path, masked
+    // or not). These branches are uniform and precede the weight stream, so
+    // they cannot make the compiler wait on it. Within an issued round a
+    // masked-off lane reads bytes it loads anyway (its first weight chunk or
+    // its column scale), never one shared address: thousands of requests to
+    // one line would queue on one cache channel.
     const uint8_t* own = tb0 + (size_t)min(tid, CPT - 4) * 16;  // 64 readable bytes (CPT >= 16)
     v4u xraw[XMAX][4];
     const T* x = static_cast<const T*>(P.x);
 #pragma unroll
     for (int j = 0; j < XMAX; ++j) {
+        if (256 * j >= chunks) break;
         const int c = tid + 256 * j, kg = c / MR, m = c % MR;
         if (PREQ) {
             const bool ok = c < chunks && m < P.M;
@@ -888,15 +910,17 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
     }
     float pv[MR][PV];
     const float* own_cs = P.colscale + 8 * tile[0] + c8;
-    if (!PREQ) {
+    if (!PREQ && P.part_in) {
 #pragma unroll
-        for (int m = 0; m < MR; ++m)
+        for (int i = 0; i < PV; ++i) {
+            if (256 * i >= P.part_count) break;
 #pragma unroll
-            for (int i = 0; i < PV; ++i) {
+            for (int m = 0; m < MR; ++m) {
                 const int idx = tid + 256 * i;
-                const bool ok = P.part_in && m < P.M && idx < P.part_count;
+                const bool ok = m < P.M && idx < P.part_count;
                 pv[m][i] = *(ok ? P.part_in + (size_t)m * P.part_count + idx : own_cs);  // masked at use
             }
+        }
     }
     // (the empty asm statements keep the compiler from sinking these loads
     // to their first use, which would put them behind the weight stream)
@@ -904,9 +928,13 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
     auto load_window = [&](int w, auto& buf) {
 #pragma unroll
         for (int i = 0; i < RW; ++i) {
-            const int q = (tid + 256 * (w * RW + i)) % CPG;  // past the group: a re-read, skipped
-            const bool second = TPB == 2 && q >= CPT;
-            buf[i] = *reinterpret_cast<const v4u*>((second ? tb1 : tb0) + (size_t)(second ? q - CPT : q) * 16);
+            const int q = (tid + 256 * (w * RW + i)) % CPG;  // past the block's tiles: a re-read, skipped
+            int t, r;
+            locate(q, t, r);
+            const uint8_t* base = tb[0];
+#pragma unroll
+            for (int u = 1; u < TPB; ++u) base = (t == u) ? tb[u] : base;
+            buf[i] = *reinterpret_cast<const v4u*>(base + (size_t)r * 16);
         }
     };
     v4u wa[RW], wb[NW == 2 ? RW : 1];
@@ -1054,8 +1082,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
         for (int i = 0; i < RW; ++i) {
             const int q = tid + 256 * (w * RW + i);
             if (q >= CPG) continue;
-            const bool second = TPB == 2 && q >= CPT;
-            const int pl = (second ? q - CPT : q) >> 3;
+            int tq, rq;
+            locate(q, tq, rq);
+            const int pl = rq >> 3;
             const v4u wv = buf[i];
             int d[MR];
             if (BITS == 8) {
@@ -1088,12 +1117,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
                 }
             }
 #pragma unroll
-            for (int m = 0; m < MR; ++m) {
-                if (second)
-                    acc[TPB - 1][m] += d[m];
-                else
-                    acc[0][m] += d[m];
-            }
+            for (int t = 0; t < TPB; ++t)
+#pragma unroll
+                for (int m = 0; m < MR; ++m) acc[t][m] += (tq == t) ? d[m] : 0;
         }
     };
     // Windows ping-pong between the two register sets (longer K only); with
@@ -1130,28 +1156,33 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
     __builtin_amdgcn_s_barrier();
     if (wave == 0) {
 #pragma unroll
-        for (int m = 0; m < MR; ++m) {
-            const bool row_ok = m < P.M;
-            float y[TPB];
+        for (int gp = 0; gp < GPB; ++gp) {
+            const int g = g0 + gp;
 #pragma unroll
-            for (int t = 0; t < TPB; ++t) {
-                const int tot = red[0][t][m][c8] + red[1][t][m][c8] + red[2][t][m][c8] + red[3][t][m][c8];
-                y[t] = ((float)(tot - corr[m]) * scale[m]) * cs[t];
-            }
-            const int p = 8 * tile[0] + c8;
-            if (EPI == EPI_PLAIN) {
-                if (lane < 8 && row_ok && p < P.N)
-                    store_out(P.c, P.c_type, (size_t)m * P.ldc + orig_col(p, P.half), y[0]);
-            } else {
-                const float o = hm_swiglu(y[0], y[TPB - 1]);
-                if (lane < 8 && row_ok && p < P.N)
-                    store_out(P.c, P.c_type, (size_t)m * P.ldc + ((p >> 6) << 5) + (p & 31), o);
-                if (EPI == EPI_SWIGLU_MAX) {
-                    float mxo = (lane < 8 && p < P.N) ? fabsf(o) : 0.0f;
-                    mxo = fmaxf(mxo, __shfl_xor(mxo, 1));
-                    mxo = fmaxf(mxo, __shfl_xor(mxo, 2));
-                    mxo = fmaxf(mxo, __shfl_xor(mxo, 4));
-                    if (lane == 0) P.part_out[(size_t)m * groups + g] = row_ok ? mxo : 0.0f;
+            for (int m = 0; m < MR; ++m) {
+                const bool row_ok = m < P.M;
+                float y[TPG];
+#pragma unroll
+                for (int t = 0; t < TPG; ++t) {
+                    const int tt = gp * TPG + t;
+                    const int tot = red[0][tt][m][c8] + red[1][tt][m][c8] + red[2][tt][m][c8] + red[3][tt][m][c8];
+                    y[t] = ((float)(tot - corr[m]) * scale[m]) * cs[tt];
+                }
+                const int p = 8 * tile[gp * TPG] + c8;
+                if (EPI == EPI_PLAIN) {
+                    if (lane < 8 && row_ok && p < P.N)
+                        store_out(P.c, P.c_type, (size_t)m * P.ldc + orig_col(p, P.half), y[0]);
+                } else {
+                    const float o = hm_swiglu(y[0], y[TPG - 1]);
+                    if (lane < 8 && row_ok && p < P.N)
+                        store_out(P.c, P.c_type, (size_t)m * P.ldc + ((p >> 6) << 5) + (p & 31), o);
+                    if (EPI == EPI_SWIGLU_MAX) {
+                        float mxo = (lane < 8 && p < P.N) ? fabsf(o) : 0.0f;
+                        mxo = fmaxf(mxo, __shfl_xor(mxo, 1));
+                        mxo = fmaxf(mxo, __shfl_xor(mxo, 2));
+                        mxo = fmaxf(mxo, __shfl_xor(mxo, 4));
+                        if (lane == 0) P.part_out[(size_t)m * groups + g] = row_ok ? mxo : 0.0f;
+                    }
                 }
             }
         }

@@ -50,16 +50,42 @@ static __global__ __launch_bounds__(1024) void moe_route_kernel(RouteParams P) {
         if (in_range && P.routes[a] > 0.0f) atomicAdd(&cnt[e], 1);
     }
     __syncthreads();
-    if (tid == 0) {
-        int run = 0, tiles = 0;
-        for (int e = 0; e < P.experts; ++e) {
-            off[e] = run;
-            toff[e] = tiles;
-            run += cnt[e];
-            tiles += (cnt[e] + P.bm - 1) / P.bm;
+    // Exclusive prefix sums of slots and tiles over the experts: wave 0, each
+    // lane owns MOE_MAX_EXPERTS / 64 consecutive experts, then a wave scan.
+    if (tid < 64) {
+        constexpr int PER = MOE_MAX_EXPERTS / 64;
+        int ls = 0, lt = 0;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int e = tid * PER + i;
+            const int c = e < P.experts ? cnt[e] : 0;
+            ls += c;
+            lt += (c + P.bm - 1) / P.bm;
         }
-        P.counts[0] = run;
-        P.counts[1] = tiles;
+        int is = ls, it = lt;  // inclusive scans over lanes
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int us = __shfl_up(is, d), ut = __shfl_up(it, d);
+            if (tid >= d) {
+                is += us;
+                it += ut;
+            }
+        }
+        int run = is - ls, tiles = it - lt;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int e = tid * PER + i;
+            if (e < P.experts) {
+                off[e] = run;
+                toff[e] = tiles;
+                run += cnt[e];
+                tiles += (cnt[e] + P.bm - 1) / P.bm;
+            }
+        }
+        if (tid == 63) {
+            P.counts[0] = is;
+            P.counts[1] = it;
+        }
     }
     __syncthreads();
     for (int a = tid; a < A; a += 1024) {
