@@ -229,11 +229,91 @@ void weights_destroy(Weights* w) {
         delete static_cast<rk_npu_w4a8_weights*>(w);
 }
 
+// --- launch plans -------------------------------------------------------------
+
+enum GemmVariant { V256x256 = 0, V256x128 = 1, V128x128 = 2, V64x128 = 3, V32x128 = 4 };
+static const int kBM[] = {256, 256, 128, 64, 32};
+static const int kBN[] = {256, 128, 128, 128, 128};
+
+static int env_int(const char* name, int fallback) {
+    const char* v = std::getenv(name);
+    return v ? std::atoi(v) : fallback;
+}
+
+// Activation codes of the whole K live in the GEMV's LDS.
+constexpr int GEMV_MAX_LDS = 60 * 1024;
+
+// GEMM plan for a given variant (-1: chosen by shape). Measured on the
+// Qwen3-4B projection shapes: up to M = 1024 the 4-wave 64x128 tile (wave
+// tile 32x64) leads, since more, smaller tiles keep every CU busy (M = 512:
+// 36 us vs 47 us for 128x128 and 110 us for 256x256 on the 9728x2560 down
+// projection); up to M = 2048 the 4-wave 128x128 tile (the 256x256 tile
+// leaves CUs idle on N = 2560); above that the 8-wave 256x256 tile, 5% ahead
+// of 128x128 over the whole M = 4096 projection set. Rows <= 32 take the
+// 32x128 tile.
+// Split-K (HM_SPLITS) is an experiment switch only: with the device-scope
+// fences its meeting point needs, it measured slower than the unsplit launch
+// on every shape.
+static Plan plan_gemm(int rows, const Geometry& g, int variant) {
+    Plan p{};
+    p.kind = 1;
+    int v = variant;
+    if (v < 0) {
+        const int forced = env_int("HM_GEMM_VARIANT", -1);
+        if (forced >= 0 && forced <= 4)
+            v = forced;
+        else
+            v = rows <= 32 ? V32x128 : rows <= 1024 ? V64x128 : rows <= 2048 ? V128x128 : V256x256;
+    }
+    p.variant = v;
+    p.bm = kBM[v];
+    p.bn = kBN[v];
+    p.tiles = ((rows + p.bm - 1) / p.bm) * (g.N_pad / p.bn);
+    const int KT = g.K_pad / 64;
+    const int forced_f = env_int("HM_SPLITS", 0);
+    p.ksplit = forced_f > 0 ? std::min(forced_f, KT) : 1;
+    p.grid = p.tiles * p.ksplit;
+    return p;
+}
+
+Plan plan_linear(int rows, const Geometry& g) {
+    const int mr = rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : 8;
+    if (rows <= 8 && g.K_pad * mr <= GEMV_MAX_LDS && env_int("HM_FORCE_GEMM", 0) == 0) {
+        Plan p{};
+        p.kind = 0;
+        p.mr = mr;
+        p.ksplit = 1;
+        p.grid = g.N_pad / 8;  // one 8-column tile per block (SwiGLU: a tile pair)
+        p.tiles = p.grid;
+        p.bm = p.mr;
+        p.bn = 8;
+        return p;
+    }
+    return plan_gemm(rows, g, -1);
+}
+
 // --- workspaces -------------------------------------------------------------
 
 struct WsLayout {
-    size_t a, codes, rows, c, part, total;
+    size_t a, codes, rows, c, part, split_cnt, split_part, total;
+    int split_tiles;
+    size_t split_part_ints;
 };
+
+static Plan plan_gemm(int rows, const Geometry& g, int variant);
+
+// Split-K buffers cover the plans of `M` rows for both output alignments.
+static void split_need(const Geometry& g, int M, int& tiles, size_t& ints) {
+    tiles = 0;
+    ints = 0;
+    if (plan_linear(M, g).kind == 0) return;
+    for (int v : {-1, (int)V128x128}) {
+        const Plan p = plan_gemm(M, g, v);
+        if (p.ksplit <= 1) continue;
+        tiles = std::max(tiles, p.tiles);
+        ints = std::max(ints, (size_t)p.tiles * p.ksplit * p.bm * p.bn);
+    }
+}
 
 static WsLayout ws_layout(const Geometry& g, int M) {
     WsLayout L;
@@ -243,7 +323,10 @@ static WsLayout ws_layout(const Geometry& g, int M) {
     L.rows = round_up_z((size_t)M_alloc * 4, 256);
     L.c = round_up_z((size_t)M * g.N * 4, 256);
     L.part = round_up_z((size_t)8 * (g.N_pad / 8) * 4, 256);
-    L.total = L.a + L.codes + 3 * L.rows + L.c + L.part;
+    split_need(g, M, L.split_tiles, L.split_part_ints);
+    L.split_cnt = round_up_z((size_t)L.split_tiles * 4, 256);
+    L.split_part = round_up_z(L.split_part_ints * 4, 256);
+    L.total = L.a + L.codes + 3 * L.rows + L.c + L.part + L.split_cnt + L.split_part;
     return L;
 }
 
@@ -283,6 +366,12 @@ Workspace* workspace_create(Domain* d, int bits, int M, int K, int N) {
     ws->c_f32 = reinterpret_cast<float*>(base + off);
     off += L.c;
     ws->partmax = reinterpret_cast<float*>(base + off);
+    off += L.part;
+    ws->split_cnt = reinterpret_cast<int*>(base + off);
+    off += L.split_cnt;
+    ws->split_part = reinterpret_cast<int*>(base + off);
+    ws->split_tiles = L.split_tiles;
+    ws->split_part_ints = L.split_part_ints;
     // Zero everything once (padding rows of the code planes stay zero).
     bool ok = hipMemset(base, 0, L.total) == hipSuccess &&
               hipStreamCreateWithFlags(&ws->stream, hipStreamNonBlocking) == hipSuccess &&
@@ -306,59 +395,6 @@ void workspace_destroy(Workspace* ws) {
         delete static_cast<rk_npu_matmul_workspace*>(ws);
     else
         delete static_cast<rk_npu_w4a8_workspace*>(ws);
-}
-
-// --- launch plans -------------------------------------------------------------
-
-enum GemmVariant { V256x256 = 0, V256x128 = 1, V128x128 = 2, V64x128 = 3, V32x128 = 4 };
-static const int kBM[] = {256, 256, 128, 64, 32};
-static const int kBN[] = {256, 128, 128, 128, 128};
-
-static int env_int(const char* name, int fallback) {
-    const char* v = std::getenv(name);
-    return v ? std::atoi(v) : fallback;
-}
-
-// Activation codes of the whole K live in the GEMV's LDS.
-constexpr int GEMV_MAX_LDS = 60 * 1024;
-
-Plan plan_linear(int rows, const Geometry& g) {
-    Plan p{};
-    const int mr = rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : 8;
-    if (rows <= 8 && g.K_pad * mr <= GEMV_MAX_LDS && env_int("HM_FORCE_GEMM", 0) == 0) {
-        p.kind = 0;
-        p.mr = mr;
-        p.ksplit = 1;
-        p.grid = g.N_pad / 8;  // one 8-column tile per block (SwiGLU: a tile pair)
-        p.bm = p.mr;
-        p.bn = 8;
-        return p;
-    }
-    p.kind = 1;
-    p.ksplit = 1;
-    int v;
-    const int forced = env_int("HM_GEMM_VARIANT", -1);
-    if (forced >= 0 && forced <= 4) {
-        v = forced;
-    } else if (rows <= 32) {
-        v = V32x128;
-    } else if (rows <= 64) {
-        v = V64x128;
-    } else if (rows <= 128) {
-        v = V128x128;
-    } else {
-        // The 8-wave 256x256 tile runs about 1.4x the MFMA rate of the 4-wave
-        // 256x128 one (measured), so it wins even when its tile count only
-        // fills half of the 256 CUs.
-        const int t256 = ((rows + 255) / 256) * (g.N_pad / 256);
-        const int t256x128 = ((rows + 255) / 256) * (g.N_pad / 128);
-        v = t256 >= 128 ? V256x256 : (t256x128 >= 256 ? V256x128 : V128x128);
-    }
-    p.variant = v;
-    p.bm = kBM[v];
-    p.bn = kBN[v];
-    p.grid = ((rows + p.bm - 1) / p.bm) * (g.N_pad / p.bn);
-    return p;
 }
 
 // --- enqueue ------------------------------------------------------------------
@@ -409,23 +445,30 @@ int enqueue_quant(Workspace* ws, const void* x, int x_type, long lda, int rows, 
     return hipGetLastError() == hipSuccess ? RK_NPU_OK : RK_NPU_ERR_DEVICE;
 }
 
+// Outputs without a 16-byte aligned base and row pitch take the 128x128
+// tile with per-lane stores (staged = false); all other launches stage rows
+// through LDS.
 template <int BITS, int EPI>
-static void launch_gemm(int v, const GemmParams& G, int grid, hipStream_t s) {
+static void launch_gemm(int v, bool staged, const GemmParams& G, int grid, hipStream_t s) {
+    if (!staged) {
+        hipLaunchKernelGGL((gemm_kernel<128, 128, 2, 2, BITS, EPI, false>), dim3(grid), dim3(256), 0, s, G);
+        return;
+    }
     switch (v) {
         case V256x256:
-            hipLaunchKernelGGL((gemm_kernel<256, 256, 2, 4, BITS, EPI>), dim3(grid), dim3(512), 0, s, G);
+            hipLaunchKernelGGL((gemm_kernel<256, 256, 2, 4, BITS, EPI, true>), dim3(grid), dim3(512), 0, s, G);
             break;
         case V256x128:
-            hipLaunchKernelGGL((gemm_kernel<256, 128, 2, 2, BITS, EPI>), dim3(grid), dim3(256), 0, s, G);
+            hipLaunchKernelGGL((gemm_kernel<256, 128, 2, 2, BITS, EPI, true>), dim3(grid), dim3(256), 0, s, G);
             break;
         case V128x128:
-            hipLaunchKernelGGL((gemm_kernel<128, 128, 2, 2, BITS, EPI>), dim3(grid), dim3(256), 0, s, G);
+            hipLaunchKernelGGL((gemm_kernel<128, 128, 2, 2, BITS, EPI, true>), dim3(grid), dim3(256), 0, s, G);
             break;
         case V64x128:
-            hipLaunchKernelGGL((gemm_kernel<64, 128, 1, 2, BITS, EPI>), dim3(grid), dim3(128), 0, s, G);
+            hipLaunchKernelGGL((gemm_kernel<64, 128, 2, 2, BITS, EPI, true>), dim3(grid), dim3(256), 0, s, G);
             break;
         default:
-            hipLaunchKernelGGL((gemm_kernel<32, 128, 1, 2, BITS, EPI>), dim3(grid), dim3(128), 0, s, G);
+            hipLaunchKernelGGL((gemm_kernel<32, 128, 1, 2, BITS, EPI, true>), dim3(grid), dim3(128), 0, s, G);
             break;
     }
 }
@@ -483,8 +526,8 @@ static void launch_gemv_epi(int epi, int mr, const GemvParams& V, int grid, size
 int enqueue_linear(Workspace* ws, const Weights* w, const void* x, int x_type, long lda, int rows, int rule,
                    RowMax in_max, void* c, int c_type, long ldc, int epi, RowMax* out_max, hipStream_t s) {
     const Geometry& g = w->g;
-    const Plan p = plan_linear(rows, g);
-    if (p.kind == 0) {
+    const Plan pv = plan_linear(rows, g);
+    if (pv.kind == 0) {
         GemvParams V;
         V.x = x;
         V.lda = lda;
@@ -510,33 +553,43 @@ int enqueue_linear(Workspace* ws, const Weights* w, const void* x, int x_type, l
         V.diag_rowsum = ws->rowsum;
         V.M_alloc = ws->M_alloc;
         const int grid = epi == EPI_PLAIN ? g.N_pad / 8 : g.N_pad / 16;
-        const size_t lds = (size_t)g.K_pad * p.mr;
+        const size_t lds = (size_t)g.K_pad * pv.mr;
         // Rows the kernel cannot quantize from registers (unaligned or ragged
         // rows, or more than GEMV_XMAX chunks per thread) are quantized first.
-        const bool preq = !V.vec || (g.K_pad / 16) * p.mr > 256 * GEMV_XMAX;
+        const bool preq = !V.vec || (g.K_pad / 16) * pv.mr > 256 * GEMV_XMAX;
         if (preq) {
             int rc = enqueue_quant(ws, x, x_type, lda, rows, rule, in_max, nullptr, s);
             if (rc != RK_NPU_OK) return rc;
         }
         char name[64];
-        std::snprintf(name, sizeof(name), "gemv<mr=%d,w%d,epi=%d>", p.mr, g.bits, epi);
+        std::snprintf(name, sizeof(name), "gemv<mr=%d,w%d,epi=%d>", pv.mr, g.bits, epi);
         const int slot = prof_begin(s, 0, g.bits, epi, rows, g.K, g.N, name);
         if (x_type == DT_F32) {
             if (g.bits == 8)
-                launch_gemv_epi<float, 8>(epi, p.mr, V, grid, lds, s, preq);
+                launch_gemv_epi<float, 8>(epi, pv.mr, V, grid, lds, s, preq);
             else
-                launch_gemv_epi<float, 4>(epi, p.mr, V, grid, lds, s, preq);
+                launch_gemv_epi<float, 4>(epi, pv.mr, V, grid, lds, s, preq);
         } else {
             if (g.bits == 8)
-                launch_gemv_epi<__half, 8>(epi, p.mr, V, grid, lds, s, preq);
+                launch_gemv_epi<__half, 8>(epi, pv.mr, V, grid, lds, s, preq);
             else
-                launch_gemv_epi<__half, 4>(epi, p.mr, V, grid, lds, s, preq);
+                launch_gemv_epi<__half, 4>(epi, pv.mr, V, grid, lds, s, preq);
         }
         prof_end(slot, s);
         if (out_max) *out_max = RowMax{ws->partmax, grid};
     } else {
         int rc = enqueue_quant(ws, x, x_type, lda, rows, rule, in_max, epi != EPI_PLAIN ? ws->rowmax : nullptr, s);
         if (rc != RK_NPU_OK) return rc;
+        const size_t c_esz = c_type == DT_F32 ? 4 : 2;
+        const bool staged = (reinterpret_cast<uintptr_t>(c) & 15) == 0 && ((size_t)ldc * c_esz) % 16 == 0;
+        Plan p = staged ? plan_linear(rows, g) : plan_gemm(rows, g, V128x128);
+        // Split-K buffers are sized for the workspace's own row count; a plan
+        // that needs more runs unsplit (same result, integer sums are exact).
+        if (p.ksplit > 1 && (p.tiles > ws->split_tiles ||
+                             (size_t)p.tiles * p.ksplit * p.bm * p.bn > ws->split_part_ints)) {
+            p.ksplit = 1;
+            p.grid = p.tiles;
+        }
         GemmParams G;
         G.a = ws->codes;
         G.b = w->packed;
@@ -555,14 +608,17 @@ int enqueue_linear(Workspace* ws, const Weights* w, const void* x, int x_type, l
         G.rowmax = ws->rowmax;
         G.tiles_m = (rows + p.bm - 1) / p.bm;
         G.tiles_n = g.N_pad / p.bn;
+        G.splits = p.ksplit;
+        G.split_cnt = ws->split_cnt;
+        G.split_part = ws->split_part;
         char name[64];
-        std::snprintf(name, sizeof(name), "gemm<%dx%d,w%d,epi=%d>", p.bm, p.bn, g.bits, epi);
+        std::snprintf(name, sizeof(name), "gemm<%dx%d,w%d,epi=%d,k/%d>", p.bm, p.bn, g.bits, epi, p.ksplit);
         const int slot = prof_begin(s, 1, g.bits, epi, rows, g.K, g.N, name);
-#define HM_GEMM(B)                                                   \
-    if (epi == EPI_PLAIN)                                            \
-        launch_gemm<B, EPI_PLAIN>(p.variant, G, p.grid, s);          \
-    else                                                             \
-        launch_gemm<B, EPI_SWIGLU_MAX>(p.variant, G, p.grid, s);
+#define HM_GEMM(B)                                                           \
+    if (epi == EPI_PLAIN)                                                    \
+        launch_gemm<B, EPI_PLAIN>(p.variant, staged, G, p.grid, s);          \
+    else                                                                     \
+        launch_gemm<B, EPI_SWIGLU_MAX>(p.variant, staged, G, p.grid, s);
         if (g.bits == 8) {
             HM_GEMM(8)
         } else {

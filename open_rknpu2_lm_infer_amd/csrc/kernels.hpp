@@ -359,12 +359,14 @@ static __global__ __launch_bounds__(256) void pack_w4_kernel(PackParams P) {
 // ---------------------------------------------------------------------------
 // Prefill GEMM on MFMA: v_mfma_i32_32x32x32_i8, int32 accumulation.
 // Block tile BM x BN, K step 64, WGM x WGN waves, wave tile (BM/WGM) x (BN/WGN).
-// A and B tiles go global -> registers -> LDS (two stages, one barrier per
-// K step); every LDS fragment read is a 16-byte read at consecutive addresses
-// for each half-wave. The W4 B tile stays packed in LDS (half the bytes) and
-// is unpacked in registers: one 16-byte entry feeds both 32-k MFMA steps.
+// The W4 B tile stays packed in LDS (half the bytes) and is unpacked in
+// registers: one 16-byte entry feeds both 32-k MFMA steps.
 // Epilogue: optional W4 offset correction, dequant (f32(acc)*s_row)*s_col,
 // and plain / SwiGLU / SwiGLU+row-max stores.
+// Split-K: with splits > 1 block b computes K range piece b / tiles of tile
+// b % tiles; the pieces' int32 partials meet in split_part and the piece that
+// arrives last (split_cnt[tile]) finishes the tile. Integer sums are exact, so
+// the output does not depend on the split.
 // ---------------------------------------------------------------------------
 struct GemmParams {
     const int8_t* a;
@@ -378,6 +380,9 @@ struct GemmParams {
     int M, N, K_pad, M_alloc, N_pad, half;
     unsigned* rowmax;
     int tiles_m, tiles_n;
+    int splits;       // K pieces per tile (1: no split)
+    int* split_cnt;   // [tiles], zero between launches
+    int* split_part;  // [tiles][splits][BM*BN] int32 partials
 };
 
 // Main loop shared by the dense and the grouped GEMM: accumulates the
@@ -409,6 +414,10 @@ struct TileCfg {
     // as many stages as fit in 128 KB of LDS, at most 4
     static constexpr int STAGES = (4 * STAGE <= 131072) ? 4 : (3 * STAGE <= 131072 ? 3 : 2);
     static constexpr int LDS = STAGES * STAGE;
+    // Shared memory of a block: the stage ring, or the epilogue's staging of
+    // 32 rows per wave (f32, worst case) when that is larger.
+    static constexpr int EPI_ROW = TN * 4 + 16;
+    static constexpr int SMEM = LDS > WGM * WGN * 32 * EPI_ROW ? LDS : WGM * WGN * 32 * EPI_ROW;
     static_assert(A_STAGE % (16 * NT) == 0 && B_STAGE % (16 * NT) == 0, "tile/thread mismatch");
     static_assert(BN % 64 == 0, "a wave's B loads must cover one plane");
     static_assert(LPS * (STAGES - 1) <= 63, "vmcnt range");
@@ -588,7 +597,7 @@ __device__ __forceinline__ EpiPre<BM, BN, WGM, WGN, BITS> epilogue_prefetch(cons
 // Epilogue of a finished tile: dequantize (two RNE multiplies, row scale then
 // column scale), optional SwiGLU with the row max of |out| for the next
 // quantization, and the store.
-template <int BM, int BN, int WGM, int WGN, int BITS, int EPI, typename RowMap>
+template <int BM, int BN, int WGM, int WGN, int BITS, int EPI, bool STAGED, typename RowMap>
 __device__ __forceinline__ void gemm_epilogue(
     const v16i (&acc)[TileCfg<BM, BN, WGM, WGN, BITS>::FM][TileCfg<BM, BN, WGM, WGN, BITS>::FN], int n0,
     const EpiPre<BM, BN, WGM, WGN, BITS>& pre, int N, int half, void* c, long ldc, int c_type, unsigned* rowmax,
@@ -606,14 +615,14 @@ __device__ __forceinline__ void gemm_epilogue(
     const int out0 = (EPI == EPI_PLAIN) ? n0 + wn * TN : (n0 + wn * TN) >> 1;
     const int n_out = (EPI == EPI_PLAIN) ? N : N / 2;
 
-    // Rows are staged through LDS (SwiGLU values in f32, so the row max is
-    // taken on exact values; plain values in the output type) and written as
-    // 16-byte runs when the output allows it (16-byte aligned base and row
-    // pitch); otherwise each lane stores its own elements. Values and
-    // rounding are identical either way.
-    const bool staged = ((reinterpret_cast<uintptr_t>(c) & 15) == 0) && ((((size_t)ldc * esz) & 15) == 0);
+    // STAGED (the output has a 16-byte aligned base and row pitch): rows are
+    // staged through LDS (SwiGLU values in f32, so the row max is taken on
+    // exact values; plain values in the output type) and written as 16-byte
+    // runs. Otherwise each lane stores its own elements. Values and rounding
+    // are identical either way.
+    constexpr bool staged = STAGED;
     const int ssz = (EPI == EPI_PLAIN) ? esz : 4;  // staged element size
-    constexpr int WAVE_LDS = C::LDS / NW;
+    constexpr int WAVE_LDS = C::SMEM / NW;
     constexpr int FIT = WAVE_LDS / (32 * (OUTC * 4 + 16));
     static_assert(FIT >= 1, "epilogue staging does not fit in LDS");
     constexpr int FPI = FIT >= FM ? FM : ((FIT >= 2 && FM % 2 == 0) ? 2 : 1);
@@ -641,7 +650,7 @@ __device__ __forceinline__ void gemm_epilogue(
 #pragma unroll
                     for (int j = 0; j < FN; ++j) {
                         const float y = ((float)(acc[i][j][r] - corr) * s_row) * pre.cs[j];
-                        if (staged) {
+                        if constexpr (staged) {
                             store_out(lrow, c_type, j * 32 + l32, y);
                         } else {
                             const int p = n0 + wn * TN + j * 32 + l32;
@@ -657,7 +666,7 @@ __device__ __forceinline__ void gemm_epilogue(
                         const float g = ((float)(acc[i][j][r] - corr) * s_row) * pre.cs[j];
                         const float u = ((float)(acc[i][j + 1][r] - corr) * s_row) * pre.cs[j + 1];
                         const float o = hm_swiglu(g, u);
-                        if (staged) {
+                        if constexpr (staged) {
                             reinterpret_cast<float*>(lrow)[(j >> 1) * 32 + l32] = o;
                         } else {
                             const int p = n0 + wn * TN + j * 32 + l32;
@@ -667,7 +676,7 @@ __device__ __forceinline__ void gemm_epilogue(
                                 store_out(c, c_type, (size_t)out_row * ldc + ((p >> 6) << 5) + l32, o);
                         }
                     }
-                    if (EPI == EPI_SWIGLU_MAX && !staged) {
+                    if constexpr (EPI == EPI_SWIGLU_MAX && !staged) {
 #pragma unroll
                         for (int off = 16; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
                         int out_row, src_row;
@@ -676,7 +685,7 @@ __device__ __forceinline__ void gemm_epilogue(
                 }
             }
         }
-        if (!staged) continue;
+        if constexpr (!staged) continue;
         __syncthreads();
         if (EPI == EPI_PLAIN) {
             // 16-byte runs: chunk q of the staged rows -> (row, 16/esz columns).
@@ -737,17 +746,66 @@ __device__ __forceinline__ void gemm_epilogue(
     }
 }
 
-template <int BM, int BN, int WGM, int WGN, int BITS, int EPI>
+// Split-K meeting point of one tile: every piece stores its int32 partial
+// (16 bytes per lane, fragment order), then counts itself in; the piece that
+// arrives last adds the other pieces' partials to its own accumulators and
+// returns true (it finishes the tile and re-arms the counter), the others
+// return false. Release (store, fence, count) and acquire (count, fence, load)
+// are at device scope, so pieces may run on any XCD. No piece waits for
+// another.
+template <int FM, int FN, int NT>
+__device__ __forceinline__ bool split_meet(v16i (&acc)[FM][FN], int* __restrict__ part, int* cnt, int splits,
+                                           int piece) {
+    constexpr int TILE = FM * FN * 16 * NT;  // ints per partial
+    const int tid = threadIdx.x;
+    __shared__ int s_last;
+    int* mine = part + (size_t)piece * TILE;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int h = 0; h < 4; ++h) {
+                const v4i v = {acc[i][j][4 * h], acc[i][j][4 * h + 1], acc[i][j][4 * h + 2], acc[i][j][4 * h + 3]};
+                *reinterpret_cast<v4i*>(mine + ((size_t)((i * FN + j) * 4 + h) * NT + tid) * 4) = v;
+            }
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) s_last = atomicAdd(cnt, 1) == splits - 1;
+    __syncthreads();
+    if (!s_last) return false;
+    __threadfence();
+    for (int q = 0; q < splits; ++q) {
+        if (q == piece) continue;
+        const int* other = part + (size_t)q * TILE;
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int h = 0; h < 4; ++h) {
+                    const v4i v = *reinterpret_cast<const v4i*>(other + ((size_t)((i * FN + j) * 4 + h) * NT + tid) * 4);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[i][j][4 * h + e] += v[e];
+                }
+    }
+    if (tid == 0) atomicExch(cnt, 0);
+    return true;
+}
+
+template <int BM, int BN, int WGM, int WGN, int BITS, int EPI, bool STAGED>
 __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_kernel(GemmParams P) {
     using C = TileCfg<BM, BN, WGM, WGN, BITS>;
     static_assert(EPI == EPI_PLAIN || C::FN % 2 == 0, "SwiGLU pairs need an even fragment count");
-    __shared__ __attribute__((aligned(16))) uint8_t smem[C::LDS];
+    __shared__ __attribute__((aligned(16))) uint8_t smem[C::SMEM];
 
-    // Block -> tile: give each of the 8 XCDs (blocks are dealt round-robin)
-    // a contiguous range of tile ids, then walk groups of 8 M-tiles so that
-    // neighbouring tiles share weight panels in the XCD's L2.
+    // Block -> (K piece, tile). Tiles: give each of the 8 XCDs (blocks are
+    // dealt round-robin) a contiguous range of tile ids, then walk groups of
+    // 8 M-tiles so that neighbouring tiles share weight panels in the XCD's
+    // L2. Pieces are the outer index, so blocks of one piece share K ranges.
     const int T = P.tiles_m * P.tiles_n;
-    const int bid = blockIdx.x;
+    const int piece = blockIdx.x / T;
+    const int bid = blockIdx.x - piece * T;
     const int per = T >> 3;
     const int tile = (bid < (per << 3)) ? ((bid & 7) * per + (bid >> 3)) : bid;
     constexpr int G = 8;
@@ -758,6 +816,10 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_kernel(GemmParams P) {
     const int tm = first_m + in_g % gm;
     const int tn = in_g / gm;
     const int m0 = tm * BM, n0 = tn * BN;
+    const int KT_all = P.K_pad >> 6;
+    const int k0 = (int)((long)KT_all * piece / P.splits);
+    const int k1 = (int)((long)KT_all * (piece + 1) / P.splits);
+    constexpr int PPS = (BITS == 8) ? 4 : 2;  // weight planes per 64-k step
 
     size_t a_off[C::A_LOADS];
 #pragma unroll
@@ -780,9 +842,14 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_kernel(GemmParams P) {
         return row < M;
     };
     const auto pre = epilogue_prefetch<BM, BN, WGM, WGN, BITS>(P.rowscale, P.rowsum, P.colscale, n0, row_of);
-    gemm_mainloop<BM, BN, WGM, WGN, BITS>(smem, P.a, (size_t)P.M_alloc, a_off, P.b, P.K_pad, n0, P.K_pad >> 6, acc);
-    gemm_epilogue<BM, BN, WGM, WGN, BITS, EPI>(acc, n0, pre, P.N, P.half, P.c, P.ldc, P.c_type, P.rowmax, row_of,
-                                               smem);
+    gemm_mainloop<BM, BN, WGM, WGN, BITS>(smem, P.a + (size_t)k0 * 64 * P.M_alloc, (size_t)P.M_alloc, a_off,
+                                          P.b + (size_t)k0 * PPS * 128, P.K_pad, n0, k1 - k0, acc);
+    if (P.splits > 1 &&
+        !split_meet<C::FM, C::FN, C::NT>(acc, P.split_part + (size_t)tile * P.splits * BM * BN,
+                                          P.split_cnt + tile, P.splits, piece))
+        return;
+    gemm_epilogue<BM, BN, WGM, WGN, BITS, EPI, STAGED>(acc, n0, pre, P.N, P.half, P.c, P.ldc, P.c_type, P.rowmax,
+                                                       row_of, smem);
 }
 
 // ---------------------------------------------------------------------------

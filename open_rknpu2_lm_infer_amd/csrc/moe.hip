@@ -286,7 +286,11 @@ static void work_destroy(MoeWork* ws) {
 template <int BITS, int EPI>
 static void launch_moe_gemm(const MoeGemmParams& G, int grid, hipStream_t s, int rows) {
     const int slot = prof_begin(s, 3, BITS, EPI, rows, G.K_pad, G.N, EPI == EPI_PLAIN ? "moe_gemm<down>" : "moe_gemm<gate_up>");
-    hipLaunchKernelGGL((moe_gemm_kernel<MOE_BM, MOE_BN, 1, 2, BITS, EPI>), dim3(grid), dim3(128), 0, s, G);
+    const size_t esz = G.c_type == DT_F32 ? 4 : 2;
+    if ((reinterpret_cast<uintptr_t>(G.c) & 15) == 0 && ((size_t)G.ldc * esz) % 16 == 0)
+        hipLaunchKernelGGL((moe_gemm_kernel<MOE_BM, MOE_BN, 1, 2, BITS, EPI, true>), dim3(grid), dim3(128), 0, s, G);
+    else
+        hipLaunchKernelGGL((moe_gemm_kernel<MOE_BM, MOE_BN, 1, 2, BITS, EPI, false>), dim3(grid), dim3(128), 0, s, G);
     prof_end(slot, s);
 }
 

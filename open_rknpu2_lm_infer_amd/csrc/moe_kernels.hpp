@@ -130,10 +130,10 @@ struct MoeGemmParams {
     int N, K_pad, N_pad, half, tiles_n;
 };
 
-template <int BM, int BN, int WGM, int WGN, int BITS, int EPI>
+template <int BM, int BN, int WGM, int WGN, int BITS, int EPI, bool STAGED>
 __global__ __launch_bounds__(WGM* WGN * 64, 1) void moe_gemm_kernel(MoeGemmParams P) {
     using C = TileCfg<BM, BN, WGM, WGN, BITS>;
-    __shared__ __attribute__((aligned(16))) uint8_t smem[C::LDS];
+    __shared__ __attribute__((aligned(16))) uint8_t smem[C::SMEM];
     __shared__ int s_rows[BM];
     const int t = blockIdx.x / P.tiles_n, tn = blockIdx.x % P.tiles_n;
     if (t >= P.counts[1]) return;
@@ -166,8 +166,8 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void moe_gemm_kernel(MoeGemmParam
     const auto pre = epilogue_prefetch<BM, BN, WGM, WGN, BITS>(P.rowscale, P.rowsum, P.s_tab[e], n0, row_of);
     gemm_mainloop<BM, BN, WGM, WGN, BITS>(smem, P.a, (size_t)P.a_alloc, a_off, P.b_tab[e], P.K_pad, n0, P.K_pad >> 6,
                                           acc);
-    gemm_epilogue<BM, BN, WGM, WGN, BITS, EPI>(acc, n0, pre, P.N, P.half, P.c, P.ldc, P.c_type, P.rowmax, row_of,
-                                               smem);
+    gemm_epilogue<BM, BN, WGM, WGN, BITS, EPI, STAGED>(acc, n0, pre, P.N, P.half, P.c, P.ldc, P.c_type, P.rowmax,
+                                                       row_of, smem);
 }
 
 // ---------------------------------------------------------------------------

@@ -83,6 +83,10 @@ struct Workspace {
     unsigned* rowmax; // [M_alloc]  max|middle| of a fused SwiGLU output
     float* c_f32;     // [M][N]   output staging / fused middle
     float* partmax;   // [8][N_pad/8] per-block max|middle| of a GEMV SwiGLU
+    int* split_cnt;   // [split_tiles] split-K arrival counters (zero between launches)
+    int* split_part;  // split-K int32 partials
+    int split_tiles;        // counters available
+    size_t split_part_ints; // partial ints available
 };
 
 size_t workspace_bytes(const Geometry& g, int M);
@@ -97,9 +101,10 @@ struct Plan {
     int kind;  // 0 GEMV, 1 GEMM
     int bm, bn;
     int mr;
-    int ksplit;
+    int ksplit;  // GEMM: K pieces per tile
     int grid;
     int variant;
+    int tiles;   // GEMM: output tiles
 };
 Plan plan_linear(int rows, const Geometry& g);
 

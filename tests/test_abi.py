@@ -107,8 +107,13 @@ def test_plans():
     # a K too long for the GEMV's quantized rows in LDS (8 x 9728 bytes) takes the GEMM
     assert L.rk_npu_hip_linear_plan(8, 9728, 2560, 8, ctypes.byref(plan)) == 0
     assert (plan.kind, plan.block_m, plan.block_n) == (1, 32, 128)
+    # 64x128 tiles up to 1024 rows, 128x128 up to 2048, then 256x256; no K split
+    assert L.rk_npu_hip_linear_plan(512, 9728, 2560, 8, ctypes.byref(plan)) == 0
+    assert (plan.kind, plan.block_m, plan.block_n, plan.k_splits, plan.grid) == (1, 64, 128, 1, 8 * 20)
+    assert L.rk_npu_hip_linear_plan(2048, 9728, 2560, 8, ctypes.byref(plan)) == 0
+    assert (plan.kind, plan.block_m, plan.block_n, plan.k_splits, plan.grid) == (1, 128, 128, 1, 16 * 20)
     assert L.rk_npu_hip_linear_plan(4096, 2560, 9728, 8, ctypes.byref(plan)) == 0
-    assert plan.kind == 1 and plan.block_m == 256 and plan.block_n == 256
+    assert (plan.kind, plan.block_m, plan.block_n, plan.k_splits) == (1, 256, 256, 1)
     assert L.rk_npu_hip_linear_plan(0, 2560, 9728, 8, ctypes.byref(plan)) == F.RK_NPU_ERR_PARAM
 
 

@@ -42,6 +42,62 @@ def test_device_linear_matches_oracle_f32_and_f16(ctx, bits, rows):
     assert np.array_equal(y16.cpu().numpy(), ref.astype(np.float16))
 
 
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("rows", [1100, 2100])
+def test_device_linear_large_row_tiles(ctx, bits, rows):
+    """Row counts that select the 128x128 (<= 2048 rows) and 256x256 tiles."""
+    k, n = 640, 768
+    codes, scales = R.weights(5, f"dl{bits}", bits, k, n)
+    w = ctx.weights(bits, dev(codes), dev(scales))
+    x = R.activations(5, f"dlL-x{rows}", rows, k)
+    y = torch.empty(rows, n, dtype=torch.float32, device="cuda")
+    D.linear(ctx, w, dev(x), y, rows)
+    torch.cuda.synchronize()
+    assert np.array_equal(y.cpu().numpy(), oracle.linear(codes, scales, x))
+    m = torch.empty(rows, n // 2, dtype=torch.float32, device="cuda")
+    D.linear(ctx, w, dev(x), m, rows, swiglu=True)
+    torch.cuda.synchronize()
+    assert np.array_equal(m.cpu().numpy(), oracle.linear_swiglu(codes, scales, x))
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
+def test_unaligned_output_matches_oracle(ctx, bits, dtype):
+    """An output base off 16-byte alignment takes the per-lane store epilogue."""
+    rows, k, n = 300, 640, 768
+    codes, scales = R.weights(5, f"dl{bits}", bits, k, n)
+    w = ctx.weights(bits, dev(codes), dev(scales))
+    x = R.activations(5, f"dlU-x{rows}", rows, k)
+    t = torch.float16 if dtype == "f16" else torch.float32
+    for swiglu, width, ref in ((False, n, oracle.linear(codes, scales, x)),
+                               (True, n // 2, oracle.linear_swiglu(codes, scales, x))):
+        buf = torch.zeros(rows * width + 1, dtype=t, device="cuda")
+        y = buf[1:].view(rows, width)
+        D.linear(ctx, w, dev(x), y, rows, swiglu=swiglu)
+        torch.cuda.synchronize()
+        assert buf[0].item() == 0
+        assert np.array_equal(y.cpu().numpy(), ref.astype(np.float16) if dtype == "f16" else ref)
+
+
+@pytest.mark.parametrize("splits", [2, 3])
+def test_split_k_switch_is_bit_exact(ctx, splits, monkeypatch):
+    """HM_SPLITS: K pieces per tile meet through int32 partials; same result."""
+    monkeypatch.setenv("HM_SPLITS", str(splits))
+    local = D.DeviceContext(3)  # workspaces sized under the switch
+    rows, k, n = 300, 640, 768
+    for bits in (4, 8):
+        codes, scales = R.weights(5, f"dl{bits}", bits, k, n)
+        w = local.weights(bits, dev(codes), dev(scales))
+        x = R.activations(5, f"dlS-x{rows}", rows, k)
+        y = torch.empty(rows, n, dtype=torch.float16, device="cuda")
+        D.linear(local, w, dev(x).half(), y, rows)
+        m = torch.empty(rows, n // 2, dtype=torch.float32, device="cuda")
+        D.linear(local, w, dev(x), m, rows, swiglu=True)
+        torch.cuda.synchronize()
+        assert np.array_equal(y.cpu().numpy(), oracle.linear(codes, scales, x).astype(np.float16))
+        assert np.array_equal(m.cpu().numpy(), oracle.linear_swiglu(codes, scales, x))
+
+
 @pytest.mark.parametrize("rows", [1, 4, 64])
 def test_device_ffn_matches_oracle(ctx, rows):
     h, f = 512, 768
