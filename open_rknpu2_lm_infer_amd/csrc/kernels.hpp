@@ -173,6 +173,29 @@ __device__ __forceinline__ void cvt16_raw(const v4u (&r)[4], float (&v)[16], __h
     }
 }
 
+// 16 values -> 16 int8 codes (q = clamp(round(v * inv), +-127), dense rule
+// rounding half away from zero, MoE rule half to even), sum += codes.
+template <int RULE>
+__device__ __forceinline__ v4u quant_chunk(const float (&v)[16], float inv, int& sum) {
+    unsigned packed[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int b = 0; b < 16; ++b) {
+        float q = v[b] * inv;
+        q = (RULE == QUANT_DENSE) ? roundf(q) : __builtin_rintf(q);
+        q = fminf(fmaxf(q, -127.0f), 127.0f);
+        const int qi = (int)q;
+        sum += qi;
+        packed[b >> 2] |= ((unsigned)qi & 0xffu) << ((b & 3) * 8);
+    }
+    return v4u{packed[0], packed[1], packed[2], packed[3]};
+}
+
+template <int RULE>
+__device__ __forceinline__ float quant_scale(float m) {
+    if (RULE == QUANT_DENSE) return (m == 0.0f) ? 1.0f : fmaxf(m / 127.0f, FLT_MIN);
+    return (m == 0.0f) ? 1.0f : m / 127.0f;
+}
+
 template <typename T, int RULE, int TPR>
 __global__ __launch_bounds__(256) void quant_rows_kernel(QuantParams P) {
     constexpr int J = QUANT_CHUNKS;  // chunks per thread held in registers
@@ -246,29 +269,14 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantParams P) {
         __syncthreads();
         m = fmaxf(fmaxf(s_max[0], s_max[1]), fmaxf(s_max[2], s_max[3]));
     }
-    float sc;
-    if (RULE == QUANT_DENSE)
-        sc = (m == 0.0f) ? 1.0f : fmaxf(m / 127.0f, FLT_MIN);
-    else
-        sc = (m == 0.0f) ? 1.0f : m / 127.0f;
+    const float sc = quant_scale<RULE>(m);
     const float inv = 1.0f / sc;
     if (tid == 0) P.rowscale[r] = sc;
 
     // 2. Quantize each chunk into its 16-byte entry.
     int sum = 0;
     auto quantize = [&](int kg, const float (&v)[16]) {
-        unsigned packed[4] = {0u, 0u, 0u, 0u};
-#pragma unroll
-        for (int b = 0; b < 16; ++b) {
-            float q = v[b] * inv;
-            q = (RULE == QUANT_DENSE) ? roundf(q) : __builtin_rintf(q);
-            q = fminf(fmaxf(q, -127.0f), 127.0f);
-            const int qi = (int)q;
-            sum += qi;
-            packed[b >> 2] |= ((unsigned)qi & 0xffu) << ((b & 3) * 8);
-        }
-        *reinterpret_cast<v4u*>(P.codes + ((size_t)kg * P.M_alloc + r) * 16) =
-            v4u{packed[0], packed[1], packed[2], packed[3]};
+        *reinterpret_cast<v4u*>(P.codes + ((size_t)kg * P.M_alloc + r) * 16) = quant_chunk<RULE>(v, inv, sum);
     };
 #pragma unroll
     for (int j = 0; j < J; ++j) {
@@ -291,6 +299,112 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantParams P) {
         sum = s_sum[0] + s_sum[1] + s_sum[2] + s_sum[3];
     }
     if (tid == 0) P.rowsum[r] = sum;
+}
+
+// Row-tiled quantization for many rows: a block quantizes RB rows, 256/RB
+// threads per row, and writes the code planes [K_pad/16][M_alloc][16] as
+// RB*16-byte runs (one plane of its RB rows) through an LDS transpose, instead
+// of one 16-byte entry per cache line. Loads stay contiguous along each row.
+// The row max comes from precomputed maxima (HAS_MAX, any K: one streaming
+// pass, NI groups of loads in flight) or from the row itself, held in
+// registers (at most NI groups of 256/RB chunks). Values and rounding are
+// those of quant_rows_kernel. Needs 16-byte aligned rows with K % 16 == 0.
+template <typename T, int RULE, int RB, int NI, bool HAS_MAX>
+__global__ __launch_bounds__(256) void quant_tile_kernel(QuantParams P) {
+    constexpr int TW = 256 / RB;    // threads (chunk columns) per row
+    constexpr int PITCH = RB + 1;   // LDS entries per chunk column (padding against bank conflicts)
+    __shared__ v4u s_codes[2][TW * PITCH];
+    const T* x = static_cast<const T*>(P.x);
+    const int t = threadIdx.x;
+    const int ri = t / TW, cg = t % TW;  // row in block, chunk column
+    const int r0 = blockIdx.x * RB, r = r0 + ri;
+    const int rows = P.rows_dev ? min(P.rows, *P.rows_dev) : P.rows;
+    if (r0 >= rows) {
+        if (P.rowmax_clear && cg == 0 && r < P.M_alloc) P.rowmax_clear[r] = 0u;
+        return;  // uniform over the block
+    }
+    const bool live = r < rows;
+    const int KG = P.K_pad >> 4;
+    const int groups = (KG + TW - 1) / TW;
+    const T* xr = x + (size_t)(live ? r : r0) * P.lda;
+    auto ok = [&](int kg) { return live && kg * 16 < P.K; };
+
+    float m = 0.0f;
+    v4u raw[NI][4];
+    if (HAS_MAX) {
+        const float* pr = P.part_in + (size_t)(live ? r : r0) * P.part_count;
+        for (int i = cg; i < P.part_count; i += TW) m = fmaxf(m, pr[i]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int kg = i * TW + cg;
+            load16_raw(ok(kg) ? xr + kg * 16 : xr, raw[i]);
+        }
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int kg = i * TW + cg;
+            if (!ok(kg)) continue;
+            float v[16];
+            cvt16_raw(raw[i], v, T());
+#pragma unroll
+            for (int b = 0; b < 16; ++b) m = fmaxf(m, fabsf(v[b]));
+        }
+    }
+#pragma unroll
+    for (int off = TW / 2; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    if (P.rowmax_clear && cg == 0) P.rowmax_clear[r] = 0u;
+    const float sc = quant_scale<RULE>(m);
+    const float inv = 1.0f / sc;
+    int sum = 0;
+    // Group g: chunk g*TW+cg of every row -> LDS -> TW planes of RB rows.
+    auto emit = [&](int g, float (&v)[16]) {
+        const int kg = g * TW + cg;
+        if (!ok(kg)) {
+#pragma unroll
+            for (int b = 0; b < 16; ++b) v[b] = 0.0f;
+        }
+        v4u* buf = s_codes[g & 1];
+        buf[cg * PITCH + ri] = quant_chunk<RULE>(v, inv, sum);
+        __syncthreads();
+        // thread t stores plane t / RB of row t % RB
+        const int pk = g * TW + t / RB;
+        if (pk < KG)
+            *reinterpret_cast<v4u*>(P.codes + ((size_t)pk * P.M_alloc + r0 + t % RB) * 16) =
+                buf[(t / RB) * PITCH + t % RB];
+    };
+    if constexpr (HAS_MAX) {
+        // batches of NI groups: all of a batch's loads are issued first
+        for (int g0 = 0; g0 < groups; g0 += NI) {
+#pragma unroll
+            for (int i = 0; i < NI; ++i) {
+                const int kg = (g0 + i) * TW + cg;
+                load16_raw(ok(kg) ? xr + kg * 16 : xr, raw[i]);
+            }
+            asm volatile("" ::: "memory");
+#pragma unroll
+            for (int i = 0; i < NI; ++i) {
+                if (g0 + i >= groups) break;
+                float v[16];
+                cvt16_raw(raw[i], v, T());
+                emit(g0 + i, v);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int g = 0; g < NI; ++g) {
+            if (g >= groups) break;
+            float v[16];
+            cvt16_raw(raw[g], v, T());
+            emit(g, v);
+        }
+    }
+#pragma unroll
+    for (int off = TW / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+    if (live && cg == 0) {
+        P.rowscale[r] = sc;
+        P.rowsum[r] = sum;
+    }
 }
 
 // ---------------------------------------------------------------------------

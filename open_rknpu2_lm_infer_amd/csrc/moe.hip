@@ -15,7 +15,7 @@ namespace hm {
 constexpr uint32_t MAGIC_MOE_W = 0x574d4841u;
 constexpr uint32_t MAGIC_MOE_WS = 0x534d4841u;
 constexpr uint32_t BLOB_MAGIC = 0x31584d48u;  // "HMX1"
-constexpr int MOE_BM = 32, MOE_BN = 128;
+constexpr int MOE_BM = 64, MOE_BN = 128;
 
 // One routed expert in device memory: [gate_up payload | gate_up scales |
 // down payload | down scales], each region 256-byte aligned.
@@ -288,9 +288,9 @@ static void launch_moe_gemm(const MoeGemmParams& G, int grid, hipStream_t s, int
     const int slot = prof_begin(s, 3, BITS, EPI, rows, G.K_pad, G.N, EPI == EPI_PLAIN ? "moe_gemm<down>" : "moe_gemm<gate_up>");
     const size_t esz = G.c_type == DT_F32 ? 4 : 2;
     if ((reinterpret_cast<uintptr_t>(G.c) & 15) == 0 && ((size_t)G.ldc * esz) % 16 == 0)
-        hipLaunchKernelGGL((moe_gemm_kernel<MOE_BM, MOE_BN, 1, 2, BITS, EPI, true>), dim3(grid), dim3(128), 0, s, G);
+        hipLaunchKernelGGL((moe_gemm_kernel<MOE_BM, MOE_BN, 2, 2, BITS, EPI, true>), dim3(grid), dim3(256), 0, s, G);
     else
-        hipLaunchKernelGGL((moe_gemm_kernel<MOE_BM, MOE_BN, 1, 2, BITS, EPI, false>), dim3(grid), dim3(128), 0, s, G);
+        hipLaunchKernelGGL((moe_gemm_kernel<MOE_BM, MOE_BN, 2, 2, BITS, EPI, false>), dim3(grid), dim3(256), 0, s, G);
     prof_end(slot, s);
 }
 
