@@ -173,17 +173,27 @@ __device__ __forceinline__ void cvt16_raw(const v4u (&r)[4], float (&v)[16], __h
     }
 }
 
-// 16 values -> 16 int8 codes (q = clamp(round(v * inv), +-127), dense rule
-// rounding half away from zero, MoE rule half to even), sum += codes.
+// Code of one scaled value, q = clamp(round(s), +-127) with the dense rule's
+// rounding (half away from zero) or the MoE rule's (half to even). Clamping
+// first is equivalent (the bounds are integers). For a value already in
+// [-127, 127], trunc(q + copysign(0x1.fffffep-2, q)) is exactly roundf(q):
+// the sum is exact or rounds within the integer interval except at q = n - 0.5,
+// where it reaches n; adding 0.5 instead would send 0x1.fffffep-2 to 1. (The
+// identity is checked over every float of the range by the test suite.)
+template <int RULE>
+__device__ __forceinline__ int quant_code(float s) {
+    const float q = fminf(fmaxf(s, -127.0f), 127.0f);
+    if (RULE == QUANT_DENSE) return (int)(q + __builtin_copysignf(0x1.fffffep-2f, q));
+    return (int)__builtin_rintf(q);
+}
+
+// 16 values -> 16 int8 codes of v * inv, sum += codes.
 template <int RULE>
 __device__ __forceinline__ v4u quant_chunk(const float (&v)[16], float inv, int& sum) {
     unsigned packed[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
     for (int b = 0; b < 16; ++b) {
-        float q = v[b] * inv;
-        q = (RULE == QUANT_DENSE) ? roundf(q) : __builtin_rintf(q);
-        q = fminf(fmaxf(q, -127.0f), 127.0f);
-        const int qi = (int)q;
+        const int qi = quant_code<RULE>(v[b] * inv);
         sum += qi;
         packed[b >> 2] |= ((unsigned)qi & 0xffu) << ((b & 3) * 8);
     }
@@ -1220,10 +1230,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
             int sum = 0;
 #pragma unroll
             for (int b = 0; b < 16; ++b) {
-                float q = v[b] * iv;
-                q = (P.rule == QUANT_DENSE) ? roundf(q) : __builtin_rintf(q);
-                q = fminf(fmaxf(q, -127.0f), 127.0f);
-                const int qi = (int)q;
+                const float sv = v[b] * iv;
+                const int qi = (P.rule == QUANT_DENSE) ? quant_code<QUANT_DENSE>(sv) : quant_code<QUANT_MOE>(sv);
                 sum += qi;
                 packed[b >> 2] |= ((unsigned)qi & 0xffu) << ((b & 3) * 8);
             }
