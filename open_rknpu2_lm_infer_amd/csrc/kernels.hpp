@@ -187,15 +187,27 @@ __device__ __forceinline__ int quant_code(float s) {
     return (int)__builtin_rintf(q);
 }
 
+// Low bytes of four codes as one word (v_perm_b32: byte i of the result is
+// byte sel_i of {second operand bytes 0-3, first operand bytes 4-7}, 0x0c
+// gives zero), and the sum of a word's four signed bytes (v_dot4 with ones).
+__device__ __forceinline__ unsigned pack4(int a, int b, int c, int d) {
+    const unsigned ab = __builtin_amdgcn_perm((unsigned)b, (unsigned)a, 0x0c0c0400u);
+    const unsigned cd = __builtin_amdgcn_perm((unsigned)d, (unsigned)c, 0x0c0c0400u);
+    return __builtin_amdgcn_perm(cd, ab, 0x05040100u);
+}
+__device__ __forceinline__ int sum4(unsigned w, int acc) {
+    return __builtin_amdgcn_sdot4((int)w, 0x01010101, acc, false);
+}
+
 // 16 values -> 16 int8 codes of v * inv, sum += codes.
 template <int RULE>
 __device__ __forceinline__ v4u quant_chunk(const float (&v)[16], float inv, int& sum) {
-    unsigned packed[4] = {0u, 0u, 0u, 0u};
+    unsigned packed[4];
 #pragma unroll
-    for (int b = 0; b < 16; ++b) {
-        const int qi = quant_code<RULE>(v[b] * inv);
-        sum += qi;
-        packed[b >> 2] |= ((unsigned)qi & 0xffu) << ((b & 3) * 8);
+    for (int w = 0; w < 4; ++w) {
+        packed[w] = pack4(quant_code<RULE>(v[4 * w] * inv), quant_code<RULE>(v[4 * w + 1] * inv),
+                          quant_code<RULE>(v[4 * w + 2] * inv), quant_code<RULE>(v[4 * w + 3] * inv));
+        sum = sum4(packed[w], sum);
     }
     return v4u{packed[0], packed[1], packed[2], packed[3]};
 }
@@ -1226,15 +1238,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
             float iv = inv[0];
 #pragma unroll
             for (int r = 1; r < MR; ++r) iv = (r == m) ? inv[r] : iv;
-            unsigned packed[4] = {0u, 0u, 0u, 0u};
             int sum = 0;
-#pragma unroll
-            for (int b = 0; b < 16; ++b) {
-                const float sv = v[b] * iv;
-                const int qi = (P.rule == QUANT_DENSE) ? quant_code<QUANT_DENSE>(sv) : quant_code<QUANT_MOE>(sv);
-                sum += qi;
-                packed[b >> 2] |= ((unsigned)qi & 0xffu) << ((b & 3) * 8);
-            }
+            const v4u pk = (P.rule == QUANT_DENSE) ? quant_chunk<QUANT_DENSE>(v, iv, sum)
+                                                   : quant_chunk<QUANT_MOE>(v, iv, sum);
+            const unsigned packed[4] = {pk[0], pk[1], pk[2], pk[3]};
 #pragma unroll
             for (int r = 0; r < MR; ++r) psum[r] += (r == m) ? sum : 0;
             *reinterpret_cast<v4u*>(sa + c * 16) = v4u{packed[0], packed[1], packed[2], packed[3]};
