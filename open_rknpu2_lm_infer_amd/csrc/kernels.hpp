@@ -93,16 +93,59 @@ __device__ __forceinline__ float to_f32<__half>(__half v) {
     return __half2float(v);
 }
 
+// Cross-lane reductions on DPP moves (no LDS round trip): quad_perm
+// [1,0,3,2] and [2,3,0,1] reduce lanes within a quad, row_half_mirror within
+// 8 lanes, row_mirror within a 16-lane row, row_bcast:15 / row_bcast:31 carry
+// row results upward so lane 63 ends with the whole wave's; lanes a move does
+// not write keep their own value (the operation's identity on itself).
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ int dpp_move(int v) {
+    return __builtin_amdgcn_update_dpp(v, v, CTRL, ROW_MASK, 0xf, false);
+}
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp_move(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v),
+                                                                 CTRL, ROW_MASK, 0xf, false));
+}
+constexpr int DPP_QUAD_XOR1 = 0xB1, DPP_QUAD_XOR2 = 0x4E, DPP_ROW_HALF_MIRROR = 0x141, DPP_ROW_MIRROR = 0x140,
+              DPP_ROW_BCAST15 = 0x142, DPP_ROW_BCAST31 = 0x143;
+
+// Sum over the 8 lanes of the wave that share lane % 8, in each of them:
+// row_ror:8 pairs lanes 8 apart within a 16-lane row; v_permlane16_swap /
+// v_permlane32_swap exchange odd with even rows / the upper with the lower
+// half, so the two halves of each swap add to the pair's sum.
+__device__ __forceinline__ int sum_mod8(int v) {
+    v += __builtin_amdgcn_update_dpp(v, v, 0x128, 0xf, 0xf, false);  // row_ror:8
+    const auto a = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    v = (int)a[0] + (int)a[1];
+    const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return (int)b[0] + (int)b[1];
+}
+
+// max over each aligned group of 8 lanes, in every lane of the group
+__device__ __forceinline__ float max8(float v) {
+    v = fmaxf(v, dpp_move<DPP_QUAD_XOR1>(v));
+    v = fmaxf(v, dpp_move<DPP_QUAD_XOR2>(v));
+    return fmaxf(v, dpp_move<DPP_ROW_HALF_MIRROR>(v));
+}
+
 __device__ __forceinline__ int wave_sum(int v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-    return v;
+    v += dpp_move<DPP_QUAD_XOR1>(v);
+    v += dpp_move<DPP_QUAD_XOR2>(v);
+    v += dpp_move<DPP_ROW_HALF_MIRROR>(v);
+    v += dpp_move<DPP_ROW_MIRROR>(v);
+    // rows 1 and 3 add the row below; then rows 2 and 3 add row 1's total
+    v += __builtin_amdgcn_update_dpp(0, v, DPP_ROW_BCAST15, 0xa, 0xf, false);
+    v += __builtin_amdgcn_update_dpp(0, v, DPP_ROW_BCAST31, 0xc, 0xf, false);
+    return __builtin_amdgcn_readlane(v, 63);
 }
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
-    return v;
+    v = max8(v);
+    v = fmaxf(v, dpp_move<DPP_ROW_MIRROR>(v));
+    v = fmaxf(v, dpp_move<DPP_ROW_BCAST15, 0xa>(v));
+    v = fmaxf(v, dpp_move<DPP_ROW_BCAST31, 0xc>(v));
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
 // ---------------------------------------------------------------------------
@@ -373,8 +416,12 @@ __global__ __launch_bounds__(256) void quant_tile_kernel(QuantParams P) {
             for (int b = 0; b < 16; ++b) m = fmaxf(m, fabsf(v[b]));
         }
     }
+    if constexpr (TW == 64) {
+        m = wave_max(m);
+    } else {
 #pragma unroll
-    for (int off = TW / 2; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+        for (int off = TW / 2; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    }
     if (P.rowmax_clear && cg == 0) P.rowmax_clear[r] = 0u;
     const float sc = quant_scale<RULE>(m);
     const float inv = 1.0f / sc;
@@ -421,8 +468,12 @@ __global__ __launch_bounds__(256) void quant_tile_kernel(QuantParams P) {
             emit(g, v);
         }
     }
+    if constexpr (TW == 64) {
+        sum = wave_sum(sum);
+    } else {
 #pragma unroll
-    for (int off = TW / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+        for (int off = TW / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+    }
     if (live && cg == 0) {
         P.rowscale[r] = sc;
         P.rowsum[r] = sum;
@@ -872,8 +923,12 @@ __device__ __forceinline__ void gemm_epilogue(
                     for (int t = 0; t < valid; ++t) store_out(c, c_type, (size_t)out_row * ldc + col + t, vv[t]);
                 }
                 if (EPI == EPI_SWIGLU_MAX) {
+                    if constexpr (CPR == 8) {
+                        mx = max8(mx);
+                    } else {
 #pragma unroll
-                    for (int off = 1; off < CPR; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+                        for (int off = 1; off < CPR; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+                    }
                     if ((lane % CPR) == 0 && row_ok) atomicMax(rowmax + out_row, __float_as_uint(mx));
                 }
             }
@@ -1336,16 +1391,14 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
         }
     }
 
-    // 5. Reduce over threads of the same column: shuffles within a wave, LDS
+    // 5. Reduce over threads of the same column: lane moves within a wave, LDS
     // across waves; wave 0 finishes the 8 columns.
 #pragma unroll
     for (int t = 0; t < TPB; ++t)
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
             int v = acc[t][m];
-            v += __shfl_xor(v, 8);
-            v += __shfl_xor(v, 16);
-            v += __shfl_xor(v, 32);
+            v = sum_mod8(v);
             if (lane < 8) red[wave][t][m][c8] = v;
         }
     wait_lgkmcnt0();
@@ -1374,9 +1427,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
                         store_out(P.c, P.c_type, (size_t)m * P.ldc + ((p >> 6) << 5) + (p & 31), o);
                     if (EPI == EPI_SWIGLU_MAX) {
                         float mxo = (lane < 8 && p < P.N) ? fabsf(o) : 0.0f;
-                        mxo = fmaxf(mxo, __shfl_xor(mxo, 1));
-                        mxo = fmaxf(mxo, __shfl_xor(mxo, 2));
-                        mxo = fmaxf(mxo, __shfl_xor(mxo, 4));
+                        mxo = max8(mxo);
                         if (lane == 0) P.part_out[(size_t)m * groups + g] = row_ok ? mxo : 0.0f;
                     }
                 }
