@@ -107,6 +107,50 @@ static __global__ __launch_bounds__(1024) void moe_route_kernel(RouteParams P) {
 }
 
 // ---------------------------------------------------------------------------
+// Gather of the quantized token rows into slot order (slot s holds token
+// perm[s] / top): thread = one slot and GATHER_PLANES consecutive planes
+// (one index load, then independent 16-byte loads); consecutive threads take
+// consecutive slots, so every plane's writes are contiguous and the grouped
+// gate/up GEMM then reads contiguous A rows. Scales and code sums follow their
+// rows.
+// ---------------------------------------------------------------------------
+constexpr int GATHER_PLANES = 2;
+
+struct GatherParams {
+    const int8_t* src;
+    const float* src_scale;
+    const int* src_sum;
+    int src_alloc;
+    const int* perm;
+    int top;
+    const int* counts;  // [0] slots used
+    int8_t* dst;
+    float* dst_scale;
+    int* dst_sum;
+    int dst_alloc;
+    int planes;
+};
+
+static __global__ __launch_bounds__(256) void moe_gather_kernel(GatherParams P) {
+    const int s = blockIdx.x * 256 + threadIdx.x;
+    const int p0 = blockIdx.y * GATHER_PLANES;
+    if (s >= P.counts[0]) return;
+    const int tok = P.perm[s] / P.top;
+    v4u v[GATHER_PLANES];
+#pragma unroll
+    for (int i = 0; i < GATHER_PLANES; ++i)
+        if (p0 + i < P.planes)
+            v[i] = *reinterpret_cast<const v4u*>(P.src + ((size_t)(p0 + i) * P.src_alloc + tok) * 16);
+#pragma unroll
+    for (int i = 0; i < GATHER_PLANES; ++i)
+        if (p0 + i < P.planes) *reinterpret_cast<v4u*>(P.dst + ((size_t)(p0 + i) * P.dst_alloc + s) * 16) = v[i];
+    if (blockIdx.y == 0) {
+        P.dst_scale[s] = P.src_scale[tok];
+        P.dst_sum[s] = P.src_sum[tok];
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Grouped GEMM: block = (m-tile of one expert's slot run, n-tile). Gather mode
 // (perm != nullptr) reads A row perm[slot] / top (the token's quantized input
 // row); otherwise A row = slot (the requantized middle). Blocks past the
