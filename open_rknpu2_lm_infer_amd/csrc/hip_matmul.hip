@@ -251,9 +251,24 @@ constexpr int GEMV_MAX_LDS = 60 * 1024;
 // leaves CUs idle on N = 2560); above that the 8-wave 256x256 tile, 5% ahead
 // of 128x128 over the whole M = 4096 projection set. Rows <= 32 take the
 // 32x128 tile.
-// Split-K (HM_SPLITS) is an experiment switch only: with the device-scope
-// fences its meeting point needs, it measured slower than the unsplit launch
-// on every shape.
+// Split-K (two launches: partials, then sum + epilogue) when the tiles leave
+// CUs idle and K is long: measured on 9728x2560 it takes M=512 from 45 to
+// 38 us (3 pieces) and M=64 from 38 to 22 us (6 pieces); with K <= 4096 or
+// as many tiles as CUs the partial traffic costs more than it saves.
+// HM_SPLITS forces a piece count (experiments).
+static int device_cus() {
+    static std::atomic<int> cached{0};
+    int c = cached.load();
+    if (c > 0) return c;
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+        n = 256;  // MI355X
+    (void)hipGetLastError();
+    cached.store(n);
+    return n;
+}
+
 static Plan plan_gemm(int rows, const Geometry& g, int variant) {
     Plan p{};
     p.kind = 1;
@@ -270,8 +285,12 @@ static Plan plan_gemm(int rows, const Geometry& g, int variant) {
     p.bn = kBN[v];
     p.tiles = ((rows + p.bm - 1) / p.bm) * (g.N_pad / p.bn);
     const int KT = g.K_pad / 64;
+    const int cus = device_cus();
+    int f = 1;
+    if ((v == V64x128 || v == V128x128) && p.tiles < cus && KT >= 128)
+        f = std::max(1, std::min(std::min((3 * cus / 2 + p.tiles - 1) / p.tiles, KT / 24), 8));
     const int forced_f = env_int("HM_SPLITS", 0);
-    p.ksplit = forced_f > 0 ? std::min(forced_f, KT) : 1;
+    p.ksplit = forced_f > 0 ? std::min(forced_f, KT) : f;
     p.grid = p.tiles * p.ksplit;
     return p;
 }
@@ -295,24 +314,16 @@ Plan plan_linear(int rows, const Geometry& g) {
 // --- workspaces -------------------------------------------------------------
 
 struct WsLayout {
-    size_t a, codes, rows, c, part, split_cnt, split_part, total;
-    int split_tiles;
+    size_t a, codes, rows, c, part, split_part, total;
     size_t split_part_ints;
 };
 
 static Plan plan_gemm(int rows, const Geometry& g, int variant);
 
-// Split-K buffers cover the plans of `M` rows for both output alignments.
-static void split_need(const Geometry& g, int M, int& tiles, size_t& ints) {
-    tiles = 0;
-    ints = 0;
-    if (plan_linear(M, g).kind == 0) return;
-    for (int v : {-1, (int)V128x128}) {
-        const Plan p = plan_gemm(M, g, v);
-        if (p.ksplit <= 1) continue;
-        tiles = std::max(tiles, p.tiles);
-        ints = std::max(ints, (size_t)p.tiles * p.ksplit * p.bm * p.bn);
-    }
+// Split-K partials cover the plan of `M` rows.
+static size_t split_need(const Geometry& g, int M) {
+    const Plan p = plan_linear(M, g);
+    return (p.kind == 1 && p.ksplit > 1) ? (size_t)p.tiles * p.ksplit * p.bm * p.bn : 0;
 }
 
 static WsLayout ws_layout(const Geometry& g, int M) {
@@ -323,10 +334,9 @@ static WsLayout ws_layout(const Geometry& g, int M) {
     L.rows = round_up_z((size_t)M_alloc * 4, 256);
     L.c = round_up_z((size_t)M * g.N * 4, 256);
     L.part = round_up_z((size_t)8 * (g.N_pad / 8) * 4, 256);
-    split_need(g, M, L.split_tiles, L.split_part_ints);
-    L.split_cnt = round_up_z((size_t)L.split_tiles * 4, 256);
+    L.split_part_ints = split_need(g, M);
     L.split_part = round_up_z(L.split_part_ints * 4, 256);
-    L.total = L.a + L.codes + 3 * L.rows + L.c + L.part + L.split_cnt + L.split_part;
+    L.total = L.a + L.codes + 3 * L.rows + L.c + L.part + L.split_part;
     return L;
 }
 
@@ -367,10 +377,7 @@ Workspace* workspace_create(Domain* d, int bits, int M, int K, int N) {
     off += L.c;
     ws->partmax = reinterpret_cast<float*>(base + off);
     off += L.part;
-    ws->split_cnt = reinterpret_cast<int*>(base + off);
-    off += L.split_cnt;
     ws->split_part = reinterpret_cast<int*>(base + off);
-    ws->split_tiles = L.split_tiles;
     ws->split_part_ints = L.split_part_ints;
     // Zero everything once (padding rows of the code planes stay zero).
     bool ok = hipMemset(base, 0, L.total) == hipSuccess &&
@@ -488,28 +495,44 @@ int enqueue_quant(Workspace* ws, const void* x, int x_type, long lda, int rows, 
 
 // Outputs without a 16-byte aligned base and row pitch take the 128x128
 // tile with per-lane stores (staged = false); all other launches stage rows
-// through LDS.
+// through LDS. A split plan (64x128 / 128x128 tiles, staged) is two launches:
+// the K pieces' partials, then the per-tile sum and epilogue.
+template <int BM, int BN, int WGM, int WGN, int BITS, int EPI>
+static void launch_split(const GemmParams& G, int tiles, hipStream_t s) {
+    hipLaunchKernelGGL((gemm_kernel<BM, BN, WGM, WGN, BITS, EPI_PLAIN, true, SPLIT_PART>), dim3(tiles * G.splits),
+                       dim3(WGM * WGN * 64), 0, s, G);
+    hipLaunchKernelGGL((gemm_kernel<BM, BN, WGM, WGN, BITS, EPI, true, SPLIT_FINISH>), dim3(tiles),
+                       dim3(WGM * WGN * 64), 0, s, G);
+}
+
 template <int BITS, int EPI>
-static void launch_gemm(int v, bool staged, const GemmParams& G, int grid, hipStream_t s) {
+static void launch_gemm(int v, bool staged, const GemmParams& G, int tiles, hipStream_t s) {
     if (!staged) {
-        hipLaunchKernelGGL((gemm_kernel<128, 128, 2, 2, BITS, EPI, false>), dim3(grid), dim3(256), 0, s, G);
+        hipLaunchKernelGGL((gemm_kernel<128, 128, 2, 2, BITS, EPI, false>), dim3(tiles), dim3(256), 0, s, G);
+        return;
+    }
+    if (G.splits > 1) {
+        if (v == V64x128)
+            launch_split<64, 128, 2, 2, BITS, EPI>(G, tiles, s);
+        else
+            launch_split<128, 128, 2, 2, BITS, EPI>(G, tiles, s);
         return;
     }
     switch (v) {
         case V256x256:
-            hipLaunchKernelGGL((gemm_kernel<256, 256, 2, 4, BITS, EPI, true>), dim3(grid), dim3(512), 0, s, G);
+            hipLaunchKernelGGL((gemm_kernel<256, 256, 2, 4, BITS, EPI, true>), dim3(tiles), dim3(512), 0, s, G);
             break;
         case V256x128:
-            hipLaunchKernelGGL((gemm_kernel<256, 128, 2, 2, BITS, EPI, true>), dim3(grid), dim3(256), 0, s, G);
+            hipLaunchKernelGGL((gemm_kernel<256, 128, 2, 2, BITS, EPI, true>), dim3(tiles), dim3(256), 0, s, G);
             break;
         case V128x128:
-            hipLaunchKernelGGL((gemm_kernel<128, 128, 2, 2, BITS, EPI, true>), dim3(grid), dim3(256), 0, s, G);
+            hipLaunchKernelGGL((gemm_kernel<128, 128, 2, 2, BITS, EPI, true>), dim3(tiles), dim3(256), 0, s, G);
             break;
         case V64x128:
-            hipLaunchKernelGGL((gemm_kernel<64, 128, 2, 2, BITS, EPI, true>), dim3(grid), dim3(256), 0, s, G);
+            hipLaunchKernelGGL((gemm_kernel<64, 128, 2, 2, BITS, EPI, true>), dim3(tiles), dim3(256), 0, s, G);
             break;
         default:
-            hipLaunchKernelGGL((gemm_kernel<32, 128, 1, 2, BITS, EPI, true>), dim3(grid), dim3(128), 0, s, G);
+            hipLaunchKernelGGL((gemm_kernel<32, 128, 1, 2, BITS, EPI, true>), dim3(tiles), dim3(128), 0, s, G);
             break;
     }
 }
@@ -624,9 +647,10 @@ int enqueue_linear(Workspace* ws, const Weights* w, const void* x, int x_type, l
         const size_t c_esz = c_type == DT_F32 ? 4 : 2;
         const bool staged = (reinterpret_cast<uintptr_t>(c) & 15) == 0 && ((size_t)ldc * c_esz) % 16 == 0;
         Plan p = staged ? plan_linear(rows, g) : plan_gemm(rows, g, V128x128);
-        // Split-K buffers are sized for the workspace's own row count; a plan
-        // that needs more runs unsplit (same result, integer sums are exact).
-        if (p.ksplit > 1 && (p.tiles > ws->split_tiles ||
+        // Split-K: staged 64x128 / 128x128 plans only, partials sized for the
+        // workspace's own row count; otherwise the launch runs unsplit (same
+        // result: the integer sums are exact).
+        if (p.ksplit > 1 && (!staged || (p.variant != V64x128 && p.variant != V128x128) ||
                              (size_t)p.tiles * p.ksplit * p.bm * p.bn > ws->split_part_ints)) {
             p.ksplit = 1;
             p.grid = p.tiles;
@@ -650,16 +674,15 @@ int enqueue_linear(Workspace* ws, const Weights* w, const void* x, int x_type, l
         G.tiles_m = (rows + p.bm - 1) / p.bm;
         G.tiles_n = g.N_pad / p.bn;
         G.splits = p.ksplit;
-        G.split_cnt = ws->split_cnt;
         G.split_part = ws->split_part;
         char name[64];
         std::snprintf(name, sizeof(name), "gemm<%dx%d,w%d,epi=%d,k/%d>", p.bm, p.bn, g.bits, epi, p.ksplit);
         const int slot = prof_begin(s, 1, g.bits, epi, rows, g.K, g.N, name);
 #define HM_GEMM(B)                                                           \
     if (epi == EPI_PLAIN)                                                    \
-        launch_gemm<B, EPI_PLAIN>(p.variant, staged, G, p.grid, s);          \
+        launch_gemm<B, EPI_PLAIN>(p.variant, staged, G, p.tiles, s);         \
     else                                                                     \
-        launch_gemm<B, EPI_SWIGLU_MAX>(p.variant, staged, G, p.grid, s);
+        launch_gemm<B, EPI_SWIGLU_MAX>(p.variant, staged, G, p.tiles, s);
         if (g.bits == 8) {
             HM_GEMM(8)
         } else {

@@ -550,10 +550,8 @@ static __global__ __launch_bounds__(256) void pack_w4_kernel(PackParams P) {
 // registers: one 16-byte entry feeds both 32-k MFMA steps.
 // Epilogue: optional W4 offset correction, dequant (f32(acc)*s_row)*s_col,
 // and plain / SwiGLU / SwiGLU+row-max stores.
-// Split-K: with splits > 1 block b computes K range piece b / tiles of tile
-// b % tiles; the pieces' int32 partials meet in split_part and the piece that
-// arrives last (split_cnt[tile]) finishes the tile. Integer sums are exact, so
-// the output does not depend on the split.
+// Split-K (see gemm_kernel's SPLIT modes): integer sums are exact, so the
+// output does not depend on the split.
 // ---------------------------------------------------------------------------
 struct GemmParams {
     const int8_t* a;
@@ -568,8 +566,7 @@ struct GemmParams {
     unsigned* rowmax;
     int tiles_m, tiles_n;
     int splits;       // K pieces per tile (1: no split)
-    int* split_cnt;   // [tiles], zero between launches
-    int* split_part;  // [tiles][splits][BM*BN] int32 partials
+    int* split_part;  // [splits][tiles][BM*BN] int32 partials
 };
 
 // Main loop shared by the dense and the grouped GEMM: accumulates the
@@ -937,57 +934,26 @@ __device__ __forceinline__ void gemm_epilogue(
     }
 }
 
-// Split-K meeting point of one tile: every piece stores its int32 partial
-// (16 bytes per lane, fragment order), then counts itself in; the piece that
-// arrives last adds the other pieces' partials to its own accumulators and
-// returns true (it finishes the tile and re-arms the counter), the others
-// return false. Release (store, fence, count) and acquire (count, fence, load)
-// are at device scope, so pieces may run on any XCD. No piece waits for
-// another.
+// Split-K in two launches: SPLIT_PART blocks compute K piece b / tiles of
+// tile b % tiles and store the int32 accumulators (16 bytes per lane,
+// fragment order, [piece][tile][BM*BN]); one SPLIT_FINISH block per tile then
+// sums the pieces (exact integer sums, in piece order) and runs the epilogue.
+// The launch boundary orders the two, so no block waits for another and no
+// device-scope fence is needed.
+enum { SPLIT_NONE = 0, SPLIT_PART = 1, SPLIT_FINISH = 2 };
+
 template <int FM, int FN, int NT>
-__device__ __forceinline__ bool split_meet(v16i (&acc)[FM][FN], int* __restrict__ part, int* cnt, int splits,
-                                           int piece) {
-    constexpr int TILE = FM * FN * 16 * NT;  // ints per partial
-    const int tid = threadIdx.x;
-    __shared__ int s_last;
-    int* mine = part + (size_t)piece * TILE;
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-#pragma unroll
-            for (int h = 0; h < 4; ++h) {
-                const v4i v = {acc[i][j][4 * h], acc[i][j][4 * h + 1], acc[i][j][4 * h + 2], acc[i][j][4 * h + 3]};
-                *reinterpret_cast<v4i*>(mine + ((size_t)((i * FN + j) * 4 + h) * NT + tid) * 4) = v;
-            }
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) s_last = atomicAdd(cnt, 1) == splits - 1;
-    __syncthreads();
-    if (!s_last) return false;
-    __threadfence();
-    for (int q = 0; q < splits; ++q) {
-        if (q == piece) continue;
-        const int* other = part + (size_t)q * TILE;
-#pragma unroll
-        for (int i = 0; i < FM; ++i)
-#pragma unroll
-            for (int j = 0; j < FN; ++j)
-#pragma unroll
-                for (int h = 0; h < 4; ++h) {
-                    const v4i v = *reinterpret_cast<const v4i*>(other + ((size_t)((i * FN + j) * 4 + h) * NT + tid) * 4);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) acc[i][j][4 * h + e] += v[e];
-                }
-    }
-    if (tid == 0) atomicExch(cnt, 0);
-    return true;
+__device__ __forceinline__ v4i* part_slot(int* part, size_t tile_ints, int q, int T, int tile, int i, int j, int h) {
+    return reinterpret_cast<v4i*>(part + ((size_t)q * T + tile) * tile_ints +
+                                  ((size_t)((i * FN + j) * 4 + h) * NT + threadIdx.x) * 4);
 }
 
-template <int BM, int BN, int WGM, int WGN, int BITS, int EPI, bool STAGED>
+template <int BM, int BN, int WGM, int WGN, int BITS, int EPI, bool STAGED, int SPLIT = SPLIT_NONE>
 __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_kernel(GemmParams P) {
     using C = TileCfg<BM, BN, WGM, WGN, BITS>;
     static_assert(EPI == EPI_PLAIN || C::FN % 2 == 0, "SwiGLU pairs need an even fragment count");
+    constexpr int FM = C::FM, FN = C::FN, NT = C::NT;
+    constexpr size_t TILE_INTS = (size_t)BM * BN;
     __shared__ __attribute__((aligned(16))) uint8_t smem[C::SMEM];
 
     // Block -> (K piece, tile). Tiles: give each of the 8 XCDs (blocks are
@@ -995,7 +961,7 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_kernel(GemmParams P) {
     // 8 M-tiles so that neighbouring tiles share weight panels in the XCD's
     // L2. Pieces are the outer index, so blocks of one piece share K ranges.
     const int T = P.tiles_m * P.tiles_n;
-    const int piece = blockIdx.x / T;
+    const int piece = SPLIT == SPLIT_PART ? blockIdx.x / T : 0;
     const int bid = blockIdx.x - piece * T;
     const int per = T >> 3;
     const int tile = (bid < (per << 3)) ? ((bid & 7) * per + (bid >> 3)) : bid;
@@ -1007,22 +973,12 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_kernel(GemmParams P) {
     const int tm = first_m + in_g % gm;
     const int tn = in_g / gm;
     const int m0 = tm * BM, n0 = tn * BN;
-    const int KT_all = P.K_pad >> 6;
-    const int k0 = (int)((long)KT_all * piece / P.splits);
-    const int k1 = (int)((long)KT_all * (piece + 1) / P.splits);
-    constexpr int PPS = (BITS == 8) ? 4 : 2;  // weight planes per 64-k step
 
-    size_t a_off[C::A_LOADS];
+    v16i acc[FM][FN];
 #pragma unroll
-    for (int i = 0; i < C::A_LOADS; ++i) {
-        const int c = threadIdx.x + i * C::NT;
-        a_off[i] = (size_t)(c / BM) * P.M_alloc + m0 + c % BM;
-    }
-    v16i acc[C::FM][C::FN];
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int i = 0; i < C::FM; ++i)
-#pragma unroll
-        for (int j = 0; j < C::FN; ++j)
+        for (int j = 0; j < FN; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
     const int M = P.M;
@@ -1032,15 +988,59 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_kernel(GemmParams P) {
         src_row = row < M ? row : 0;
         return row < M;
     };
-    const auto pre = epilogue_prefetch<BM, BN, WGM, WGN, BITS>(P.rowscale, P.rowsum, P.colscale, n0, row_of);
+
+    if constexpr (SPLIT == SPLIT_FINISH) {
+        const auto pre = epilogue_prefetch<BM, BN, WGM, WGN, BITS>(P.rowscale, P.rowsum, P.colscale, n0, row_of);
+        for (int q = 0; q < P.splits; ++q) {
+            v4i v[FM][FN][4];
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int h = 0; h < 4; ++h)
+                        v[i][j][h] = *part_slot<FM, FN, NT>(P.split_part, TILE_INTS, q, T, tile, i, j, h);
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) acc[i][j][r] += v[i][j][r >> 2][r & 3];
+        }
+        gemm_epilogue<BM, BN, WGM, WGN, BITS, EPI, STAGED>(acc, n0, pre, P.N, P.half, P.c, P.ldc, P.c_type, P.rowmax,
+                                                           row_of, smem);
+        return;
+    }
+
+    const int KT_all = P.K_pad >> 6;
+    const int splits = SPLIT == SPLIT_PART ? P.splits : 1;
+    const int k0 = (int)((long)KT_all * piece / splits);
+    const int k1 = (int)((long)KT_all * (piece + 1) / splits);
+    constexpr int PPS = (BITS == 8) ? 4 : 2;  // weight planes per 64-k step
+    size_t a_off[C::A_LOADS];
+#pragma unroll
+    for (int i = 0; i < C::A_LOADS; ++i) {
+        const int c = threadIdx.x + i * NT;
+        a_off[i] = (size_t)(c / BM) * P.M_alloc + m0 + c % BM;
+    }
+    EpiPre<BM, BN, WGM, WGN, BITS> pre;
+    if constexpr (SPLIT == SPLIT_NONE)
+        pre = epilogue_prefetch<BM, BN, WGM, WGN, BITS>(P.rowscale, P.rowsum, P.colscale, n0, row_of);
     gemm_mainloop<BM, BN, WGM, WGN, BITS>(smem, P.a + (size_t)k0 * 64 * P.M_alloc, (size_t)P.M_alloc, a_off,
                                           P.b + (size_t)k0 * PPS * 128, P.K_pad, n0, k1 - k0, acc);
-    if (P.splits > 1 &&
-        !split_meet<C::FM, C::FN, C::NT>(acc, P.split_part + (size_t)tile * P.splits * BM * BN,
-                                          P.split_cnt + tile, P.splits, piece))
-        return;
-    gemm_epilogue<BM, BN, WGM, WGN, BITS, EPI, STAGED>(acc, n0, pre, P.N, P.half, P.c, P.ldc, P.c_type, P.rowmax,
-                                                       row_of, smem);
+    if constexpr (SPLIT == SPLIT_PART) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int h = 0; h < 4; ++h)
+                    *part_slot<FM, FN, NT>(P.split_part, TILE_INTS, piece, T, tile, i, j, h) =
+                        v4i{acc[i][j][4 * h], acc[i][j][4 * h + 1], acc[i][j][4 * h + 2], acc[i][j][4 * h + 3]};
+    } else {
+        gemm_epilogue<BM, BN, WGM, WGN, BITS, EPI, STAGED>(acc, n0, pre, P.N, P.half, P.c, P.ldc, P.c_type, P.rowmax,
+                                                           row_of, smem);
+    }
 }
 
 // ---------------------------------------------------------------------------

@@ -83,9 +83,7 @@ struct Workspace {
     unsigned* rowmax; // [M_alloc]  max|middle| of a fused SwiGLU output
     float* c_f32;     // [M][N]   output staging / fused middle
     float* partmax;   // [8][N_pad/8] per-block max|middle| of a GEMV SwiGLU
-    int* split_cnt;   // [split_tiles] split-K arrival counters (zero between launches)
-    int* split_part;  // split-K int32 partials
-    int split_tiles;        // counters available
+    int* split_part;        // split-K int32 partials [pieces][tiles][tile ints]
     size_t split_part_ints; // partial ints available
 };
 

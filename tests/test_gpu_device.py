@@ -81,7 +81,7 @@ def test_unaligned_output_matches_oracle(ctx, bits, dtype):
 
 @pytest.mark.parametrize("splits", [2, 3])
 def test_split_k_switch_is_bit_exact(ctx, splits, monkeypatch):
-    """HM_SPLITS: K pieces per tile meet through int32 partials; same result."""
+    """HM_SPLITS: K pieces per tile sum through int32 partials; same result."""
     monkeypatch.setenv("HM_SPLITS", str(splits))
     local = D.DeviceContext(3)  # workspaces sized under the switch
     rows, k, n = 300, 640, 768
@@ -96,6 +96,28 @@ def test_split_k_switch_is_bit_exact(ctx, splits, monkeypatch):
         torch.cuda.synchronize()
         assert np.array_equal(y.cpu().numpy(), oracle.linear(codes, scales, x).astype(np.float16))
         assert np.array_equal(m.cpu().numpy(), oracle.linear_swiglu(codes, scales, x))
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_long_k_split_plan_matches_oracle(ctx, bits):
+    """Few tiles over a long K: the plan splits K into pieces (partials, then a
+    summing epilogue launch); results equal the oracle's."""
+    import ctypes
+    from open_rknpu2_lm_infer_amd import _ffi as F
+    rows, k, n = 64, 8192, 512
+    plan = F.rk_npu_hip_plan()
+    assert F.lib().rk_npu_hip_linear_plan(rows, k, n, bits, ctypes.byref(plan)) == 0
+    assert plan.kind == 1 and plan.k_splits > 1
+    codes, scales = R.weights(5, f"dlK{bits}", bits, k, n)
+    w = ctx.weights(bits, dev(codes), dev(scales))
+    x = R.activations(5, "dlK-x", rows, k)
+    y = torch.empty(rows, n, dtype=torch.float16, device="cuda")
+    D.linear(ctx, w, dev(x).half(), y, rows)
+    m = torch.empty(rows, n // 2, dtype=torch.float32, device="cuda")
+    D.linear(ctx, w, dev(x), m, rows, swiglu=True)
+    torch.cuda.synchronize()
+    assert np.array_equal(y.cpu().numpy(), oracle.linear(codes, scales, x).astype(np.float16))
+    assert np.array_equal(m.cpu().numpy(), oracle.linear_swiglu(codes, scales, x))
 
 
 @pytest.mark.parametrize("rows", [1, 4, 64])
