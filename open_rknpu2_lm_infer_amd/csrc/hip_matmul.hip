@@ -619,8 +619,10 @@ int enqueue_linear(Workspace* ws, const Weights* w, const void* x, int x_type, l
         const int grid = epi == EPI_PLAIN ? g.N_pad / 8 : g.N_pad / 16;
         const size_t lds = (size_t)g.K_pad * pv.mr;
         // Rows the kernel cannot quantize from registers (unaligned or ragged
-        // rows, or more than GEMV_XMAX chunks per thread) are quantized first.
-        const bool preq = !V.vec || (g.K_pad / 16) * pv.mr > 256 * GEMV_XMAX;
+        // rows, or more than GEMV_XMAX chunks per thread) are quantized first;
+        // so are 4 or more rows, where every block re-quantizing all rows costs
+        // more than one extra launch (M=4 decode set: 1002 -> 1090 GB/s).
+        const bool preq = pv.mr >= 4 || !V.vec || (g.K_pad / 16) * pv.mr > 256 * GEMV_XMAX;
         if (preq) {
             int rc = enqueue_quant(ws, x, x_type, lda, rows, rule, in_max, nullptr, s);
             if (rc != RK_NPU_OK) return rc;
