@@ -540,17 +540,23 @@ static void launch_gemm(int v, bool staged, const GemmParams& G, int tiles, hipS
 template <typename T, int MR, int BITS, int EPI, bool PREQ>
 static void launch_gemv_w(const GemvParams& V, int groups, size_t lds, hipStream_t s) {
     // Register windows sized to the group (rounds of 256 16-byte chunks), so
-    // no registers hold chunks past its end: fewer registers, more resident blocks.
+    // no registers hold chunks past its end: fewer registers, more resident
+    // blocks. Groups of more than 8 rounds (the 9728-long down projection) take
+    // 512-thread blocks: half the serial loads, quantization and dot products
+    // per thread on the few blocks such a matrix has.
     const int planes = BITS == 8 ? V.K_pad / 16 : V.K_pad / 32;
-    const int rounds = (planes * 8 * (EPI == EPI_PLAIN ? 1 : 2) + 255) / 256;
+    const int chunks = planes * 8 * (EPI == EPI_PLAIN ? 1 : 2);
+    const int rounds = (chunks + 255) / 256;
     if (rounds <= 4)
         hipLaunchKernelGGL((gemv_kernel<T, MR, BITS, EPI, 4, 1, PREQ>), dim3(groups), dim3(256), lds, s, V);
     else if (rounds <= 6)
         hipLaunchKernelGGL((gemv_kernel<T, MR, BITS, EPI, 6, 1, PREQ>), dim3(groups), dim3(256), lds, s, V);
     else if (rounds <= 8)
         hipLaunchKernelGGL((gemv_kernel<T, MR, BITS, EPI, 8, 1, PREQ>), dim3(groups), dim3(256), lds, s, V);
+    else if (chunks <= 512 * 6)
+        hipLaunchKernelGGL((gemv_kernel<T, MR, BITS, EPI, 6, 1, PREQ, 1, 512>), dim3(groups), dim3(512), lds, s, V);
     else
-        hipLaunchKernelGGL((gemv_kernel<T, MR, BITS, EPI, 8, 2, PREQ>), dim3(groups), dim3(256), lds, s, V);
+        hipLaunchKernelGGL((gemv_kernel<T, MR, BITS, EPI, 8, 2, PREQ, 1, 512>), dim3(groups), dim3(512), lds, s, V);
 }
 
 template <typename T, int MR, int BITS, int EPI>

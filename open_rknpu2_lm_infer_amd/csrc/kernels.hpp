@@ -1050,8 +1050,8 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_kernel(GemmParams P) {
 // one block is launched per group (enough blocks are resident that every
 // weight byte of a decode-sized matrix is requested at once). The group's
 // bytes are a flat stream of 16-byte chunks (chunk q = plane q/8, column q%8
-// of its tile); thread tid takes chunks tid + 256r, so every wave load is
-// 1 KB contiguous and the column of a thread is fixed (tid % 8). All chunks
+// of its tile); thread tid of the NTHR takes chunks tid + NTHR*r, so every
+// wave load is 1 KB contiguous and the column of a thread is fixed (tid % 8). All chunks
 // (up to NW register windows of RW rounds each) are requested first; the block then
 // quantizes the activation rows itself (row max from x or from precomputed
 // partial maxima, the dense or MoE rule) into LDS while they are in flight.
@@ -1087,24 +1087,31 @@ struct GemvParams {
 };
 
 
-template <typename T, int MR, int BITS, int EPI, int RW, int NW, bool PREQ, int GPB = 1>
-__global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
+template <typename T, int MR, int BITS, int EPI, int RW, int NW, bool PREQ, int GPB = 1, int NTHR = 256>
+__global__ __launch_bounds__(NTHR) void gemv_kernel(GemvParams P) {
     extern __shared__ __attribute__((aligned(16))) int8_t sa[];  // [K_pad/16][MR][16]
     constexpr int TPG = (EPI == EPI_PLAIN) ? 1 : 2;  // tiles per group
     constexpr int TPB = TPG * GPB;                   // tiles per block (GPB groups)
     constexpr int XMAX = GEMV_XMAX;  // 16-element activation chunks per thread
     constexpr int PV = 5;            // precomputed row-max partials per thread
-    __shared__ float s_red[4][MR];
-    __shared__ int s_isum[4][MR];
-    __shared__ int red[4][TPB][MR][8];
+    constexpr int NWV = NTHR / 64;   // waves per block
+    __shared__ float s_red[NWV][MR];
+    __shared__ int s_isum[NWV][MR];
+    __shared__ int red[NWV][TPB][MR][8];
+    auto block_isum = [&](int m) {
+        int v = 0;
+#pragma unroll
+        for (int w = 0; w < NWV; ++w) v += s_isum[w][m];
+        return v;
+    };
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int c8 = tid & 7;
     const int KG16 = P.K_pad >> 4;
     const int PL = (BITS == 8) ? KG16 : (P.K_pad >> 5);
     const int CPT = PL * 8;                  // chunks per tile
     const int CPG = CPT * TPB;               // chunks per group
-    const int NWIN = (CPG + 256 * RW - 1) / (256 * RW);
-    const int chunks = KG16 * MR;            // activation chunks (<= 256 * XMAX unless PREQ)
+    const int NWIN = (CPG + NTHR * RW - 1) / (NTHR * RW);
+    const int chunks = KG16 * MR;            // activation chunks (<= NTHR * XMAX unless PREQ)
     const int g0 = blockIdx.x * GPB;  // first group of the block
     const int groups = gridDim.x * GPB;
 
@@ -1155,8 +1162,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
     const T* x = static_cast<const T*>(P.x);
 #pragma unroll
     for (int j = 0; j < XMAX; ++j) {
-        if (256 * j >= chunks) break;
-        const int c = tid + 256 * j, kg = c / MR, m = c % MR;
+        if (NTHR * j >= chunks) break;
+        const int c = tid + NTHR * j, kg = c / MR, m = c % MR;
         if (PREQ) {
             const bool ok = c < chunks && m < P.M;
             xraw[j][0] = *reinterpret_cast<const v4u*>(ok ? P.diag_codes + ((size_t)kg * P.M_alloc + m) * 16
@@ -1171,10 +1178,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
     if (!PREQ && P.part_in) {
 #pragma unroll
         for (int i = 0; i < PV; ++i) {
-            if (256 * i >= P.part_count) break;
+            if (NTHR * i >= P.part_count) break;
 #pragma unroll
             for (int m = 0; m < MR; ++m) {
-                const int idx = tid + 256 * i;
+                const int idx = tid + NTHR * i;
                 const bool ok = m < P.M && idx < P.part_count;
                 pv[m][i] = *(ok ? P.part_in + (size_t)m * P.part_count + idx : own_cs);  // masked at use
             }
@@ -1186,7 +1193,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
     auto load_window = [&](int w, auto& buf) {
 #pragma unroll
         for (int i = 0; i < RW; ++i) {
-            const int q = (tid + 256 * (w * RW + i)) % CPG;  // past the block's tiles: a re-read, skipped
+            const int q = (tid + NTHR * (w * RW + i)) % CPG;  // past the block's tiles: a re-read, skipped
             int t, r;
             locate(q, t, r);
             const uint8_t* base = tb[0];
@@ -1209,10 +1216,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
         // 2-3. Rows quantized beforehand: codes to LDS, scales and sums from HBM.
 #pragma unroll
         for (int j = 0; j < XMAX; ++j) {
-            const int c = tid + 256 * j, m = c % MR;
+            const int c = tid + NTHR * j, m = c % MR;
             if (c < chunks) *reinterpret_cast<v4u*>(sa + c * 16) = (m < P.M) ? xraw[j][0] : v4u{0u, 0u, 0u, 0u};
         }
-        for (int c = tid + 256 * XMAX; c < chunks; c += 256) {  // long rows: after the weights
+        for (int c = tid + NTHR * XMAX; c < chunks; c += NTHR) {  // long rows: after the weights
             const int m = c % MR;
             *reinterpret_cast<v4u*>(sa + c * 16) =
                 (m < P.M) ? *reinterpret_cast<const v4u*>(P.diag_codes + ((size_t)(c / MR) * P.M_alloc + m) * 16)
@@ -1232,7 +1239,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
 #pragma unroll
         for (int m = 0; m < MR; ++m) mx[m] = 0.0f;
         auto chunk_vals = [&](int j, float (&v)[16]) {
-            const int c = tid + 256 * j, kg = c / MR, m = c % MR;
+            const int c = tid + NTHR * j, kg = c / MR, m = c % MR;
             const bool ok = c < chunks && m < P.M && kg * 16 < P.K;
             cvt16_raw(xraw[j], v, T());
 #pragma unroll
@@ -1243,21 +1250,21 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
             for (int m = 0; m < MR; ++m) {
 #pragma unroll
                 for (int i = 0; i < PV; ++i)
-                    if (m < P.M && tid + 256 * i < P.part_count) mx[m] = fmaxf(mx[m], pv[m][i]);
+                    if (m < P.M && tid + NTHR * i < P.part_count) mx[m] = fmaxf(mx[m], pv[m][i]);
                 if (m < P.M)
-                    for (int i = tid + 256 * PV; i < P.part_count; i += 256)
+                    for (int i = tid + NTHR * PV; i < P.part_count; i += NTHR)
                         mx[m] = fmaxf(mx[m], P.part_in[(size_t)m * P.part_count + i]);
             }
         } else {
 #pragma unroll
             for (int j = 0; j < XMAX; ++j) {
-                if (tid + 256 * j >= chunks) continue;  // (pure arithmetic: no load under the branch)
+                if (tid + NTHR * j >= chunks) continue;  // (pure arithmetic: no load under the branch)
                 float v[16];
                 chunk_vals(j, v);
                 float lm = 0.0f;
 #pragma unroll
                 for (int b = 0; b < 16; ++b) lm = fmaxf(lm, fabsf(v[b]));
-                const int m = (tid + 256 * j) % MR;
+                const int m = (tid + NTHR * j) % MR;
 #pragma unroll
                 for (int r = 0; r < MR; ++r) mx[r] = (r == m) ? fmaxf(mx[r], lm) : mx[r];
             }
@@ -1272,7 +1279,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
         float inv[MR];
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
-            const float v = fmaxf(fmaxf(s_red[0][m], s_red[1][m]), fmaxf(s_red[2][m], s_red[3][m]));
+            float v = s_red[0][m];
+#pragma unroll
+            for (int w = 1; w < NWV; ++w) v = fmaxf(v, s_red[w][m]);
             if (P.rule == QUANT_DENSE)
                 scale[m] = (v == 0.0f) ? 1.0f : fmaxf(v / 127.0f, FLT_MIN);
             else
@@ -1286,7 +1295,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
         for (int m = 0; m < MR; ++m) psum[m] = 0;
 #pragma unroll
         for (int j = 0; j < XMAX; ++j) {
-            const int c = tid + 256 * j, m = c % MR;
+            const int c = tid + NTHR * j, m = c % MR;
             if (c >= chunks) continue;
             float v[16];
             chunk_vals(j, v);
@@ -1310,19 +1319,19 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
         __builtin_amdgcn_s_barrier();
 #pragma unroll
         for (int m = 0; m < MR; ++m)
-            corr[m] = (BITS == 4) ? 8 * (s_isum[0][m] + s_isum[1][m] + s_isum[2][m] + s_isum[3][m]) : 0;
+            corr[m] = (BITS == 4) ? 8 * block_isum(m) : 0;
         if (blockIdx.x == 0 && P.diag_codes) {
-            for (int c = tid; c < chunks; c += 256)
+            for (int c = tid; c < chunks; c += NTHR)
                 *reinterpret_cast<v4u*>(P.diag_codes + ((size_t)(c / MR) * P.M_alloc + c % MR) * 16) =
                     *reinterpret_cast<const v4u*>(sa + c * 16);
             if (tid < MR && tid < P.M) {
                 P.diag_scale[tid] = scale[tid];
-                P.diag_rowsum[tid] = s_isum[0][tid] + s_isum[1][tid] + s_isum[2][tid] + s_isum[3][tid];
+                P.diag_rowsum[tid] = block_isum(tid);
             }
         }
     }
 
-    // 4. Dots: chunk q = tid + 256r of the group's stream.
+    // 4. Dots: chunk q = tid + NTHR*r of the group's stream.
     int acc[TPB][MR];
 #pragma unroll
     for (int t = 0; t < TPB; ++t)
@@ -1331,7 +1340,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
     auto consume = [&](int w, const auto& buf) {
 #pragma unroll
         for (int i = 0; i < RW; ++i) {
-            const int q = tid + 256 * (w * RW + i);
+            const int q = tid + NTHR * (w * RW + i);
             if (q >= CPG) continue;
             int tq, rq;
             locate(q, tq, rq);
@@ -1414,7 +1423,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
 #pragma unroll
                 for (int t = 0; t < TPG; ++t) {
                     const int tt = gp * TPG + t;
-                    const int tot = red[0][tt][m][c8] + red[1][tt][m][c8] + red[2][tt][m][c8] + red[3][tt][m][c8];
+                    int tot = 0;
+#pragma unroll
+                    for (int w = 0; w < NWV; ++w) tot += red[w][tt][m][c8];
                     y[t] = ((float)(tot - corr[m]) * scale[m]) * cs[tt];
                 }
                 const int p = 8 * tile[gp * TPG] + c8;
