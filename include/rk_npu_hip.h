@@ -65,6 +65,33 @@ rk_npu_w4a8_weights* rk_npu_hip_w4a8_weights_create_device(rk_npu_iommu_domain* 
                                                            const int8_t* codes,
                                                            const float* scales);
 
+/* Weights built on the GPU straight from checkpoint storage, replacing the
+ * host path QuantLoader::load -> unpack_codes / transpose_codes -> concatenate
+ * (src/model/checkpoint.rs:505-527, 558-571, 266-280, 573-604): no [K][N]
+ * code matrix is formed on the host or the device. The parts are the fused
+ * projection's matrices along N in order (q||k||v, gate||up), all with the
+ * same k; each part's data and scales are DEVICE pointers:
+ *   RK_NPU_HIP_PACK_QUANTIZED: int32 words [n][ceil(k * bits / 32)]; the value
+ *     of (row n, column k) is bits (k % (32/bits)) * bits .. of word
+ *     k / (32/bits), code = value - 2^(bits-1) (compressed-tensors
+ *     pack-quantized, little-endian words);
+ *   RK_NPU_HIP_INT_QUANTIZED (bits 8 only): int8 codes [n][k].
+ * scales: [n] f32, all > 0. Returns a rk_npu_w4a8_weights* (bits 4) or a
+ * rk_npu_f32i8f32_weights* (bits 8) to cast to, freed with the matching
+ * *_weights_free; NULL on bad arguments (at most 8 parts), a nonpositive
+ * scale, or allocation failure. Weights are identical to creating them from
+ * the unpacked, concatenated [K][N] codes. */
+#define RK_NPU_HIP_PACK_QUANTIZED 0
+#define RK_NPU_HIP_INT_QUANTIZED 1
+typedef struct rk_npu_hip_checkpoint_part {
+    const void* data;
+    const float* scales;
+    int32_t n;
+    int32_t format;
+} rk_npu_hip_checkpoint_part;
+void* rk_npu_hip_weights_create_checkpoint(rk_npu_iommu_domain* domain, int bits, int k,
+                                           const rk_npu_hip_checkpoint_part* parts, int count);
+
 /* Diagnostics: copies what the workspace's last call left on the device for
  * its first `rows` rows: the int8 activation codes as [rows][K] row-major,
  * the per-row scales and the per-row code sums (any output may be NULL).

@@ -35,6 +35,8 @@ RK_NPU_HIP_F32 = 0
 RK_NPU_HIP_F16 = 1
 RK_NPU_HIP_PLAIN = 0
 RK_NPU_HIP_SWIGLU = 1
+RK_NPU_HIP_PACK_QUANTIZED = 0
+RK_NPU_HIP_INT_QUANTIZED = 1
 
 
 class rk_npu_domain_memory_stats(Structure):
@@ -149,6 +151,10 @@ class rk_npu_hip_plan(Structure):
                 ("k_splits", c_int32), ("grid", c_int32)]
 
 
+class rk_npu_hip_checkpoint_part(Structure):
+    _fields_ = [("data", c_void_p), ("scales", c_void_p), ("n", c_int32), ("format", c_int32)]
+
+
 P = POINTER
 i8p = P(c_int8)
 f32p = P(c_float)
@@ -244,6 +250,8 @@ SIGNATURES = {
                                                              c_void_p]),
     "rk_npu_hip_w4a8_weights_create_device": (c_void_p, [c_void_p, P(rk_npu_i4_weight_config), c_void_p,
                                                          c_void_p]),
+    "rk_npu_hip_weights_create_checkpoint": (c_void_p, [c_void_p, c_int, c_int, P(rk_npu_hip_checkpoint_part),
+                                                        c_int]),
     "rk_npu_hip_workspace_codes": (c_int, [c_void_p, c_int, c_int, i8p, f32p, i32p]),
     "rk_npu_hip_inject_alloc_failures": (c_int, [c_int]),
     "rk_npu_hip_linear_plan": (c_int, [c_int, c_int, c_int, c_int, P(rk_npu_hip_plan)]),

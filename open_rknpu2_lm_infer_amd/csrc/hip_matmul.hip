@@ -217,6 +217,72 @@ Weights* weights_create(Domain* d, int bits, int K, int N, const int8_t* codes, 
     return w;
 }
 
+// Weights straight from checkpoint storage on the device (parts fused along
+// N in order), packed by one kernel; scales checked positive on the packed copy.
+Weights* weights_create_ckpt(Domain* d, int bits, int K, const rk_npu_hip_checkpoint_part* parts, int count) {
+    if (!d || !parts || count < 1 || count > CKPT_MAX_PARTS || (bits != 4 && bits != 8) || K <= 0) return nullptr;
+    CkptParams P{};
+    long N = 0;
+    for (int i = 0; i < count; ++i) {
+        const rk_npu_hip_checkpoint_part& q = parts[i];
+        const bool fmt_ok = q.format == RK_NPU_HIP_PACK_QUANTIZED || (q.format == RK_NPU_HIP_INT_QUANTIZED && bits == 8);
+        if (!q.data || !q.scales || q.n <= 0 || !fmt_ok) return nullptr;
+        P.part[i].data = q.data;
+        P.part[i].scales = q.scales;
+        P.part[i].start = (int)N;
+        P.part[i].n = q.n;
+        P.part[i].format = q.format == RK_NPU_HIP_INT_QUANTIZED ? 1 : 0;
+        P.part[i].words = (K + 32 / bits - 1) / (32 / bits);
+        N += q.n;
+    }
+    if (N > INT32_MAX || (size_t)K * (size_t)N > (size_t)1 << 40) return nullptr;
+    if (hipSetDevice(device_of(d)) != hipSuccess) return nullptr;
+    const Geometry g = make_geometry(bits, K, (int)N);
+    Weights* w = (bits == 8) ? static_cast<Weights*>(new (std::nothrow) rk_npu_f32i8f32_weights())
+                             : static_cast<Weights*>(new (std::nothrow) rk_npu_w4a8_weights());
+    if (!w) return nullptr;
+    w->magic = bits == 8 ? MAGIC_W8 : MAGIC_W4;
+    w->g = g;
+    w->domain = d;
+    w->fingerprint = mix64(mix64(mix64(0x5eedull, (uint64_t)bits), (uint64_t)K), (uint64_t)N);
+    w->bytes = weight_bytes(g);
+    const size_t payload = w->bytes - (size_t)g.N_pad * sizeof(float);
+    w->packed = static_cast<uint8_t*>(domain_alloc(d, payload));
+    w->colscale = static_cast<float*>(domain_alloc(d, (size_t)g.N_pad * sizeof(float)));
+    bool ok = w->packed && w->colscale;
+    if (ok) {
+        P.count = count;
+        P.bits = bits;
+        P.K = K;
+        P.N = (int)N;
+        P.K_pad = g.K_pad;
+        P.N_pad = g.N_pad;
+        P.half = g.half;
+        P.out = w->packed;
+        P.colscale = w->colscale;
+        const size_t entries = (size_t)(g.K_pad / (bits == 8 ? 16 : 32)) * g.N_pad;
+        hipLaunchKernelGGL(pack_ckpt_kernel, dim3((unsigned)((entries + 255) / 256)), dim3(256), 0, 0, P);
+        ok = hipGetLastError() == hipSuccess && hipDeviceSynchronize() == hipSuccess;
+    }
+    if (ok) {
+        std::vector<float> hs((size_t)g.N_pad);
+        ok = hipMemcpy(hs.data(), w->colscale, (size_t)g.N_pad * 4, hipMemcpyDeviceToHost) == hipSuccess;
+        int valid = 0;
+        for (int p = 0; ok && p < g.N_pad; ++p) {
+            if (hs[p] > 0.0f) ++valid;  // src/model/checkpoint.rs:486-489
+            uint32_t b;
+            std::memcpy(&b, &hs[p], 4);
+            w->fingerprint = mix64(w->fingerprint, b);
+        }
+        ok = ok && valid == N;
+    }
+    if (!ok) {
+        weights_destroy(w);
+        return nullptr;
+    }
+    return w;
+}
+
 void weights_destroy(Weights* w) {
     if (!w) return;
     (void)hipSetDevice(device_of(w->domain));
@@ -1200,6 +1266,14 @@ rk_npu_w4a8_weights* rk_npu_hip_w4a8_weights_create_device(rk_npu_iommu_domain* 
     if (!config) return nullptr;
     return static_cast<rk_npu_w4a8_weights*>(
         weights_create(static_cast<Domain*>(domain), 4, config->K, config->N, codes, scales, true));
+}
+
+void* rk_npu_hip_weights_create_checkpoint(rk_npu_iommu_domain* domain, int bits, int k,
+                                           const rk_npu_hip_checkpoint_part* parts, int count) {
+    Weights* w = weights_create_ckpt(static_cast<Domain*>(domain), bits, k, parts, count);
+    if (!w) return nullptr;
+    if (bits == 8) return static_cast<rk_npu_f32i8f32_weights*>(w);
+    return static_cast<rk_npu_w4a8_weights*>(w);
 }
 
 int rk_npu_hip_workspace_codes(void* workspace, int bits, int rows, int8_t* codes, float* scales,

@@ -543,6 +543,65 @@ static __global__ __launch_bounds__(256) void pack_w4_kernel(PackParams P) {
     if (bad) atomicOr(P.bad, 1u);
 }
 
+// Packing straight from checkpoint storage (the fused matrix's parts along
+// N): pack-quantized int32 words [n][ceil(k*bits/32)] holding code + 2^(bits-1)
+// in consecutive bit fields, or int-quantized int8 codes [n][k]. Column n of
+// the fused matrix is column n - start of the part containing it.
+constexpr int CKPT_MAX_PARTS = 8;
+struct CkptPart {
+    const void* data;
+    const float* scales;
+    int start, n, format, words;  // words per row (pack-quantized)
+};
+struct CkptParams {
+    CkptPart part[CKPT_MAX_PARTS];
+    int count, bits, K, N, K_pad, N_pad, half;
+    uint8_t* out;
+    float* colscale;
+};
+
+// Code field of (k, column n) in the unpacked offset form u = code + 2^(bits-1).
+__device__ __forceinline__ unsigned ckpt_field(const CkptParams& P, const CkptPart& q, int n, int k) {
+    if (q.format == 1) return (unsigned)((int)static_cast<const int8_t*>(q.data)[(size_t)n * P.K + k] + 128) & 0xffu;
+    const int f = 32 / P.bits;
+    const unsigned w = static_cast<const unsigned*>(q.data)[(size_t)n * q.words + k / f];
+    return (w >> ((k % f) * P.bits)) & ((1u << P.bits) - 1u);
+}
+
+// One thread per 16-byte tile entry, as pack_w8_kernel / pack_w4_kernel:
+// W8 stores codes (u - 128), W4 the offset nibbles u as they are.
+static __global__ __launch_bounds__(256) void pack_ckpt_kernel(CkptParams P) {
+    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const int planes = P.bits == 8 ? P.K_pad / 16 : P.K_pad / 32;
+    if (idx >= (size_t)planes * P.N_pad) return;
+    const int p = (int)(idx % P.N_pad), j = (int)(idx / P.N_pad);
+    const int n = p < P.N ? orig_col(p, P.half) : -1;
+    int qi = 0;
+    for (int i = 1; i < P.count; ++i) qi = (n >= P.part[i].start) ? i : qi;
+    const CkptPart& q = P.part[qi];
+    const int ln = n - q.start;
+    unsigned w[4] = {0u, 0u, 0u, 0u};
+    if (P.bits == 8) {
+#pragma unroll
+        for (int b = 0; b < 16; ++b) {
+            const int k = j * 16 + b;
+            const unsigned v = (n >= 0 && k < P.K) ? ((ckpt_field(P, q, ln, k) - 128u) & 0xffu) : 0u;
+            w[b >> 2] |= v << ((b & 3) * 8);
+        }
+    } else {
+        const int klo = 64 * (j >> 1) + 16 * (j & 1), khi = klo + 32;
+#pragma unroll
+        for (int b = 0; b < 16; ++b) {
+            const unsigned lo = (n >= 0 && klo + b < P.K) ? ckpt_field(P, q, ln, klo + b) : 8u;
+            const unsigned hi = (n >= 0 && khi + b < P.K) ? ckpt_field(P, q, ln, khi + b) : 8u;
+            w[b >> 2] |= (lo | (hi << 4)) << ((b & 3) * 8);
+        }
+    }
+    const size_t dst = (((size_t)(p >> 3) * planes + j) * 8 + (p & 7)) * 16;
+    *reinterpret_cast<v4u*>(P.out + dst) = v4u{w[0], w[1], w[2], w[3]};
+    if (j == 0) P.colscale[p] = n >= 0 ? q.scales[ln] : 0.0f;
+}
+
 // ---------------------------------------------------------------------------
 // Prefill GEMM on MFMA: v_mfma_i32_32x32x32_i8, int32 accumulation.
 // Block tile BM x BN, K step 64, WGM x WGN waves, wave tile (BM/WGM) x (BN/WGN).

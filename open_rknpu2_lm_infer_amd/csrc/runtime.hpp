@@ -94,6 +94,7 @@ void workspace_destroy(Workspace* ws);
 Weights* weights_create(Domain* d, int bits, int K, int N, const int8_t* codes, const float* scales,
                         bool device_codes);
 void weights_destroy(Weights* w);
+Weights* weights_create_ckpt(Domain* d, int bits, int K, const rk_npu_hip_checkpoint_part* parts, int count);
 
 struct Plan {
     int kind;  // 0 GEMV, 1 GEMM

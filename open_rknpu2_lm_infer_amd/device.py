@@ -62,6 +62,28 @@ class DeviceContext:
             h = _Handle(raw, L.rk_npu_f32i8f32_weights_free, "W8 weights", self.shared)
         return DeviceWeights(h, bits, k, n)
 
+    def weights_from_checkpoint(self, bits: int, k: int, parts) -> "DeviceWeights":
+        """Weights from checkpoint storage on the device, fused along N in order.
+        parts: (data, scales, fmt) with data a cuda tensor of int32 words
+        [n][ceil(k*bits/32)] (fmt RK_NPU_HIP_PACK_QUANTIZED) or int8 codes [n][k]
+        (RK_NPU_HIP_INT_QUANTIZED, bits 8) and scales f32 [n]."""
+        import torch
+        torch.cuda.synchronize()
+        arr = (F.rk_npu_hip_checkpoint_part * len(parts))()
+        n_total = 0
+        keep = []
+        for i, (data, scales, fmt) in enumerate(parts):
+            ensure(data.is_cuda and scales.is_cuda and scales.dtype == torch.float32, "checkpoint parts must be on the GPU")
+            data, scales = data.contiguous(), scales.contiguous()
+            keep += [data, scales]
+            arr[i] = F.rk_npu_hip_checkpoint_part(data.data_ptr(), scales.data_ptr(), data.shape[0], fmt)
+            n_total += data.shape[0]
+        L = F.lib()
+        raw = L.rk_npu_hip_weights_create_checkpoint(self.domain, bits, k, arr, len(parts))
+        free = L.rk_npu_w4a8_weights_free if bits == 4 else L.rk_npu_f32i8f32_weights_free
+        h = _Handle(raw, free, f"W{bits} weights from checkpoint storage", self.shared)
+        return DeviceWeights(h, bits, k, n_total)
+
     def workspace(self, bits: int, rows: int, k: int, n: int) -> _Handle:
         key = (bits, rows, k, n)
         if key not in self._ws:

@@ -120,6 +120,74 @@ def test_long_k_split_plan_matches_oracle(ctx, bits):
     assert np.array_equal(m.cpu().numpy(), oracle.linear_swiglu(codes, scales, x))
 
 
+def _pack_words(codes_kn, bits):
+    """compressed-tensors pack-quantized words [n][ceil(k*bits/32)] holding the
+    codes [k][n] as code + 2^(bits-1) in consecutive bit fields."""
+    k, n = codes_kn.shape
+    f = 32 // bits
+    cols = -(-k // f)
+    u = np.zeros((cols * f, n), np.uint64)
+    u[:k] = (codes_kn.astype(np.int64) + (1 << (bits - 1))) & ((1 << bits) - 1)
+    u = u.reshape(cols, f, n)
+    words = np.zeros((n, cols), np.uint64)
+    for i in range(f):
+        words |= u[:, i, :].T << np.uint64(i * bits)
+    return words.astype(np.uint32)
+
+
+@pytest.mark.parametrize("case", ["w4_gate_up", "w8_packed_qkv", "w8_int_quantized"])
+def test_weights_from_checkpoint_storage(ctx, case):
+    """rk_npu_hip_weights_create_checkpoint unpacks / transposes / concatenates
+    on the GPU: the words are the reference's format (the oracle's unpack,
+    pinned to its known-answer test, recovers the codes), and the weights give
+    the same results as weights created from the fused [K][N] codes."""
+    from open_rknpu2_lm_infer_amd import _ffi as F
+    bits, k, ns, fmt = {"w4_gate_up": (4, 650, (768, 768), F.RK_NPU_HIP_PACK_QUANTIZED),
+                        "w8_packed_qkv": (8, 640, (512, 128, 128), F.RK_NPU_HIP_PACK_QUANTIZED),
+                        "w8_int_quantized": (8, 648, (384, 256), F.RK_NPU_HIP_INT_QUANTIZED)}[case]
+    mats = [R.weights(9, f"ck-{case}-{i}", bits, k, n) for i, n in enumerate(ns)]
+    parts = []
+    for codes, scales in mats:
+        if fmt == F.RK_NPU_HIP_PACK_QUANTIZED:
+            words = _pack_words(codes, bits)
+            assert np.array_equal(oracle.unpack_codes(words, bits, codes.shape[1], k), codes)
+            data = dev(words.view(np.int32))
+        else:
+            data = dev(np.ascontiguousarray(codes.T))
+        parts.append((data, dev(scales), fmt))
+    fused_codes = oracle.concatenate([c for c, _ in mats])
+    fused_scales = np.concatenate([s_ for _, s_ in mats]).astype(np.float32)
+    w_ck = ctx.weights_from_checkpoint(bits, k, parts)
+    w_ref = ctx.weights(bits, dev(fused_codes), dev(fused_scales))
+    n = fused_codes.shape[1]
+    for rows in (3, 300):
+        x = R.activations(9, f"ck-x{rows}", rows, k)
+        ref = oracle.linear(fused_codes, fused_scales, x)
+        for w in (w_ck, w_ref):
+            y = torch.empty(rows, n, dtype=torch.float32, device="cuda")
+            D.linear(ctx, w, dev(x), y, rows)
+            torch.cuda.synchronize()
+            assert np.array_equal(y.cpu().numpy(), ref)
+
+
+def test_weights_from_checkpoint_rejects_bad_input(ctx):
+    import ctypes
+    from open_rknpu2_lm_infer_amd import _ffi as F
+    L = F.lib()
+    codes, scales = R.weights(9, "ck-bad", 8, 64, 32)
+    data, sc = dev(np.ascontiguousarray(codes.T)), dev(scales)
+    arr = (F.rk_npu_hip_checkpoint_part * 1)(F.rk_npu_hip_checkpoint_part(data.data_ptr(), sc.data_ptr(), 32,
+                                                                        F.RK_NPU_HIP_INT_QUANTIZED))
+    # int-quantized storage exists only for 8-bit weights
+    assert not L.rk_npu_hip_weights_create_checkpoint(ctx.domain, 4, 64, arr, 1)
+    # a nonpositive scale is rejected (src/model/checkpoint.rs:486-489)
+    bad = dev(np.where(np.arange(32) == 5, 0.0, scales).astype(np.float32))
+    arr[0].scales = bad.data_ptr()
+    assert not L.rk_npu_hip_weights_create_checkpoint(ctx.domain, 8, 64, arr, 1)
+    assert not L.rk_npu_hip_weights_create_checkpoint(ctx.domain, 8, 64, arr, 0)
+    torch.cuda.synchronize()
+
+
 @pytest.mark.parametrize("rows", [1, 4, 64])
 def test_device_ffn_matches_oracle(ctx, rows):
     h, f = 512, 768
