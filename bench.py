@@ -304,7 +304,9 @@ def run_prefill(torch, ctx, rows, steps, warmup):
     ms, ms_eager, ms_graph, ok = best_time(torch, step, steps, warmup,
                                            lambda: [t.y_qkv.clone(), t.y_ffn.clone(), y_head.clone()])
     ops = t.ops_per_layer() * LAYERS + 2.0 * rows * H * VOCAB
-    # dominant kernel: the W4 gate_up GEMM with fused SwiGLU, 36 launches
+    # dominant kernel: the W4 gate_up GEMM with fused SwiGLU, 36 launches on
+    # the 36 layers' weights in a graph; each linear also launches its
+    # activation quantization (about 5% of the pair), which the time includes.
     gu = [mats["gate_up"] for mats in t.w]
     mid = torch.empty(rows, F, dtype=torch.float16, device="cuda")
     def gu_run():
@@ -312,6 +314,7 @@ def run_prefill(torch, ctx, rows, steps, warmup):
             D.linear(ctx, w, t.x_ffn, mid, rows, swiglu=True, ws=t.ws["gate_up"])
     ms_gu, _ = graph_time(torch, gu_run, max(2, steps // 2))
     per_us = ms_gu * 1e3 / len(gu)
+    launches = len(gu)
     work = 2.0 * rows * H * 2 * F
     res = {"workload": f"prefill M={rows}: Qwen3-4B qkv/o/down W8A8 + gate_up W4A8 (+SwiGLU) x36 + lm_head W8A8",
            "value": round(ops / (ms * 1e-3) / 1e12, 2), "unit": "TOPS", "ms_per_step": round(ms, 3),
@@ -319,10 +322,34 @@ def run_prefill(torch, ctx, rows, steps, warmup):
            "ms_eager": round(ms_eager, 3), "ms_graph": round(ms_graph, 3), "graph_matches_eager": ok,
            "roofline": roofline(work / (per_us * 1e-6) / 1e12, "mfma",
                                 f"gemm_kernel<256,256,2,4,W4,SwiGLU> gate_up 2560x19456, M={rows}", per_us, work,
-                                len(gu), "graph of 36 back-to-back launches, HIP events on the replay stream")}
-    log(f"[bench] prefill: {res['value']} TOPS ({ms:.2f} ms/step)")
+                                launches, "graph of 36 back-to-back quantization + GEMM launch pairs, HIP events "
+                                "on the replay stream"),
+           "vendor_ref": vendor_int8_gemm(torch, rows, H, 2 * F)}
+    log(f"[bench] prefill: {res['value']} TOPS ({ms:.2f} ms/step); vendor int8 GEMM {res['vendor_ref']}")
     del t, head
     return res
+
+
+def vendor_int8_gemm(torch, m, k, n, reps=20):
+    """Context for the MFMA roofline: the vendor library's plain int8 GEMM
+    (torch._int_mm -> hipBLASLt, int32 out, no quantization, dequant or
+    SwiGLU) on the same M, K, N, timed with HIP events on the current stream."""
+    try:
+        a = torch.randint(-127, 128, (m, k), dtype=torch.int8, device="cuda")
+        b = torch.randint(-127, 128, (n, k), dtype=torch.int8, device="cuda").t()
+        for _ in range(3):
+            torch._int_mm(a, b)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            torch._int_mm(a, b)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / reps
+        return {"op": f"torch._int_mm int8 [{m}x{k}] x [{k}x{n}] -> int32", "us": round(us, 1),
+                "tops": round(2.0 * m * k * n / (us * 1e-6) / 1e12, 1)}
+    except Exception as ex:  # library without an int8 GEMM: reported, not fatal
+        return {"op": "torch._int_mm", "error": str(ex)[:120]}
 
 
 def run_ffn512(torch, ctx, steps, warmup, rows=512):
