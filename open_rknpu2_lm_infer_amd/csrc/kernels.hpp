@@ -1143,12 +1143,40 @@ struct GemvParams {
     float* diag_scale;
     int* diag_rowsum;
     int M_alloc;
+    // Grouped mode (routed experts, one row per slot): block row s = slot s <
+    // slot_count[0] of assignment perm[s] (token perm[s] / top, expert
+    // ids[perm[s]]): weights and column scales of that expert, activation row
+    // s (or the token's pre-quantized row), output row s, partial maxima row s.
+    const uint8_t* const* b_tab;
+    const float* const* s_tab;
+    const int* perm;
+    const int* ids;
+    const int* slot_count;
+    int top;
 };
 
 
-template <typename T, int MR, int BITS, int EPI, int RW, int NW, bool PREQ, int GPB = 1, int NTHR = 256>
+template <typename T, int MR, int BITS, int EPI, int RW, int NW, bool PREQ, int GPB = 1, int NTHR = 256,
+          bool GROUPED = false>
 __global__ __launch_bounds__(NTHR) void gemv_kernel(GemvParams P) {
     extern __shared__ __attribute__((aligned(16))) int8_t sa[];  // [K_pad/16][MR][16]
+    if constexpr (GROUPED) {
+        static_assert(MR == 1 && GPB == 1, "one slot row per block");
+        const int s = blockIdx.y;
+        if (s >= P.slot_count[0]) return;  // uniform over the block
+        const int a = P.perm[s], tok = a / P.top, e = P.ids[a];
+        P.b = P.b_tab[e];
+        P.colscale = P.s_tab[e];
+        P.x = static_cast<const T*>(P.x) + (size_t)s * P.lda;
+        if (P.part_in) P.part_in += (size_t)s * P.part_count;
+        P.c = static_cast<uint8_t*>(P.c) + (size_t)s * P.ldc * (P.c_type == DT_F32 ? 4 : 2);
+        if (P.part_out) P.part_out += (size_t)s * gridDim.x;
+        if (PREQ) {
+            P.diag_codes += (size_t)tok * 16;
+            P.diag_scale += tok;
+            P.diag_rowsum += tok;
+        }
+    }
     constexpr int TPG = (EPI == EPI_PLAIN) ? 1 : 2;  // tiles per group
     constexpr int TPB = TPG * GPB;                   // tiles per block (GPB groups)
     constexpr int XMAX = GEMV_XMAX;  // 16-element activation chunks per thread

@@ -72,6 +72,8 @@ struct MoeWork {
     float* gscale;    // [g_alloc]
     int* gsum;        // [g_alloc]
     int g_alloc;
+    float* gpart;     // per-block row maxima of the slot GEMV's middle [slots][gu groups]
+    int gu_groups;
     unsigned* host_error;  // pinned
     size_t bytes;
 };
@@ -225,7 +227,9 @@ static MoeWork* work_create(Domain* d, const rk_npu_moe_w8_config* cfg) {
     const size_t sz_out = round_up_z((size_t)cfg->max_rows * w.hidden * 4, 256);
     ws->g_alloc = round_up(A, 256);
     const size_t sz_g = (size_t)round_up(w.hidden, 64) * ws->g_alloc, sz_gs = (size_t)ws->g_alloc * 4;
-    const size_t total = 4 * sz_a + sz_tiles + 256 + 256 + sz_out + sz_g + 2 * sz_gs;
+    ws->gu_groups = round_up(2 * w.intermediate, 256) / 16;
+    const size_t sz_gp = round_up_z((size_t)A * ws->gu_groups * 4, 256);
+    const size_t total = 4 * sz_a + sz_tiles + 256 + 256 + sz_out + sz_g + 2 * sz_gs + sz_gp;
     uint8_t* base = static_cast<uint8_t*>(domain_alloc(d, total));
     bool ok = ws->xws && ws->mws && (!ws->shared || (ws->sgws && ws->sdws)) && base;
     if (base) {
@@ -251,6 +255,8 @@ static MoeWork* work_create(Domain* d, const rk_npu_moe_w8_config* cfg) {
         ws->gscale = reinterpret_cast<float*>(base + off);
         off += sz_gs;
         ws->gsum = reinterpret_cast<int*>(base + off);
+        off += sz_gs;
+        ws->gpart = reinterpret_cast<float*>(base + off);
         ok = ok && hipMemset(base, 0, total) == hipSuccess;
     }
     ws->bytes = total + (ws->xws ? ws->xws->bytes : 0) + (ws->mws ? ws->mws->bytes : 0) +
@@ -277,7 +283,7 @@ static size_t work_table_bytes(const MoeWork* ws) {
     const int A = ws->max_rows * ws->top;
     return 4 * round_up_z((size_t)A * 4, 256) + round_up_z((size_t)A * 16, 256) + 512 +
            round_up_z((size_t)ws->max_rows * ws->h * 4, 256) + (size_t)round_up(ws->h, 64) * ws->g_alloc +
-           2 * (size_t)ws->g_alloc * 4;
+           2 * (size_t)ws->g_alloc * 4 + round_up_z((size_t)A * ws->gu_groups * 4, 256);
 }
 
 static void work_destroy(MoeWork* ws) {
@@ -307,6 +313,25 @@ static void launch_moe_gemm(const MoeGemmParams& G, int grid, hipStream_t s, int
     prof_end(slot, s);
 }
 
+// One GEMV block row per routed slot (decode-sized batches): the slot's
+// expert weights streamed like a dense M=1 GEMV. Register windows as in the
+// dense launch.
+template <typename T, int BITS, int EPI, bool PREQ>
+static void launch_slot_gemv(const GemvParams& V, int slots, hipStream_t s) {
+    const int planes = BITS == 8 ? V.K_pad / 16 : V.K_pad / 32;
+    const int rounds = (planes * 8 * (EPI == EPI_PLAIN ? 1 : 2) + 255) / 256;
+    const dim3 grid(EPI == EPI_PLAIN ? V.N_pad / 8 : V.N_pad / 16, slots);
+    const size_t lds = V.K_pad;
+    if (rounds <= 4)
+        hipLaunchKernelGGL((gemv_kernel<T, 1, BITS, EPI, 4, 1, PREQ, 1, 256, true>), grid, dim3(256), lds, s, V);
+    else if (rounds <= 6)
+        hipLaunchKernelGGL((gemv_kernel<T, 1, BITS, EPI, 6, 1, PREQ, 1, 256, true>), grid, dim3(256), lds, s, V);
+    else if (rounds <= 8)
+        hipLaunchKernelGGL((gemv_kernel<T, 1, BITS, EPI, 8, 1, PREQ, 1, 256, true>), grid, dim3(256), lds, s, V);
+    else
+        hipLaunchKernelGGL((gemv_kernel<T, 1, BITS, EPI, 8, 2, PREQ, 1, 256, true>), grid, dim3(256), lds, s, V);
+}
+
 // Enqueues the whole routed FFN (plus shared expert) for `rows` token rows
 // whose input, ids and routes already sit in device memory.
 static int enqueue_moe(MoeWork* ws, const MoeBank* b, int rows, const float* input, const int* ids,
@@ -329,6 +354,70 @@ static int enqueue_moe(MoeWork* ws, const MoeBank* b, int rows, const float* inp
     R.rowmax_count = A;
     R.error = ws->error;
     hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(1024), 0, s, R);
+
+    // Decode-sized batches (at most 64 slots): one GEMV block row per slot.
+    // gate/up on the tokens' quantized rows -> SwiGLU middle [slot][inter] and
+    // per-block row maxima -> down quantizes each middle row itself from them.
+    // (T=1: 43 -> 26 us.)
+    const bool slot_gemv = A <= 64 && (ws->inter % 16) == 0 && b->ggu.half != 0 &&
+                           (ws->mws->g.K_pad / 16) <= 256 * GEMV_XMAX;
+    if (slot_gemv) {
+        GemvParams V{};
+        V.rule = QUANT_MOE;
+        V.vec = 1;
+        V.M = 1;
+        V.b_tab = b->d_gu;
+        V.s_tab = b->d_gus;
+        V.perm = ws->perm;
+        V.ids = ids;
+        V.slot_count = ws->counts;
+        V.top = ws->top;
+        V.x = ws->xws->codes;  // unused (rows quantized beforehand)
+        V.diag_codes = ws->xws->codes;
+        V.diag_scale = ws->xws->rowscale;
+        V.diag_rowsum = ws->xws->rowsum;
+        V.M_alloc = ws->xws->M_alloc;
+        V.c = ws->mws->a_f32;  // middle [slot][inter]
+        V.ldc = ws->inter;
+        V.c_type = DT_F32;
+        V.part_out = ws->gpart;
+        V.K = b->ggu.K;
+        V.N = b->ggu.N;
+        V.K_pad = b->ggu.K_pad;
+        V.N_pad = b->ggu.N_pad;
+        V.half = b->ggu.half;
+        launch_slot_gemv<float, 4, EPI_SWIGLU_MAX, true>(V, A, s);
+
+        GemvParams D{};
+        D.rule = QUANT_MOE;
+        D.vec = 1;
+        D.M = 1;
+        D.b_tab = b->d_dn;
+        D.s_tab = b->d_dns;
+        D.perm = ws->perm;
+        D.ids = ids;
+        D.slot_count = ws->counts;
+        D.top = ws->top;
+        D.x = ws->mws->a_f32;
+        D.lda = ws->inter;
+        D.part_in = ws->gpart;
+        D.part_count = b->ggu.N_pad / 16;
+        D.c = ws->mws->c_f32;  // contributions [slot][h]
+        D.ldc = ws->h;
+        D.c_type = DT_F32;
+        D.K = b->gdn.K;
+        D.N = b->gdn.N;
+        D.K_pad = b->gdn.K_pad;
+        D.N_pad = b->gdn.N_pad;
+        D.half = b->gdn.half;
+        D.M_alloc = ws->mws->M_alloc;
+        if (b->dn_bits == 8)
+            launch_slot_gemv<float, 8, EPI_PLAIN, false>(D, A, s);
+        else
+            launch_slot_gemv<float, 4, EPI_PLAIN, false>(D, A, s);
+        if (hipGetLastError() != hipSuccess) return RK_NPU_ERR_DEVICE;
+    }
+
     // Upper bound of the m-tile count: every tile holds >= 1 slot, and at most
     // one partial tile per expert.
     const int max_tiles = std::min(A, (A + std::min(A, ws->experts) * (MOE_BM - 1)) / MOE_BM);
@@ -336,7 +425,7 @@ static int enqueue_moe(MoeWork* ws, const MoeBank* b, int rows, const float* inp
     // Many slots: token codes gathered into slot order first, so the grouped
     // GEMM's A loads are contiguous rows (measured at 4096 slots: gate/up 69 ->
     // 57 us for a 5.5 us gather). Few slots: the GEMM gathers rows itself.
-    const bool gather = A >= 256;
+    const bool gather = !slot_gemv && A >= 256;
     if (gather) {
         GatherParams Q;
         Q.src = ws->xws->codes;
@@ -355,6 +444,7 @@ static int enqueue_moe(MoeWork* ws, const MoeBank* b, int rows, const float* inp
         hipLaunchKernelGGL(moe_gather_kernel, grid, dim3(256), 0, s, Q);
     }
 
+    if (!slot_gemv) {
     MoeGemmParams G;
     G.a = gather ? ws->gcodes : ws->xws->codes;
     G.a_alloc = gather ? ws->g_alloc : ws->xws->M_alloc;
@@ -401,6 +491,7 @@ static int enqueue_moe(MoeWork* ws, const MoeBank* b, int rows, const float* inp
     else
         launch_moe_gemm<4, EPI_PLAIN>(G, max_tiles * G.tiles_n, s, A);
     if (hipGetLastError() != hipSuccess) return RK_NPU_ERR_DEVICE;
+    }
 
     const float* shared = nullptr;
     if (b->shared) {
