@@ -603,60 +603,92 @@ static void launch_gemm(int v, bool staged, const GemmParams& G, int tiles, hipS
     }
 }
 
-template <typename T, int MR, int BITS, int EPI, bool PREQ>
+template <typename T, int MR, int BITS, int EPI, bool PREQ, bool QW>
 static void launch_gemv_w(const GemvParams& V, int groups, size_t lds, hipStream_t s) {
     // Register windows sized to the group (rounds of 256 16-byte chunks), so
-    // no registers hold chunks past its end: fewer registers, more resident
-    // blocks. Groups of more than 8 rounds (the 9728-long down projection) take
-    // 512-thread blocks: half the serial loads, quantization and dot products
-    // per thread on the few blocks such a matrix has.
+    // no thread loads a chunk past the group's end and no registers hold one:
+    // fewer registers, more resident blocks, no wasted load issue. Groups of
+    // more than 8 rounds (the 9728-long down projection) take 512-thread
+    // blocks: half the serial loads, quantization and dot products per thread
+    // on the few blocks such a matrix has.
     const int planes = BITS == 8 ? V.K_pad / 16 : V.K_pad / 32;
     const int chunks = planes * 8 * (EPI == EPI_PLAIN ? 1 : 2);
     const int rounds = (chunks + 255) / 256;
-    if (rounds <= 4)
+    if constexpr (QW) {  // chosen for groups of 5 to 8 rounds
+        if (rounds <= 5)
+            hipLaunchKernelGGL((gemv_kernel<T, MR, BITS, EPI, 5, 1, PREQ, 1, 256, false, true>), dim3(groups), dim3(320),
+                               lds, s, V);
+        else if (rounds <= 6)
+            hipLaunchKernelGGL((gemv_kernel<T, MR, BITS, EPI, 6, 1, PREQ, 1, 256, false, true>), dim3(groups), dim3(320),
+                               lds, s, V);
+        else
+            hipLaunchKernelGGL((gemv_kernel<T, MR, BITS, EPI, 8, 1, PREQ, 1, 256, false, true>), dim3(groups), dim3(320),
+                               lds, s, V);
+        return;
+    }
+    if (rounds <= 3)
+        hipLaunchKernelGGL((gemv_kernel<T, MR, BITS, EPI, 3, 1, PREQ>), dim3(groups), dim3(256), lds, s, V);
+    else if (rounds <= 4)
         hipLaunchKernelGGL((gemv_kernel<T, MR, BITS, EPI, 4, 1, PREQ>), dim3(groups), dim3(256), lds, s, V);
+    else if (rounds <= 5)
+        hipLaunchKernelGGL((gemv_kernel<T, MR, BITS, EPI, 5, 1, PREQ>), dim3(groups), dim3(256), lds, s, V);
     else if (rounds <= 6)
         hipLaunchKernelGGL((gemv_kernel<T, MR, BITS, EPI, 6, 1, PREQ>), dim3(groups), dim3(256), lds, s, V);
     else if (rounds <= 8)
         hipLaunchKernelGGL((gemv_kernel<T, MR, BITS, EPI, 8, 1, PREQ>), dim3(groups), dim3(256), lds, s, V);
+    else if (chunks <= 512 * 5)
+        hipLaunchKernelGGL((gemv_kernel<T, MR, BITS, EPI, 5, 1, PREQ, 1, 512>), dim3(groups), dim3(512), lds, s, V);
     else if (chunks <= 512 * 6)
         hipLaunchKernelGGL((gemv_kernel<T, MR, BITS, EPI, 6, 1, PREQ, 1, 512>), dim3(groups), dim3(512), lds, s, V);
+    else if (chunks <= 512 * 10)
+        hipLaunchKernelGGL((gemv_kernel<T, MR, BITS, EPI, 5, 2, PREQ, 1, 512>), dim3(groups), dim3(512), lds, s, V);
     else
         hipLaunchKernelGGL((gemv_kernel<T, MR, BITS, EPI, 8, 2, PREQ, 1, 512>), dim3(groups), dim3(512), lds, s, V);
 }
 
+// Rows quantized beforehand (preq), by the block's quantization wave (qw:
+// one or two rows that fit it), or by every thread of the block.
 template <typename T, int MR, int BITS, int EPI>
-static void launch_gemv_mr(const GemvParams& V, int groups, size_t lds, hipStream_t s, bool preq) {
-    if (preq)
-        launch_gemv_w<float, MR, BITS, EPI, true>(V, groups, lds, s);  // activations unused
-    else
-        launch_gemv_w<T, MR, BITS, EPI, false>(V, groups, lds, s);
+static void launch_gemv_mr(const GemvParams& V, int groups, size_t lds, hipStream_t s, bool preq, bool qw) {
+    if constexpr (MR >= 4) {
+        (void)preq;  // 4 or more rows are always quantized beforehand (enqueue_linear)
+        (void)qw;
+        launch_gemv_w<float, MR, BITS, EPI, true, false>(V, groups, lds, s);
+    } else {
+        if (preq)
+            launch_gemv_w<float, MR, BITS, EPI, true, false>(V, groups, lds, s);  // activations unused
+        else if (qw)
+            launch_gemv_w<T, MR, BITS, EPI, false, true>(V, groups, lds, s);
+        else
+            launch_gemv_w<T, MR, BITS, EPI, false, false>(V, groups, lds, s);
+    }
 }
 
 template <typename T, int BITS, int EPI>
-static void launch_gemv(int mr, const GemvParams& V, int grid, size_t lds, hipStream_t s, bool preq) {
+static void launch_gemv(int mr, const GemvParams& V, int grid, size_t lds, hipStream_t s, bool preq, bool qw) {
     switch (mr) {
         case 1:
-            launch_gemv_mr<T, 1, BITS, EPI>(V, grid, lds, s, preq);
+            launch_gemv_mr<T, 1, BITS, EPI>(V, grid, lds, s, preq, qw);
             break;
         case 2:
-            launch_gemv_mr<T, 2, BITS, EPI>(V, grid, lds, s, preq);
+            launch_gemv_mr<T, 2, BITS, EPI>(V, grid, lds, s, preq, qw);
             break;
         case 4:
-            launch_gemv_mr<T, 4, BITS, EPI>(V, grid, lds, s, preq);
+            launch_gemv_mr<T, 4, BITS, EPI>(V, grid, lds, s, preq, qw);
             break;
         default:
-            launch_gemv_mr<T, 8, BITS, EPI>(V, grid, lds, s, preq);
+            launch_gemv_mr<T, 8, BITS, EPI>(V, grid, lds, s, preq, qw);
             break;
     }
 }
 
 template <typename T, int BITS>
-static void launch_gemv_epi(int epi, int mr, const GemvParams& V, int grid, size_t lds, hipStream_t s, bool preq) {
+static void launch_gemv_epi(int epi, int mr, const GemvParams& V, int grid, size_t lds, hipStream_t s, bool preq,
+                            bool qw) {
     if (epi == EPI_PLAIN)
-        launch_gemv<T, BITS, EPI_PLAIN>(mr, V, grid, lds, s, preq);
+        launch_gemv<T, BITS, EPI_PLAIN>(mr, V, grid, lds, s, preq, qw);
     else
-        launch_gemv<T, BITS, EPI_SWIGLU_MAX>(mr, V, grid, lds, s, preq);
+        launch_gemv<T, BITS, EPI_SWIGLU_MAX>(mr, V, grid, lds, s, preq, qw);
 }
 
 int enqueue_linear(Workspace* ws, const Weights* w, const void* x, int x_type, long lda, int rows, int rule,
@@ -695,6 +727,14 @@ int enqueue_linear(Workspace* ws, const Weights* w, const void* x, int x_type, l
         // so are 4 or more rows, where every block re-quantizing all rows costs
         // more than one extra launch (M=4 decode set: 1002 -> 1090 GB/s).
         const bool preq = pv.mr >= 4 || !V.vec || (g.K_pad / 16) * pv.mr > 256 * GEMV_XMAX;
+        // One or two rows that fit the quantization wave of the block are
+        // quantized by that wave beside a long weight stream (5 to 8 rounds
+        // per group: gate/up 2560x19456 W4 M=1 7.5 -> 6.7 us). Shorter streams
+        // arrive before the wave's serial chain ends (qkv 4.3 -> 4.9 us, o
+        // 4096x2560 3.9 -> 5.4 us with it), so their blocks quantize as a whole.
+        const int w_rounds = ((g.bits == 8 ? g.K_pad / 16 : g.K_pad / 32) * 8 * (epi == EPI_PLAIN ? 1 : 2) + 255) / 256;
+        const int qb = x_type == DT_F32 ? gemv_qb<float>() : gemv_qb<__half>();
+        const bool qw = !preq && pv.mr <= 2 && (g.K_pad / 16) * pv.mr <= 64 * qb && w_rounds >= 5 && w_rounds <= 8;
         if (preq) {
             int rc = enqueue_quant(ws, x, x_type, lda, rows, rule, in_max, nullptr, s);
             if (rc != RK_NPU_OK) return rc;
@@ -704,14 +744,14 @@ int enqueue_linear(Workspace* ws, const Weights* w, const void* x, int x_type, l
         const int slot = prof_begin(s, 0, g.bits, epi, rows, g.K, g.N, name);
         if (x_type == DT_F32) {
             if (g.bits == 8)
-                launch_gemv_epi<float, 8>(epi, pv.mr, V, grid, lds, s, preq);
+                launch_gemv_epi<float, 8>(epi, pv.mr, V, grid, lds, s, preq, qw);
             else
-                launch_gemv_epi<float, 4>(epi, pv.mr, V, grid, lds, s, preq);
+                launch_gemv_epi<float, 4>(epi, pv.mr, V, grid, lds, s, preq, qw);
         } else {
             if (g.bits == 8)
-                launch_gemv_epi<__half, 8>(epi, pv.mr, V, grid, lds, s, preq);
+                launch_gemv_epi<__half, 8>(epi, pv.mr, V, grid, lds, s, preq, qw);
             else
-                launch_gemv_epi<__half, 4>(epi, pv.mr, V, grid, lds, s, preq);
+                launch_gemv_epi<__half, 4>(epi, pv.mr, V, grid, lds, s, preq, qw);
         }
         prof_end(slot, s);
         if (out_max) *out_max = RowMax{ws->partmax, grid};

@@ -1156,9 +1156,126 @@ struct GemvParams {
 };
 
 
+// Activation chunks per lane of the quantization wave (QW blocks): rows of at
+// most 64 * GEMV_QB chunks in all (M * K / 16) take that path.
+template <typename T>
+constexpr int gemv_qb() { return sizeof(T) == 2 ? 4 : 3; }
+
+// The quantization wave of a QW block: the wave loads every activation row of
+// the block, takes the row maxima from them (or from the precomputed partial
+// maxima), writes the codes [k16][row][16] to LDS and each row's scale and W4
+// correction (8 * code sum) to s_scale / s_corr. It runs beside the weight
+// waves, which only issue their weight loads and then wait at the block
+// barrier, so the quantization chain (row max, scale, codes) overlaps the
+// weight stream instead of following the weight waves' load issue.
+template <typename T, int MR, int BITS>
+__device__ __forceinline__ void gemv_quant_wave(const GemvParams& P, int8_t* sa, float* s_scale, int* s_corr,
+                                                int lane) {
+    constexpr int QB = gemv_qb<T>();
+    constexpr int PB = 8;  // precomputed partial maxima per lane per batch
+    const int chunks = (P.K_pad >> 4) * MR;
+    const T* x = static_cast<const T*>(P.x);
+    // a masked lane reads its own chunk of row 0 (never one shared address)
+    const T* spare = x + (size_t)min(lane, (P.K >> 4) - 1) * 16;
+    v4u xr[QB][4];
+#pragma unroll
+    for (int j = 0; j < QB; ++j) {
+        if (64 * j >= chunks) break;
+        const int c = lane + 64 * j, kg = c / MR, m = c % MR;
+        const bool ok = c < chunks && m < P.M && kg * 16 < P.K;
+        load16_raw(ok ? x + (size_t)m * P.lda + kg * 16 : spare, xr[j]);
+    }
+    auto chunk_vals = [&](int j, float (&v)[16]) {
+        const int c = lane + 64 * j, kg = c / MR, m = c % MR;
+        const bool ok = c < chunks && m < P.M && kg * 16 < P.K;
+        cvt16_raw(xr[j], v, T());
+#pragma unroll
+        for (int b = 0; b < 16; ++b) v[b] = ok ? v[b] : 0.0f;
+    };
+    float mx[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) mx[m] = 0.0f;
+    if (P.part_in) {
+        const int spare_idx = lane < P.part_count ? lane : 0;
+        for (int base = 0; base < P.part_count; base += 64 * PB) {
+            float pv[MR][PB];
+#pragma unroll
+            for (int i = 0; i < PB; ++i)
+#pragma unroll
+                for (int m = 0; m < MR; ++m) {
+                    const int idx = base + lane + 64 * i;
+                    const bool ok = m < P.M && idx < P.part_count;
+                    pv[m][i] = P.part_in[ok ? (size_t)m * P.part_count + idx : (size_t)spare_idx];
+                }
+#pragma unroll
+            for (int i = 0; i < PB; ++i)
+#pragma unroll
+                for (int m = 0; m < MR; ++m)
+                    if (m < P.M && base + lane + 64 * i < P.part_count) mx[m] = fmaxf(mx[m], pv[m][i]);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < QB; ++j) {
+            if (lane + 64 * j >= chunks) continue;
+            float v[16];
+            chunk_vals(j, v);
+            float lm = 0.0f;
+#pragma unroll
+            for (int b = 0; b < 16; ++b) lm = fmaxf(lm, fabsf(v[b]));
+            const int m = (lane + 64 * j) % MR;
+#pragma unroll
+            for (int r = 0; r < MR; ++r) mx[r] = (r == m) ? fmaxf(mx[r], lm) : mx[r];
+        }
+    }
+    float scale[MR], inv[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+        const float v = wave_max(mx[m]);
+        if (P.rule == QUANT_DENSE)
+            scale[m] = (v == 0.0f) ? 1.0f : fmaxf(v / 127.0f, FLT_MIN);
+        else
+            scale[m] = (v == 0.0f) ? 1.0f : v / 127.0f;
+        inv[m] = 1.0f / scale[m];
+    }
+    const bool diag = blockIdx.x == 0 && P.diag_codes;
+    int psum[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) psum[m] = 0;
+#pragma unroll
+    for (int j = 0; j < QB; ++j) {
+        const int c = lane + 64 * j, m = c % MR;
+        if (c >= chunks) continue;
+        float v[16];
+        chunk_vals(j, v);
+        float iv = inv[0];
+#pragma unroll
+        for (int r = 1; r < MR; ++r) iv = (r == m) ? inv[r] : iv;
+        int sum = 0;
+        const v4u pk = (P.rule == QUANT_DENSE) ? quant_chunk<QUANT_DENSE>(v, iv, sum) : quant_chunk<QUANT_MOE>(v, iv, sum);
+#pragma unroll
+        for (int r = 0; r < MR; ++r) psum[r] += (r == m) ? sum : 0;
+        *reinterpret_cast<v4u*>(sa + c * 16) = pk;
+        if (diag) *reinterpret_cast<v4u*>(P.diag_codes + ((size_t)(c / MR) * P.M_alloc + m) * 16) = pk;
+    }
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+        const int isum = wave_sum(psum[m]);
+        if (lane == 0) {
+            s_scale[m] = scale[m];
+            s_corr[m] = BITS == 4 ? 8 * isum : 0;
+        }
+        if (diag && lane == 0 && m < P.M) {
+            P.diag_scale[m] = scale[m];
+            P.diag_rowsum[m] = isum;
+        }
+    }
+}
+
+// QW: the block has a quantization wave (gemv_quant_wave) before its NTHR
+// weight threads; the rows must fit it (at most 64 * gemv_qb<T>() chunks).
 template <typename T, int MR, int BITS, int EPI, int RW, int NW, bool PREQ, int GPB = 1, int NTHR = 256,
-          bool GROUPED = false>
-__global__ __launch_bounds__(NTHR) void gemv_kernel(GemvParams P) {
+          bool GROUPED = false, bool QW = false>
+__global__ __launch_bounds__(NTHR + (QW ? 64 : 0)) void gemv_kernel(GemvParams P) {
     extern __shared__ __attribute__((aligned(16))) int8_t sa[];  // [K_pad/16][MR][16]
     if constexpr (GROUPED) {
         static_assert(MR == 1 && GPB == 1, "one slot row per block");
@@ -1191,7 +1308,25 @@ __global__ __launch_bounds__(NTHR) void gemv_kernel(GemvParams P) {
         for (int w = 0; w < NWV; ++w) v += s_isum[w][m];
         return v;
     };
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // (QW: hardware wave 0 is the quantization wave; the weight threads are
+    // numbered from the second wave on)
+    const int tid = (int)threadIdx.x - (QW ? 64 : 0), lane = threadIdx.x & 63, wave = tid >> 6;
+    if constexpr (QW) {
+        static_assert(!PREQ, "the quantization wave quantizes the rows");
+        if (threadIdx.x < 64) {
+            // First wave of the block and the highest issue priority: its row
+            // loads and its quantization chain go ahead of the weight waves'
+            // load issue (which stalls on the memory pipeline's back-pressure)
+            // instead of queuing behind it (gate/up 2560x19456 W4 M=1: 8.7 us
+            // as the last wave at normal priority, 6.5 us first at priority 3).
+            __builtin_amdgcn_s_setprio(3);
+            gemv_quant_wave<T, MR, BITS>(P, sa, s_red[0], s_isum[0], lane);
+            wait_lgkmcnt0();
+            __builtin_amdgcn_s_barrier();  // codes, scales and corrections are in LDS
+            __builtin_amdgcn_s_barrier();  // (the weight waves' partial sums)
+            return;
+        }
+    }
     const int c8 = tid & 7;
     const int KG16 = P.K_pad >> 4;
     const int PL = (BITS == 8) ? KG16 : (P.K_pad >> 5);
@@ -1249,7 +1384,7 @@ __global__ __launch_bounds__(NTHR) void gemv_kernel(GemvParams P) {
     const T* x = static_cast<const T*>(P.x);
 #pragma unroll
     for (int j = 0; j < XMAX; ++j) {
-        if (NTHR * j >= chunks) break;
+        if (QW || NTHR * j >= chunks) break;  // (QW: the quantization wave loads the rows)
         const int c = tid + NTHR * j, kg = c / MR, m = c % MR;
         if (PREQ) {
             const bool ok = c < chunks && m < P.M;
@@ -1262,7 +1397,7 @@ __global__ __launch_bounds__(NTHR) void gemv_kernel(GemvParams P) {
     }
     float pv[MR][PV];
     const float* own_cs = P.colscale + 8 * tile[0] + c8;
-    if (!PREQ && P.part_in) {
+    if (!PREQ && !QW && P.part_in) {
 #pragma unroll
         for (int i = 0; i < PV; ++i) {
             if (NTHR * i >= P.part_count) break;
@@ -1286,7 +1421,8 @@ __global__ __launch_bounds__(NTHR) void gemv_kernel(GemvParams P) {
             const uint8_t* base = tb[0];
 #pragma unroll
             for (int u = 1; u < TPB; ++u) base = (t == u) ? tb[u] : base;
-            buf[i] = *reinterpret_cast<const v4u*>(base + (size_t)r * 16);
+            // (streamed once: non-temporal)
+            buf[i] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(base + (size_t)r * 16));
         }
     };
     v4u wa[RW], wb[NW == 2 ? RW : 1];
@@ -1319,6 +1455,14 @@ __global__ __launch_bounds__(NTHR) void gemv_kernel(GemvParams P) {
         }
         wait_lgkmcnt0();
         __builtin_amdgcn_s_barrier();
+    } else if (QW) {
+        // 2-3. Codes, scales and corrections from the quantization wave.
+        __builtin_amdgcn_s_barrier();
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            scale[m] = s_red[0][m];
+            corr[m] = s_isum[0][m];
+        }
     } else {
         // 2. Row maxima (from the activations or the precomputed partials),
         // block max through LDS, row scales.
