@@ -380,7 +380,7 @@ Plan plan_linear(int rows, const Geometry& g) {
 // --- workspaces -------------------------------------------------------------
 
 struct WsLayout {
-    size_t a, codes, rows, c, part, split_part, total;
+    size_t a, codes, rows, c, part, split_part, kacc, total;
     size_t split_part_ints;
 };
 
@@ -402,7 +402,8 @@ static WsLayout ws_layout(const Geometry& g, int M) {
     L.part = round_up_z((size_t)8 * (g.N_pad / 8) * 4, 256);
     L.split_part_ints = split_need(g, M);
     L.split_part = round_up_z(L.split_part_ints * 4, 256);
-    L.total = L.a + L.codes + 3 * L.rows + L.c + L.part + L.split_part;
+    L.kacc = round_up_z(((size_t)g.N_pad + 8) * 8, 256);
+    L.total = L.a + L.codes + 3 * L.rows + L.c + L.part + L.split_part + L.kacc;
     return L;
 }
 
@@ -445,6 +446,8 @@ Workspace* workspace_create(Domain* d, int bits, int M, int K, int N) {
     off += L.part;
     ws->split_part = reinterpret_cast<int*>(base + off);
     ws->split_part_ints = L.split_part_ints;
+    off += L.split_part;
+    ws->kacc = reinterpret_cast<unsigned long long*>(base + off);
     // Zero everything once (padding rows of the code planes stay zero).
     bool ok = hipMemset(base, 0, L.total) == hipSuccess &&
               hipStreamCreateWithFlags(&ws->stream, hipStreamNonBlocking) == hipSuccess &&
@@ -603,7 +606,7 @@ static void launch_gemm(int v, bool staged, const GemmParams& G, int tiles, hipS
     }
 }
 
-template <typename T, int MR, int BITS, int EPI, bool PREQ, bool QW>
+template <typename T, int MR, int BITS, int EPI, bool PREQ, int QWN>
 static void launch_gemv_w(const GemvParams& V, int groups, size_t lds, hipStream_t s) {
     // Register windows sized to the group (rounds of 256 16-byte chunks), so
     // no thread loads a chunk past the group's end and no registers hold one:
@@ -614,15 +617,15 @@ static void launch_gemv_w(const GemvParams& V, int groups, size_t lds, hipStream
     const int planes = BITS == 8 ? V.K_pad / 16 : V.K_pad / 32;
     const int chunks = planes * 8 * (EPI == EPI_PLAIN ? 1 : 2);
     const int rounds = (chunks + 255) / 256;
-    if constexpr (QW) {  // chosen for groups of 5 to 8 rounds
+    if constexpr (QWN == 1) {  // groups of 5 to 8 rounds
         if (rounds <= 5)
-            hipLaunchKernelGGL((gemv_kernel<T, MR, BITS, EPI, 5, 1, PREQ, 1, 256, false, true>), dim3(groups), dim3(320),
+            hipLaunchKernelGGL((gemv_kernel<T, MR, BITS, EPI, 5, 1, PREQ, 1, 256, false, 1>), dim3(groups), dim3(320),
                                lds, s, V);
         else if (rounds <= 6)
-            hipLaunchKernelGGL((gemv_kernel<T, MR, BITS, EPI, 6, 1, PREQ, 1, 256, false, true>), dim3(groups), dim3(320),
+            hipLaunchKernelGGL((gemv_kernel<T, MR, BITS, EPI, 6, 1, PREQ, 1, 256, false, 1>), dim3(groups), dim3(320),
                                lds, s, V);
         else
-            hipLaunchKernelGGL((gemv_kernel<T, MR, BITS, EPI, 8, 1, PREQ, 1, 256, false, true>), dim3(groups), dim3(320),
+            hipLaunchKernelGGL((gemv_kernel<T, MR, BITS, EPI, 8, 1, PREQ, 1, 256, false, 1>), dim3(groups), dim3(320),
                                lds, s, V);
         return;
     }
@@ -646,49 +649,69 @@ static void launch_gemv_w(const GemvParams& V, int groups, size_t lds, hipStream
         hipLaunchKernelGGL((gemv_kernel<T, MR, BITS, EPI, 8, 2, PREQ, 1, 512>), dim3(groups), dim3(512), lds, s, V);
 }
 
-// Rows quantized beforehand (preq), by the block's quantization wave (qw:
-// one or two rows that fit it), or by every thread of the block.
+// Split-K GEMV (one row, plain epilogue): rounds of the largest piece.
+template <typename T, int BITS>
+static void launch_gemv_split(const GemvParams& V, int grid, int rounds, size_t lds, hipStream_t s) {
+    if (rounds <= 3)
+        hipLaunchKernelGGL((gemv_kernel<T, 1, BITS, EPI_PLAIN, 3, 1, false, 1, 256, false, 0, true>), dim3(grid),
+                           dim3(256), lds, s, V);
+    else if (rounds <= 4)
+        hipLaunchKernelGGL((gemv_kernel<T, 1, BITS, EPI_PLAIN, 4, 1, false, 1, 256, false, 0, true>), dim3(grid),
+                           dim3(256), lds, s, V);
+    else if (rounds <= 5)
+        hipLaunchKernelGGL((gemv_kernel<T, 1, BITS, EPI_PLAIN, 5, 1, false, 1, 256, false, 0, true>), dim3(grid),
+                           dim3(256), lds, s, V);
+    else if (rounds <= 6)
+        hipLaunchKernelGGL((gemv_kernel<T, 1, BITS, EPI_PLAIN, 6, 1, false, 1, 256, false, 0, true>), dim3(grid),
+                           dim3(256), lds, s, V);
+    else
+        hipLaunchKernelGGL((gemv_kernel<T, 1, BITS, EPI_PLAIN, 8, 1, false, 1, 256, false, 0, true>), dim3(grid),
+                           dim3(256), lds, s, V);
+}
+
+// Rows quantized beforehand (preq), by a quantization wave of the block
+// (qwn = 1), or by every thread of the block.
 template <typename T, int MR, int BITS, int EPI>
-static void launch_gemv_mr(const GemvParams& V, int groups, size_t lds, hipStream_t s, bool preq, bool qw) {
+static void launch_gemv_mr(const GemvParams& V, int groups, size_t lds, hipStream_t s, bool preq, int qwn) {
     if constexpr (MR >= 4) {
         (void)preq;  // 4 or more rows are always quantized beforehand (enqueue_linear)
-        (void)qw;
-        launch_gemv_w<float, MR, BITS, EPI, true, false>(V, groups, lds, s);
+        (void)qwn;
+        launch_gemv_w<float, MR, BITS, EPI, true, 0>(V, groups, lds, s);
     } else {
         if (preq)
-            launch_gemv_w<float, MR, BITS, EPI, true, false>(V, groups, lds, s);  // activations unused
-        else if (qw)
-            launch_gemv_w<T, MR, BITS, EPI, false, true>(V, groups, lds, s);
+            launch_gemv_w<float, MR, BITS, EPI, true, 0>(V, groups, lds, s);  // activations unused
+        else if (qwn == 1)
+            launch_gemv_w<T, MR, BITS, EPI, false, 1>(V, groups, lds, s);
         else
-            launch_gemv_w<T, MR, BITS, EPI, false, false>(V, groups, lds, s);
+            launch_gemv_w<T, MR, BITS, EPI, false, 0>(V, groups, lds, s);
     }
 }
 
 template <typename T, int BITS, int EPI>
-static void launch_gemv(int mr, const GemvParams& V, int grid, size_t lds, hipStream_t s, bool preq, bool qw) {
+static void launch_gemv(int mr, const GemvParams& V, int grid, size_t lds, hipStream_t s, bool preq, int qwn) {
     switch (mr) {
         case 1:
-            launch_gemv_mr<T, 1, BITS, EPI>(V, grid, lds, s, preq, qw);
+            launch_gemv_mr<T, 1, BITS, EPI>(V, grid, lds, s, preq, qwn);
             break;
         case 2:
-            launch_gemv_mr<T, 2, BITS, EPI>(V, grid, lds, s, preq, qw);
+            launch_gemv_mr<T, 2, BITS, EPI>(V, grid, lds, s, preq, qwn);
             break;
         case 4:
-            launch_gemv_mr<T, 4, BITS, EPI>(V, grid, lds, s, preq, qw);
+            launch_gemv_mr<T, 4, BITS, EPI>(V, grid, lds, s, preq, qwn);
             break;
         default:
-            launch_gemv_mr<T, 8, BITS, EPI>(V, grid, lds, s, preq, qw);
+            launch_gemv_mr<T, 8, BITS, EPI>(V, grid, lds, s, preq, qwn);
             break;
     }
 }
 
 template <typename T, int BITS>
 static void launch_gemv_epi(int epi, int mr, const GemvParams& V, int grid, size_t lds, hipStream_t s, bool preq,
-                            bool qw) {
+                            int qwn) {
     if (epi == EPI_PLAIN)
-        launch_gemv<T, BITS, EPI_PLAIN>(mr, V, grid, lds, s, preq, qw);
+        launch_gemv<T, BITS, EPI_PLAIN>(mr, V, grid, lds, s, preq, qwn);
     else
-        launch_gemv<T, BITS, EPI_SWIGLU_MAX>(mr, V, grid, lds, s, preq, qw);
+        launch_gemv<T, BITS, EPI_SWIGLU_MAX>(mr, V, grid, lds, s, preq, qwn);
 }
 
 int enqueue_linear(Workspace* ws, const Weights* w, const void* x, int x_type, long lda, int rows, int rule,
@@ -720,6 +743,8 @@ int enqueue_linear(Workspace* ws, const Weights* w, const void* x, int x_type, l
         V.diag_scale = ws->rowscale;
         V.diag_rowsum = ws->rowsum;
         V.M_alloc = ws->M_alloc;
+        V.ksplit = 1;
+        V.kacc = ws->kacc;
         const int grid = epi == EPI_PLAIN ? g.N_pad / 8 : g.N_pad / 16;
         const size_t lds = (size_t)g.K_pad * pv.mr;
         // Rows the kernel cannot quantize from registers (unaligned or ragged
@@ -732,9 +757,31 @@ int enqueue_linear(Workspace* ws, const Weights* w, const void* x, int x_type, l
         // per group: gate/up 2560x19456 W4 M=1 7.5 -> 6.7 us). Shorter streams
         // arrive before the wave's serial chain ends (qkv 4.3 -> 4.9 us, o
         // 4096x2560 3.9 -> 5.4 us with it), so their blocks quantize as a whole.
-        const int w_rounds = ((g.bits == 8 ? g.K_pad / 16 : g.K_pad / 32) * 8 * (epi == EPI_PLAIN ? 1 : 2) + 255) / 256;
+        const int w_chunks = (g.bits == 8 ? g.K_pad / 16 : g.K_pad / 32) * 8 * (epi == EPI_PLAIN ? 1 : 2);
+        const int w_rounds = (w_chunks + 255) / 256;
+        const int x_chunks = (g.K_pad / 16) * pv.mr;
         const int qb = x_type == DT_F32 ? gemv_qb<float>() : gemv_qb<__half>();
-        const bool qw = !preq && pv.mr <= 2 && (g.K_pad / 16) * pv.mr <= 64 * qb && w_rounds >= 5 && w_rounds <= 8;
+        int qwn = 0;
+        if (!preq && pv.mr <= 2 && x_chunks <= 64 * qb && w_rounds >= 5 && w_rounds <= 8) qwn = 1;
+        // One row with precomputed maxima (the down projection after the
+        // SwiGLU GEMV) whose groups stream more than 8 rounds splits K so that
+        // about 1280 blocks run (5 per CU) and each quantizes only its piece
+        // of the row: the 320 blocks of the 9728x2560 down projection each
+        // loaded and quantized all 38.9 KB of the f32 row before their first
+        // dot product (7.45 -> 7.1 us; decode step +3.4% at 4 pieces, 6 and 8
+        // pieces slower). Short groups lose to the pieces' extra partial-max
+        // loads and atomic tail (MoE shared down 2048x2048). Pieces are whole
+        // 64-k units, at least 8 of them; HM_GEMV_SPLITS forces a count.
+        const int units = g.K_pad / 64;
+        int ksplit = 1;
+        const int forced_splits = env_int("HM_GEMV_SPLITS", 0);
+        if (!preq && qwn == 0 && pv.mr == 1 && epi == EPI_PLAIN && in_max.p && (w_rounds > 8 || forced_splits > 0)) {
+            ksplit = forced_splits > 0 ? forced_splits : (1280 + grid / 2) / grid;
+            ksplit = std::max(1, std::min(std::min(ksplit, 8), units / 8));
+        }
+        const int piece_units = (units + ksplit - 1) / ksplit;
+        const int piece_rounds = ((g.bits == 8 ? 4 : 2) * piece_units * 8 + 255) / 256;
+        if (ksplit > 1 && piece_rounds > 8) ksplit = 1;
         if (preq) {
             int rc = enqueue_quant(ws, x, x_type, lda, rows, rule, in_max, nullptr, s);
             if (rc != RK_NPU_OK) return rc;
@@ -742,16 +789,30 @@ int enqueue_linear(Workspace* ws, const Weights* w, const void* x, int x_type, l
         char name[64];
         std::snprintf(name, sizeof(name), "gemv<mr=%d,w%d,epi=%d>", pv.mr, g.bits, epi);
         const int slot = prof_begin(s, 0, g.bits, epi, rows, g.K, g.N, name);
-        if (x_type == DT_F32) {
+        if (ksplit > 1) {
+            V.ksplit = ksplit;
+            const size_t piece_lds = (size_t)64 * piece_units;
+            if (x_type == DT_F32) {
+                if (g.bits == 8)
+                    launch_gemv_split<float, 8>(V, grid * ksplit, piece_rounds, piece_lds, s);
+                else
+                    launch_gemv_split<float, 4>(V, grid * ksplit, piece_rounds, piece_lds, s);
+            } else {
+                if (g.bits == 8)
+                    launch_gemv_split<__half, 8>(V, grid * ksplit, piece_rounds, piece_lds, s);
+                else
+                    launch_gemv_split<__half, 4>(V, grid * ksplit, piece_rounds, piece_lds, s);
+            }
+        } else if (x_type == DT_F32) {
             if (g.bits == 8)
-                launch_gemv_epi<float, 8>(epi, pv.mr, V, grid, lds, s, preq, qw);
+                launch_gemv_epi<float, 8>(epi, pv.mr, V, grid, lds, s, preq, qwn);
             else
-                launch_gemv_epi<float, 4>(epi, pv.mr, V, grid, lds, s, preq, qw);
+                launch_gemv_epi<float, 4>(epi, pv.mr, V, grid, lds, s, preq, qwn);
         } else {
             if (g.bits == 8)
-                launch_gemv_epi<__half, 8>(epi, pv.mr, V, grid, lds, s, preq, qw);
+                launch_gemv_epi<__half, 8>(epi, pv.mr, V, grid, lds, s, preq, qwn);
             else
-                launch_gemv_epi<__half, 4>(epi, pv.mr, V, grid, lds, s, preq, qw);
+                launch_gemv_epi<__half, 4>(epi, pv.mr, V, grid, lds, s, preq, qwn);
         }
         prof_end(slot, s);
         if (out_max) *out_max = RowMax{ws->partmax, grid};

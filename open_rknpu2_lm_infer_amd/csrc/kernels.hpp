@@ -242,17 +242,46 @@ __device__ __forceinline__ int sum4(unsigned w, int acc) {
     return __builtin_amdgcn_sdot4((int)w, 0x01010101, acc, false);
 }
 
-// 16 values -> 16 int8 codes of v * inv, sum += codes.
+// 16 already scaled values -> 16 int8 codes, sum += codes.
 template <int RULE>
-__device__ __forceinline__ v4u quant_chunk(const float (&v)[16], float inv, int& sum) {
+__device__ __forceinline__ v4u quant_scaled(const float (&sv)[16], int& sum) {
     unsigned packed[4];
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-        packed[w] = pack4(quant_code<RULE>(v[4 * w] * inv), quant_code<RULE>(v[4 * w + 1] * inv),
-                          quant_code<RULE>(v[4 * w + 2] * inv), quant_code<RULE>(v[4 * w + 3] * inv));
+        packed[w] = pack4(quant_code<RULE>(sv[4 * w]), quant_code<RULE>(sv[4 * w + 1]), quant_code<RULE>(sv[4 * w + 2]),
+                          quant_code<RULE>(sv[4 * w + 3]));
         sum = sum4(packed[w], sum);
     }
     return v4u{packed[0], packed[1], packed[2], packed[3]};
+}
+
+// 16 values -> 16 int8 codes of v * inv, sum += codes.
+template <int RULE>
+__device__ __forceinline__ v4u quant_chunk(const float (&v)[16], float inv, int& sum) {
+    float sv[16];
+#pragma unroll
+    for (int b = 0; b < 16; ++b) sv[b] = v[b] * inv;
+    return quant_scaled<RULE>(sv, sum);
+}
+
+// v * inv for 16 raw activations: f32 as is; fp16 through v_fma_mix_f32, the
+// conversion folded into the multiply: fma(h, inv, -0) is the product rounded
+// once, exactly h * inv (the -0 addend keeps signed zeros; it is held in a
+// register the compiler cannot see through, or it would fold the fma back
+// into a convert and a multiply).
+__device__ __forceinline__ void scale16_raw(const v4u (&r)[4], float inv, float (&sv)[16], float) {
+#pragma unroll
+    for (int b = 0; b < 16; ++b) sv[b] = __uint_as_float(r[b >> 2][b & 3]) * inv;
+}
+__device__ __forceinline__ void scale16_raw(const v4u (&r)[4], float inv, float (&sv)[16], __half) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    float nz;
+    asm volatile("v_mov_b32 %0, 0x80000000" : "=v"(nz));
+#pragma unroll
+    for (int b = 0; b < 16; ++b) {
+        const h2 pair = __builtin_bit_cast(h2, r[b >> 3][(b >> 1) & 3]);
+        sv[b] = __builtin_fmaf((float)pair[b & 1], inv, nz);
+    }
 }
 
 template <int RULE>
@@ -1153,49 +1182,68 @@ struct GemvParams {
     const int* ids;
     const int* slot_count;
     int top;
+    // Split K (one row, plain epilogue, row maxima as partials): block b is
+    // piece b % ksplit of group b / ksplit over its share of the 64-k units.
+    // Each piece adds (1 << 40) + (its exact int32 column sum + 2^31) into the
+    // column's 64-bit slot kacc[col]: bits 40 and up count the pieces, the
+    // low 40 bits hold the biased sum (below ksplit * 2^32 <= 2^35). The piece
+    // that sees ksplit - 1 earlier pieces finishes the column and clears the
+    // slot; kacc[N_pad] collects the row's code sum for diagnostics the same
+    // way.
+    int ksplit;
+    unsigned long long* kacc;
 };
 
 
-// Activation chunks per lane of the quantization wave (QW blocks): rows of at
-// most 64 * GEMV_QB chunks in all (M * K / 16) take that path.
+// Activation chunks per lane of the quantization wave (QWN = 1 blocks): rows
+// of at most 64 * gemv_qb<T>() chunks in all (M * K / 16) take that path.
 template <typename T>
 constexpr int gemv_qb() { return sizeof(T) == 2 ? 4 : 3; }
 
-// The quantization wave of a QW block: the wave loads every activation row of
-// the block, takes the row maxima from them (or from the precomputed partial
-// maxima), writes the codes [k16][row][16] to LDS and each row's scale and W4
-// correction (8 * code sum) to s_scale / s_corr. It runs beside the weight
-// waves, which only issue their weight loads and then wait at the block
-// barrier, so the quantization chain (row max, scale, codes) overlaps the
-// weight stream instead of following the weight waves' load issue.
-template <typename T, int MR, int BITS>
-__device__ __forceinline__ void gemv_quant_wave(const GemvParams& P, int8_t* sa, float* s_scale, int* s_corr,
-                                                int lane) {
+// The quantization wave of a block with QWN = 1 (threads 0-63): it loads the
+// block's activation rows (chunk c = lane + 64*j, in registers), takes each
+// row's max from them or from the precomputed partial maxima, and writes the
+// codes [k16][row][16] to LDS, the row scales to s_scale and the code sums to
+// s_sum[0]. It runs beside the weight waves, which only issue their weight
+// loads and then wait at the block barrier, so the quantization chain overlaps
+// the weight stream instead of following the weight waves' load issue. (The
+// code keeps QWN general; four such waves in front of the 512-thread down
+// projection were slower than its in-block quantization: 7.3 -> 7.8 us, the
+// partial-maxima batches of each wave running in series.)
+template <typename T, int MR, int QWN>
+__device__ __forceinline__ void gemv_quant_waves(const GemvParams& P, int8_t* sa, float* s_scale,
+                                                 int (*s_sum)[MR], int qt) {
     constexpr int QB = gemv_qb<T>();
+    constexpr int QT = 64 * QWN;
     constexpr int PB = 8;  // precomputed partial maxima per lane per batch
+    const int lane = qt & 63, qwave = qt >> 6;
     const int chunks = (P.K_pad >> 4) * MR;
     const T* x = static_cast<const T*>(P.x);
     // a masked lane reads its own chunk of row 0 (never one shared address)
-    const T* spare = x + (size_t)min(lane, (P.K >> 4) - 1) * 16;
+    const T* spare = x + (size_t)min(qt, (P.K >> 4) - 1) * 16;
     v4u xr[QB][4];
 #pragma unroll
     for (int j = 0; j < QB; ++j) {
-        if (64 * j >= chunks) break;
-        const int c = lane + 64 * j, kg = c / MR, m = c % MR;
+        if (QT * j >= chunks) break;
+        const int c = qt + QT * j, kg = c / MR, m = c % MR;
         const bool ok = c < chunks && m < P.M && kg * 16 < P.K;
         load16_raw(ok ? x + (size_t)m * P.lda + kg * 16 : spare, xr[j]);
     }
-    auto chunk_vals = [&](int j, float (&v)[16]) {
-        const int c = lane + 64 * j, kg = c / MR, m = c % MR;
-        const bool ok = c < chunks && m < P.M && kg * 16 < P.K;
-        cvt16_raw(xr[j], v, T());
+    // words of a chunk the lane does not own (it read its spare chunk) are
+    // zeroed once, before both passes
 #pragma unroll
-        for (int b = 0; b < 16; ++b) v[b] = ok ? v[b] : 0.0f;
-    };
+    for (int j = 0; j < QB; ++j) {
+        if (QT * j >= chunks) break;
+        const int c = qt + QT * j, kg = c / MR, m = c % MR;
+        const bool ok = c < chunks && m < P.M && kg * 16 < P.K;
+#pragma unroll
+        for (int q = 0; q < (int)sizeof(T); ++q)  // (sizeof(T) 16-byte words per chunk)
+            xr[j][q] = ok ? xr[j][q] : v4u{0u, 0u, 0u, 0u};
+    }
     float mx[MR];
 #pragma unroll
     for (int m = 0; m < MR; ++m) mx[m] = 0.0f;
-    if (P.part_in) {
+    if (QWN > 1 || P.part_in) {
         const int spare_idx = lane < P.part_count ? lane : 0;
         for (int base = 0; base < P.part_count; base += 64 * PB) {
             float pv[MR][PB];
@@ -1216,13 +1264,13 @@ __device__ __forceinline__ void gemv_quant_wave(const GemvParams& P, int8_t* sa,
     } else {
 #pragma unroll
         for (int j = 0; j < QB; ++j) {
-            if (lane + 64 * j >= chunks) continue;
+            if (qt + QT * j >= chunks) continue;
             float v[16];
-            chunk_vals(j, v);
+            cvt16_raw(xr[j], v, T());
             float lm = 0.0f;
 #pragma unroll
             for (int b = 0; b < 16; ++b) lm = fmaxf(lm, fabsf(v[b]));
-            const int m = (lane + 64 * j) % MR;
+            const int m = (qt + QT * j) % MR;
 #pragma unroll
             for (int r = 0; r < MR; ++r) mx[r] = (r == m) ? fmaxf(mx[r], lm) : mx[r];
         }
@@ -1243,15 +1291,15 @@ __device__ __forceinline__ void gemv_quant_wave(const GemvParams& P, int8_t* sa,
     for (int m = 0; m < MR; ++m) psum[m] = 0;
 #pragma unroll
     for (int j = 0; j < QB; ++j) {
-        const int c = lane + 64 * j, m = c % MR;
+        const int c = qt + QT * j, m = c % MR;
         if (c >= chunks) continue;
-        float v[16];
-        chunk_vals(j, v);
         float iv = inv[0];
 #pragma unroll
         for (int r = 1; r < MR; ++r) iv = (r == m) ? inv[r] : iv;
+        float sv[16];
+        scale16_raw(xr[j], iv, sv, T());
         int sum = 0;
-        const v4u pk = (P.rule == QUANT_DENSE) ? quant_chunk<QUANT_DENSE>(v, iv, sum) : quant_chunk<QUANT_MOE>(v, iv, sum);
+        const v4u pk = (P.rule == QUANT_DENSE) ? quant_scaled<QUANT_DENSE>(sv, sum) : quant_scaled<QUANT_MOE>(sv, sum);
 #pragma unroll
         for (int r = 0; r < MR; ++r) psum[r] += (r == m) ? sum : 0;
         *reinterpret_cast<v4u*>(sa + c * 16) = pk;
@@ -1261,22 +1309,36 @@ __device__ __forceinline__ void gemv_quant_wave(const GemvParams& P, int8_t* sa,
     for (int m = 0; m < MR; ++m) {
         const int isum = wave_sum(psum[m]);
         if (lane == 0) {
-            s_scale[m] = scale[m];
-            s_corr[m] = BITS == 4 ? 8 * isum : 0;
-        }
-        if (diag && lane == 0 && m < P.M) {
-            P.diag_scale[m] = scale[m];
-            P.diag_rowsum[m] = isum;
+            if (qwave == 0) s_scale[m] = scale[m];
+            s_sum[qwave][m] = isum;
         }
     }
 }
 
-// QW: the block has a quantization wave (gemv_quant_wave) before its NTHR
-// weight threads; the rows must fit it (at most 64 * gemv_qb<T>() chunks).
+// QWN = 1: the block has a quantization wave (gemv_quant_waves) before its
+// NTHR weight threads; the rows must fit it (at most 64 * gemv_qb<T>() chunks).
+// SPLITK: the block is one K piece of a group (GemvParams::ksplit).
 template <typename T, int MR, int BITS, int EPI, int RW, int NW, bool PREQ, int GPB = 1, int NTHR = 256,
-          bool GROUPED = false, bool QW = false>
-__global__ __launch_bounds__(NTHR + (QW ? 64 : 0)) void gemv_kernel(GemvParams P) {
-    extern __shared__ __attribute__((aligned(16))) int8_t sa[];  // [K_pad/16][MR][16]
+          bool GROUPED = false, int QWN = 0, bool SPLITK = false>
+__global__ __launch_bounds__(NTHR + 64 * QWN) void gemv_kernel(GemvParams P) {
+    extern __shared__ __attribute__((aligned(16))) int8_t sa[];  // [K_pad/16][MR][16] (the piece's K)
+    // Split K: this block's piece of the 64-k units, the row slice, and where
+    // its planes start in the tile.
+    int plane_off = 0, grp = blockIdx.x;
+    const int K_pad_full = P.K_pad;
+    if constexpr (SPLITK) {
+        static_assert(MR == 1 && GPB == 1 && EPI == EPI_PLAIN && !PREQ && !GROUPED && QWN == 0,
+                      "split K: one row, plain epilogue, in-block quantization");
+        const int piece = blockIdx.x % P.ksplit;
+        grp = blockIdx.x / P.ksplit;
+        const int U = P.K_pad >> 6;
+        const int u0 = U * piece / P.ksplit, u1 = U * (piece + 1) / P.ksplit;
+        plane_off = u0 * (BITS == 8 ? 4 : 2);
+        P.x = static_cast<const T*>(P.x) + 64 * u0;
+        P.K = max(0, min(P.K - 64 * u0, 64 * (u1 - u0)));
+        P.K_pad = 64 * (u1 - u0);
+        if (P.diag_codes) P.diag_codes += (size_t)4 * u0 * P.M_alloc * 16;
+    }
     if constexpr (GROUPED) {
         static_assert(MR == 1 && GPB == 1, "one slot row per block");
         const int s = blockIdx.y;
@@ -1308,21 +1370,23 @@ __global__ __launch_bounds__(NTHR + (QW ? 64 : 0)) void gemv_kernel(GemvParams P
         for (int w = 0; w < NWV; ++w) v += s_isum[w][m];
         return v;
     };
-    // (QW: hardware wave 0 is the quantization wave; the weight threads are
-    // numbered from the second wave on)
-    const int tid = (int)threadIdx.x - (QW ? 64 : 0), lane = threadIdx.x & 63, wave = tid >> 6;
+    // (QWN > 0: the first QWN hardware waves quantize; the weight threads are
+    // numbered from the next wave on)
+    constexpr bool QW = QWN > 0;
+    static_assert(QWN <= 1, "one quantization wave (more were slower)");
+    const int tid = (int)threadIdx.x - 64 * QWN, lane = threadIdx.x & 63, wave = tid >> 6;
     if constexpr (QW) {
-        static_assert(!PREQ, "the quantization wave quantizes the rows");
-        if (threadIdx.x < 64) {
-            // First wave of the block and the highest issue priority: its row
-            // loads and its quantization chain go ahead of the weight waves'
+        static_assert(!PREQ, "the quantization waves quantize the rows");
+        if (threadIdx.x < 64 * QWN) {
+            // First waves of the block and the highest issue priority: their
+            // row loads and quantization chain go ahead of the weight waves'
             // load issue (which stalls on the memory pipeline's back-pressure)
             // instead of queuing behind it (gate/up 2560x19456 W4 M=1: 8.7 us
-            // as the last wave at normal priority, 6.5 us first at priority 3).
+            // with the wave last at normal priority, 6.5 us first at priority 3).
             __builtin_amdgcn_s_setprio(3);
-            gemv_quant_wave<T, MR, BITS>(P, sa, s_red[0], s_isum[0], lane);
+            gemv_quant_waves<T, MR, QWN>(P, sa, s_red[0], s_isum, threadIdx.x);
             wait_lgkmcnt0();
-            __builtin_amdgcn_s_barrier();  // codes, scales and corrections are in LDS
+            __builtin_amdgcn_s_barrier();  // codes, scales and code sums are in LDS
             __builtin_amdgcn_s_barrier();  // (the weight waves' partial sums)
             return;
         }
@@ -1334,8 +1398,10 @@ __global__ __launch_bounds__(NTHR + (QW ? 64 : 0)) void gemv_kernel(GemvParams P
     const int CPG = CPT * TPB;               // chunks per group
     const int NWIN = (CPG + NTHR * RW - 1) / (NTHR * RW);
     const int chunks = KG16 * MR;            // activation chunks (<= NTHR * XMAX unless PREQ)
-    const int g0 = blockIdx.x * GPB;  // first group of the block
-    const int groups = gridDim.x * GPB;
+    const int g0 = grp * GPB;  // first group of the block
+    const int groups = SPLITK ? gridDim.x / P.ksplit : gridDim.x * GPB;
+    // (a tile's planes span the whole K even when the block takes a piece)
+    const int CPT_full = (BITS == 8 ? K_pad_full >> 4 : K_pad_full >> 5) * 8;
 
     // Tile group g: one 8-column tile, or (SwiGLU) a gate tile and its up
     // tile; the block's GPB groups are consecutive and their tiles form one
@@ -1353,7 +1419,7 @@ __global__ __launch_bounds__(NTHR + (QW ? 64 : 0)) void gemv_kernel(GemvParams P
         }
     }
 #pragma unroll
-    for (int t = 0; t < TPB; ++t) tb[t] = P.b + (size_t)tile[t] * CPT * 16;
+    for (int t = 0; t < TPB; ++t) tb[t] = P.b + ((size_t)tile[t] * CPT_full + (size_t)plane_off * 8) * 16;
     // Stream position q -> (tile t of the block, chunk within the tile).
     auto locate = [&](int q, int& t, int& r) {
         t = 0;
@@ -1456,12 +1522,19 @@ __global__ __launch_bounds__(NTHR + (QW ? 64 : 0)) void gemv_kernel(GemvParams P
         wait_lgkmcnt0();
         __builtin_amdgcn_s_barrier();
     } else if (QW) {
-        // 2-3. Codes, scales and corrections from the quantization wave.
+        // 2-3. Codes, scales and code sums from the quantization waves.
         __builtin_amdgcn_s_barrier();
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
             scale[m] = s_red[0][m];
-            corr[m] = s_isum[0][m];
+            int isum = 0;
+#pragma unroll
+            for (int w = 0; w < QWN; ++w) isum += s_isum[w][m];
+            corr[m] = BITS == 4 ? 8 * isum : 0;
+            if (blockIdx.x == 0 && P.diag_codes && tid == m && m < P.M) {
+                P.diag_scale[m] = scale[m];
+                P.diag_rowsum[m] = isum;
+            }
         }
     } else {
         // 2. Row maxima (from the activations or the precomputed partials),
@@ -1551,13 +1624,13 @@ __global__ __launch_bounds__(NTHR + (QW ? 64 : 0)) void gemv_kernel(GemvParams P
 #pragma unroll
         for (int m = 0; m < MR; ++m)
             corr[m] = (BITS == 4) ? 8 * block_isum(m) : 0;
-        if (blockIdx.x == 0 && P.diag_codes) {
+        if (grp == 0 && P.diag_codes) {
             for (int c = tid; c < chunks; c += NTHR)
                 *reinterpret_cast<v4u*>(P.diag_codes + ((size_t)(c / MR) * P.M_alloc + c % MR) * 16) =
                     *reinterpret_cast<const v4u*>(sa + c * 16);
             if (tid < MR && tid < P.M) {
                 P.diag_scale[tid] = scale[tid];
-                P.diag_rowsum[tid] = block_isum(tid);
+                if (!SPLITK) P.diag_rowsum[tid] = block_isum(tid);  // (split: summed over pieces below)
             }
         }
     }
@@ -1643,6 +1716,41 @@ __global__ __launch_bounds__(NTHR + (QW ? 64 : 0)) void gemv_kernel(GemvParams P
         }
     wait_lgkmcnt0();
     __builtin_amdgcn_s_barrier();
+    if constexpr (SPLITK) {
+        // One device-scope 64-bit add per column returns the slot as it was:
+        // the piece that finds ksplit - 1 pieces counted holds the whole sum
+        // (earlier adds are performed before it, being atomics on the same
+        // slot), writes the column and clears the slot for the next call.
+        if (wave == 0) {
+            constexpr unsigned long long ONE = 1ull << 40, BIAS = 1ull << 31, LOW = ONE - 1;
+            int tot = 0;
+#pragma unroll
+            for (int w = 0; w < NWV; ++w) tot += red[w][0][0][c8];
+            const unsigned long long mine = ONE + (unsigned long long)((long long)(tot - corr[0]) + (long long)BIAS);
+            unsigned long long* slot = P.kacc + 8 * tile[0] + c8;
+            const unsigned long long last = (unsigned long long)(P.ksplit - 1);
+            if (lane < 8) {
+                const unsigned long long was = __hip_atomic_fetch_add(slot, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if ((was >> 40) == last) {
+                    const long long total = (long long)((was + mine) & LOW) - (long long)(P.ksplit * BIAS);
+                    __hip_atomic_exchange(slot, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    const float y = ((float)(int)total * scale[0]) * cs[0];
+                    const int p = 8 * tile[0] + c8;
+                    if (P.M > 0 && p < P.N) store_out(P.c, P.c_type, orig_col(p, P.half), y);
+                }
+            }
+            if (lane == 0 && grp == 0 && P.diag_codes) {
+                const unsigned long long sm = ONE + (unsigned long long)((long long)block_isum(0) + (long long)BIAS);
+                unsigned long long* row_slot = P.kacc + P.N_pad;
+                const unsigned long long was = __hip_atomic_fetch_add(row_slot, sm, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if ((was >> 40) == last) {
+                    P.diag_rowsum[0] = (int)((long long)((was + sm) & LOW) - (long long)(P.ksplit * BIAS));
+                    __hip_atomic_exchange(row_slot, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+        }
+        return;
+    }
     if (wave == 0) {
 #pragma unroll
         for (int gp = 0; gp < GPB; ++gp) {

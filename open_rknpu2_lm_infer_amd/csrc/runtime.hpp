@@ -85,6 +85,7 @@ struct Workspace {
     float* partmax;   // [8][N_pad/8] per-block max|middle| of a GEMV SwiGLU
     int* split_part;        // split-K int32 partials [pieces][tiles][tile ints]
     size_t split_part_ints; // partial ints available
+    unsigned long long* kacc;  // split-K GEMV column slots [N_pad] + row code-sum slot, kept zero between calls
 };
 
 size_t workspace_bytes(const Geometry& g, int M);

@@ -98,6 +98,37 @@ def test_split_k_switch_is_bit_exact(ctx, splits, monkeypatch):
         assert np.array_equal(m.cpu().numpy(), oracle.linear_swiglu(codes, scales, x))
 
 
+@pytest.mark.parametrize("splits", [1, 2, 3, 4])
+def test_gemv_split_k_down_is_bit_exact(ctx, splits, monkeypatch):
+    """One-row FFN whose down GEMV (K = 2240: 35 units of 64, uneven pieces)
+    splits K (HM_GEMV_SPLITS forces the piece count): the pieces' int32 sums
+    meet through device-scope atomics and the last piece writes the tile and
+    clears the accumulators, so three calls in a row must each equal the
+    oracle; the down workspace's diagnostics hold the middle row's codes,
+    scale and code sum."""
+    from tests.test_gpu_linear import read_codes
+    monkeypatch.setenv("HM_GEMV_SPLITS", str(splits))
+    h, f = 256, 2240
+    for dbits in (4, 8):
+        gc, gs = R.weights(7, "dsk-g", 4, h, 2 * f)
+        dc, ds = R.weights(7, f"dsk-d{dbits}", dbits, f, h)
+        gu = ctx.weights(4, dev(gc), dev(gs))
+        dn = ctx.weights(dbits, dev(dc), dev(ds))
+        dws = ctx.workspace(dbits, 1, f, h)
+        for rep in range(3):
+            print(f"splits={splits} down W{dbits} call {rep}", flush=True)
+            x = R.activations(7, f"dsk-x{rep}", 1, h)
+            y = torch.empty(1, h, dtype=torch.float32, device="cuda")
+            D.ffn(ctx, gu, dn, dev(x), y, 1, dws=dws)
+            torch.cuda.synchronize()
+            want, mid = oracle.ffn(gc, gs, dc, ds, x, with_middle=True)
+            assert np.array_equal(y.cpu().numpy(), want)
+            codes, scale, sums = read_codes(dws, dbits, 1, f)
+            q, qs = oracle.quant_dense(mid)
+            assert np.array_equal(codes, q) and np.array_equal(scale, qs)
+            assert sums[0] == int(q.astype(np.int64).sum())
+
+
 @pytest.mark.parametrize("bits", [4, 8])
 def test_long_k_split_plan_matches_oracle(ctx, bits):
     """Few tiles over a long K: the plan splits K into pieces (partials, then a
