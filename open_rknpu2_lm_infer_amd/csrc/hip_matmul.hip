@@ -617,7 +617,7 @@ static void launch_gemv_w(const GemvParams& V, int groups, size_t lds, hipStream
     const int planes = BITS == 8 ? V.K_pad / 16 : V.K_pad / 32;
     const int chunks = planes * 8 * (EPI == EPI_PLAIN ? 1 : 2);
     const int rounds = (chunks + 255) / 256;
-    if constexpr (QWN == 1) {  // groups of 5 to 8 rounds
+    if constexpr (QWN == 1) {  // groups of 5 to 8 rounds (shorter ones, forced by HM_GEMV_QW, take 5)
         if (rounds <= 5)
             hipLaunchKernelGGL((gemv_kernel<T, MR, BITS, EPI, 5, 1, PREQ, 1, 256, false, 1>), dim3(groups), dim3(320),
                                lds, s, V);
@@ -761,8 +761,11 @@ int enqueue_linear(Workspace* ws, const Weights* w, const void* x, int x_type, l
         const int w_rounds = (w_chunks + 255) / 256;
         const int x_chunks = (g.K_pad / 16) * pv.mr;
         const int qb = x_type == DT_F32 ? gemv_qb<float>() : gemv_qb<__half>();
+        // HM_GEMV_QW: 0 never, 1 whenever the rows fit (tests, experiments).
+        const int qw_env = env_int("HM_GEMV_QW", -1);
+        const bool qw_fits = !preq && pv.mr <= 2 && x_chunks <= 64 * qb && w_rounds <= 8;
         int qwn = 0;
-        if (!preq && pv.mr <= 2 && x_chunks <= 64 * qb && w_rounds >= 5 && w_rounds <= 8) qwn = 1;
+        if (qw_fits && (qw_env == 1 || (qw_env < 0 && w_rounds >= 5))) qwn = 1;
         // One row with precomputed maxima (the down projection after the
         // SwiGLU GEMV) whose groups stream more than 8 rounds splits K so that
         // about 1280 blocks run (5 per CU) and each quantizes only its piece

@@ -279,7 +279,10 @@ __device__ __forceinline__ void scale16_raw(const v4u (&r)[4], float inv, float 
     asm volatile("v_mov_b32 %0, 0x80000000" : "=v"(nz));
 #pragma unroll
     for (int b = 0; b < 16; ++b) {
-        const h2 pair = __builtin_bit_cast(h2, r[b >> 3][(b >> 1) & 3]);
+        // (the word is copied out first: __builtin_bit_cast of a vector-element
+        // lvalue reads the vector's first word whatever the element index)
+        const unsigned word = r[b >> 3][(b >> 1) & 3];
+        const h2 pair = __builtin_bit_cast(h2, word);
         sv[b] = __builtin_fmaf((float)pair[b & 1], inv, nz);
     }
 }
@@ -1542,13 +1545,17 @@ __global__ __launch_bounds__(NTHR + 64 * QWN) void gemv_kernel(GemvParams P) {
         float mx[MR];
 #pragma unroll
         for (int m = 0; m < MR; ++m) mx[m] = 0.0f;
-        auto chunk_vals = [&](int j, float (&v)[16]) {
+        // words of a chunk the thread does not own (it read its own weight
+        // bytes) are zeroed once, before both passes
+#pragma unroll
+        for (int j = 0; j < XMAX; ++j) {
+            if (NTHR * j >= chunks) break;
             const int c = tid + NTHR * j, kg = c / MR, m = c % MR;
             const bool ok = c < chunks && m < P.M && kg * 16 < P.K;
-            cvt16_raw(xraw[j], v, T());
 #pragma unroll
-            for (int b = 0; b < 16; ++b) v[b] = ok ? v[b] : 0.0f;
-        };
+            for (int q = 0; q < (int)sizeof(T); ++q)  // (sizeof(T) 16-byte words per chunk)
+                xraw[j][q] = ok ? xraw[j][q] : v4u{0u, 0u, 0u, 0u};
+        }
         if (P.part_in) {
 #pragma unroll
             for (int m = 0; m < MR; ++m) {
@@ -1564,7 +1571,7 @@ __global__ __launch_bounds__(NTHR + 64 * QWN) void gemv_kernel(GemvParams P) {
             for (int j = 0; j < XMAX; ++j) {
                 if (tid + NTHR * j >= chunks) continue;  // (pure arithmetic: no load under the branch)
                 float v[16];
-                chunk_vals(j, v);
+                cvt16_raw(xraw[j], v, T());
                 float lm = 0.0f;
 #pragma unroll
                 for (int b = 0; b < 16; ++b) lm = fmaxf(lm, fabsf(v[b]));
@@ -1601,14 +1608,13 @@ __global__ __launch_bounds__(NTHR + 64 * QWN) void gemv_kernel(GemvParams P) {
         for (int j = 0; j < XMAX; ++j) {
             const int c = tid + NTHR * j, m = c % MR;
             if (c >= chunks) continue;
-            float v[16];
-            chunk_vals(j, v);
             float iv = inv[0];
 #pragma unroll
             for (int r = 1; r < MR; ++r) iv = (r == m) ? inv[r] : iv;
+            float sv[16];
+            scale16_raw(xraw[j], iv, sv, T());
             int sum = 0;
-            const v4u pk = (P.rule == QUANT_DENSE) ? quant_chunk<QUANT_DENSE>(v, iv, sum)
-                                                   : quant_chunk<QUANT_MOE>(v, iv, sum);
+            const v4u pk = (P.rule == QUANT_DENSE) ? quant_scaled<QUANT_DENSE>(sv, sum) : quant_scaled<QUANT_MOE>(sv, sum);
             const unsigned packed[4] = {pk[0], pk[1], pk[2], pk[3]};
 #pragma unroll
             for (int r = 0; r < MR; ++r) psum[r] += (r == m) ? sum : 0;

@@ -98,6 +98,41 @@ def test_split_k_switch_is_bit_exact(ctx, splits, monkeypatch):
         assert np.array_equal(m.cpu().numpy(), oracle.linear_swiglu(codes, scales, x))
 
 
+@pytest.mark.parametrize("qw", ["default", "0", "1"])
+def test_gemv_quantization_wave_matches_oracle(ctx, qw, monkeypatch):
+    """One-row GEMVs with K = 2560 (5 rounds of 256 weight chunks per tile
+    group: the shapes the block's dedicated quantization wave serves), fp16
+    and f32 rows, W4 and W8, plain and SwiGLU: equal to the oracle with the
+    wave (default rule or HM_GEMV_QW=1) and without it (HM_GEMV_QW=0); the
+    workspace diagnostics hold the row's codes, scale and code sum."""
+    from tests.test_gpu_linear import read_codes
+    if qw != "default":
+        monkeypatch.setenv("HM_GEMV_QW", qw)
+    k = 2560
+    for bits, n, swiglu in ((4, 1024, True), (8, 512, False), (4, 4096, False), (8, 1024, True)):
+        codes, scales = R.weights(9, f"dqw{bits}-{n}", bits, k, n)
+        w = ctx.weights(bits, dev(codes), dev(scales))
+        ws = ctx.workspace(bits, 1, k, n)
+        for rep, half in enumerate((False, True)):
+            print(f"qw={qw} W{bits} n={n} swiglu={swiglu} fp16={half}", flush=True)
+            x = R.activations(9, f"dqw-x{rep}", 1, k)
+            xin = dev(x).half() if half else dev(x)
+            if swiglu:
+                y = torch.empty(1, n // 2, dtype=torch.float32, device="cuda")
+                D.linear(ctx, w, xin, y, 1, swiglu=True, ws=ws)
+                want = oracle.linear_swiglu(codes, scales, x)
+            else:
+                y = torch.empty(1, n, dtype=torch.float32, device="cuda")
+                D.linear(ctx, w, xin, y, 1, ws=ws)
+                want = oracle.linear(codes, scales, x)
+            torch.cuda.synchronize()
+            assert np.array_equal(y.cpu().numpy(), want)
+            got, scale, sums = read_codes(ws, bits, 1, k)
+            q, qs = oracle.quant_dense(x)
+            assert np.array_equal(got, q) and np.array_equal(scale, qs)
+            assert sums[0] == int(q.astype(np.int64).sum())
+
+
 @pytest.mark.parametrize("splits", [1, 2, 3, 4])
 def test_gemv_split_k_down_is_bit_exact(ctx, splits, monkeypatch):
     """One-row FFN whose down GEMV (K = 2240: 35 units of 64, uneven pieces)
