@@ -98,6 +98,37 @@ def test_split_k_switch_is_bit_exact(ctx, splits, monkeypatch):
         assert np.array_equal(m.cpu().numpy(), oracle.linear_swiglu(codes, scales, x))
 
 
+@pytest.mark.parametrize("bits", [4, 8])
+def test_gemv_window_configurations_match_oracle(ctx, bits):
+    """One- and two-row GEMVs over K values that select every register-window
+    configuration of the GEMV launch (3/4/5/6/8 rounds of 256 weight chunks
+    per tile group, 512-thread blocks with one 5- or 6-round window, two
+    5-round windows, and 8-round windows that ping-pong; a row too long to be
+    quantized in the block goes through the quantization launch first), plain
+    and SwiGLU, fp16 rows: equal to the oracle."""
+    per_k = 2 if bits == 4 else 1  # weight chunks per 64 k per column: W4 4, W8 8 (x2 for SwiGLU)
+    ks = [1536, 2048, 2560, 3072, 4096, 5120, 6144, 10240, 16384, 24576]
+    for k in ks:
+        for swiglu in (False, True):
+            n = 256
+            codes, scales = R.weights(11, f"dwin{bits}-{k}-{swiglu}", bits, k, n)
+            w = ctx.weights(bits, dev(codes), dev(scales))
+            for rows in (1, 2):
+                print(f"W{bits} K={k} swiglu={swiglu} rows={rows} chunks={k // 64 * 4 * per_k * (2 if swiglu else 1)}",
+                      flush=True)
+                x = R.activations(11, f"dwin-x{k}-{rows}", rows, k)
+                if swiglu:
+                    y = torch.empty(rows, n // 2, dtype=torch.float32, device="cuda")
+                    D.linear(ctx, w, dev(x).half(), y, rows, swiglu=True)
+                    want = oracle.linear_swiglu(codes, scales, x)
+                else:
+                    y = torch.empty(rows, n, dtype=torch.float32, device="cuda")
+                    D.linear(ctx, w, dev(x).half(), y, rows)
+                    want = oracle.linear(codes, scales, x)
+                torch.cuda.synchronize()
+                assert np.array_equal(y.cpu().numpy(), want)
+
+
 @pytest.mark.parametrize("qw", ["default", "0", "1"])
 def test_gemv_quantization_wave_matches_oracle(ctx, qw, monkeypatch):
     """One-row GEMVs with K = 2560 (5 rounds of 256 weight chunks per tile
