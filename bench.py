@@ -154,9 +154,9 @@ def graph_time(torch, fn, reps, check=None):
 # two rocprofv3 counter runs of `bench.py --traffic-probe` (FETCH_SIZE, then
 # WRITE_SIZE, KiB per dispatch, median over 108 dispatches), each scaled by
 # what the same counter reads for a 268,435,456-byte device copy in the same
-# run: FETCH_SIZE 131,089.5 KiB (factor 2.0), WRITE_SIZE 262,144 KiB (factor 1.0).
+# run: FETCH_SIZE 131,090.2 KiB (factor 2.0), WRITE_SIZE 262,144 KiB (factor 1.0).
 # Summary and commands: profiles/traffic_gemv_gate_up_m1.txt.
-TRAFFIC_GEMV_GATE_UP_M1 = int(round((12416.5 * 2.0 + 81.0625 * 1.0) * 1024))
+TRAFFIC_GEMV_GATE_UP_M1 = int(round((12431.0 * 2.0 + 81.0625 * 1.0) * 1024))
 
 
 def roofline(achieved, bound, kernel, avg_us, work, launches, method, traffic=None):

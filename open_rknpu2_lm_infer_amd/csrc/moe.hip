@@ -322,7 +322,11 @@ static void launch_slot_gemv(const GemvParams& V, int slots, hipStream_t s) {
     const int rounds = (planes * 8 * (EPI == EPI_PLAIN ? 1 : 2) + 255) / 256;
     const dim3 grid(EPI == EPI_PLAIN ? V.N_pad / 8 : V.N_pad / 16, slots);
     const size_t lds = V.K_pad;
-    if (rounds <= 4)
+    if (rounds <= 2)
+        hipLaunchKernelGGL((gemv_kernel<T, 1, BITS, EPI, 2, 1, PREQ, 1, 256, true>), grid, dim3(256), lds, s, V);
+    else if (rounds <= 3)
+        hipLaunchKernelGGL((gemv_kernel<T, 1, BITS, EPI, 3, 1, PREQ, 1, 256, true>), grid, dim3(256), lds, s, V);
+    else if (rounds <= 4)
         hipLaunchKernelGGL((gemv_kernel<T, 1, BITS, EPI, 4, 1, PREQ, 1, 256, true>), grid, dim3(256), lds, s, V);
     else if (rounds <= 6)
         hipLaunchKernelGGL((gemv_kernel<T, 1, BITS, EPI, 6, 1, PREQ, 1, 256, true>), grid, dim3(256), lds, s, V);
