@@ -37,6 +37,9 @@ RK_NPU_HIP_PLAIN = 0
 RK_NPU_HIP_SWIGLU = 1
 RK_NPU_HIP_PACK_QUANTIZED = 0
 RK_NPU_HIP_INT_QUANTIZED = 1
+RK_NPU_ATTENTION_F16_CAUSAL = 0
+RK_NPU_ATTENTION_F16_NO_MASK = 1
+RK_NPU_ATTENTION_F16_STABLE_SOFTMAX = 1
 
 
 class rk_npu_domain_memory_stats(Structure):
@@ -155,6 +158,27 @@ class rk_npu_hip_checkpoint_part(Structure):
     _fields_ = [("data", c_void_p), ("scales", c_void_p), ("n", c_int32), ("format", c_int32)]
 
 
+class rk_npu_attention_f16_config(Structure):
+    _fields_ = [("query_heads", c_int32), ("kv_heads", c_int32), ("head_dim", c_int32), ("softmax_scale", c_float),
+                ("max_query_rows", c_int32), ("max_capacity", c_int32), ("initial_capacity", c_int32),
+                ("core_mask", c_uint32), ("kv_tile", c_int32), ("flags", c_uint32), ("mask_mode", c_int32)]
+
+
+class rk_npu_attention_f16_sizes(Structure):
+    _fields_ = [("key_bytes", c_uint64), ("value_bytes", c_uint64), ("tail_bytes", c_uint64),
+                ("workspace_bytes", c_uint64), ("active_core_mask", c_uint32)]
+
+
+class rk_npu_attention_f16_cache_info(Structure):
+    _fields_ = [("length", c_int32), ("capacity", c_int32), ("key_bytes", c_uint64), ("value_bytes", c_uint64),
+                ("tail_bytes", c_uint64)]
+
+
+class rk_npu_attention_f16_timings(Structure):
+    _fields_ = [("upload_us", c_double), ("device_us", c_double), ("download_us", c_double),
+                ("total_us", c_double)]
+
+
 P = POINTER
 i8p = P(c_int8)
 f32p = P(c_float)
@@ -258,6 +282,25 @@ SIGNATURES = {
     "rk_npu_hip_profile_begin": (c_int, [c_int]),
     "rk_npu_hip_profile_end": (c_int, []),
     "rk_npu_hip_profile_read": (c_int, [P(rk_npu_hip_kernel_stat), c_int, P(c_int)]),
+    "rk_npu_attention_f16_config_init": (None, [P(rk_npu_attention_f16_config)]),
+    "rk_npu_attention_f16_query": (c_int, [P(rk_npu_attention_f16_config), c_int32, c_int32, c_int32,
+                                           P(rk_npu_attention_f16_sizes)]),
+    "rk_npu_attention_f16_prepare": (c_int, [c_void_p, P(rk_npu_attention_f16_config), P(c_void_p)]),
+    "rk_npu_attention_f16_workspace_free": (None, [c_void_p]),
+    "rk_npu_attention_f16_cache_create": (c_int, [c_void_p, P(rk_npu_attention_f16_config), P(c_void_p)]),
+    "rk_npu_attention_f16_cache_free": (None, [c_void_p]),
+    "rk_npu_attention_f16_cache_reserve": (c_int, [c_void_p, c_void_p, c_int32]),
+    "rk_npu_attention_f16_cache_load": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int32]),
+    "rk_npu_attention_f16_cache_append": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int32]),
+    "rk_npu_attention_f16_cache_truncate": (c_int, [c_void_p, c_int32]),
+    "rk_npu_attention_f16_cache_get_info": (c_int, [c_void_p, P(rk_npu_attention_f16_cache_info)]),
+    "rk_npu_attention_f16_run": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_void_p,
+                                         P(rk_npu_attention_f16_timings), c_void_p]),
+    "rk_npu_attention_f16_run_half": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_void_p,
+                                              P(rk_npu_attention_f16_timings), c_void_p]),
+    "rk_npu_hip_attention_cache_append": (c_int, [c_void_p, c_void_p, c_void_p, c_int32, c_void_p]),
+    "rk_npu_hip_attention_run": (c_int, [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_void_p, c_int32,
+                                         c_void_p]),
 }
 
 RECLAIM_CALLBACK = ctypes.CFUNCTYPE(None, c_void_p)

@@ -1,0 +1,672 @@
+// FP16 grouped-query attention over a device KV cache: the rk_npu_attention_f16
+// C ABI (include/rk_npu_attention_f16.h) and its kernels.
+//
+// Layout in HBM: a cache holds K and V as [kv_heads][capacity][head_dim] fp16
+// (one contiguous head_dim row per key). A run takes Q as
+// [query_heads][rows][head_dim] fp16 and writes [query_heads][rows][head_dim]
+// f32 or fp16. Math is f32: q is scaled by softmax_scale on load, scores are
+// f32 dot products, the softmax is online (running max and sum, the
+// accumulators rescaled when the max grows), and the output is the
+// accumulated sum of p * v divided by the sum of p.
+//
+// Work split: block = (key split, tile of RT query rows, KV head). The query
+// rows of one KV head are its (query head of the group, query row) pairs, so
+// the group's heads share every K/V tile read. A block streams 64-key tiles
+// of K then V through LDS; a decode-sized call (few rows) spreads the keys
+// over many splits whose partial (max, sum, accumulators) a second launch
+// combines.
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstring>
+#include <new>
+
+#include "../../include/rk_npu_attention_f16.h"
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Wunused-function"  // (the header's other kernels)
+#include "kernels.hpp"
+#pragma clang diagnostic pop
+#include "runtime.hpp"
+
+namespace hm {
+
+constexpr uint32_t MAGIC_ATTN_CACHE = 0x43414841u;
+constexpr uint32_t MAGIC_ATTN_WORK = 0x57414841u;
+constexpr int ATTN_KT = 64;              // keys per tile
+// Blocks that write partials: at most 1024 (see plan_attention), RT <= 16 rows each.
+constexpr size_t ATTN_PARTIAL_ROWS = 1024 * 16;
+
+struct AttnParams {
+    const __half* q;  // [qh][m][D]
+    const __half* k;  // [kh][cap][D]
+    const __half* v;
+    void* out;        // [qh][m][D], f32 or fp16
+    int out_f16;
+    float* part;      // [kh][row_tiles*RT][splits][D + 2]: max, sum, accumulators
+    int qh, kh, m, cap, len, pos, causal;
+    float scale;
+    int splits, keys_per_split, row_tiles, key_end;
+    int rows_pad;     // row_tiles * RT: partial rows per KV head
+};
+
+// max / sum over the N consecutive lanes (N = 16 or 64) that share a query row
+template <int N>
+__device__ __forceinline__ float group_max(float v) {
+    v = fmaxf(v, dpp_move<DPP_QUAD_XOR1>(v));
+    v = fmaxf(v, dpp_move<DPP_QUAD_XOR2>(v));
+    v = fmaxf(v, dpp_move<DPP_ROW_HALF_MIRROR>(v));
+    v = fmaxf(v, dpp_move<DPP_ROW_MIRROR>(v));
+    if constexpr (N == 64) {
+        v = fmaxf(v, dpp_move<DPP_ROW_BCAST15, 0xa>(v));
+        v = fmaxf(v, dpp_move<DPP_ROW_BCAST31, 0xc>(v));
+        v = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+    }
+    return v;
+}
+template <int N>
+__device__ __forceinline__ float group_sum(float v) {
+    v = v + dpp_move<DPP_QUAD_XOR1>(v);
+    v = v + dpp_move<DPP_QUAD_XOR2>(v);
+    v = v + dpp_move<DPP_ROW_HALF_MIRROR>(v);
+    v = v + dpp_move<DPP_ROW_MIRROR>(v);
+    if constexpr (N == 64) {
+        v = v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), DPP_ROW_BCAST15,
+                                                                      0xa, 0xf, false));
+        v = v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), DPP_ROW_BCAST31,
+                                                                      0xc, 0xf, false));
+        v = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+    }
+    return v;
+}
+
+// Block: 256 threads; RT query rows (RT = 4: 64 threads per row, RT = 16: 16
+// threads per row). Thread (row, sub) scores keys sub + RPT*i of each tile
+// and owns output dims [sub*DPT, sub*DPT + DPT) of its row.
+template <int D, int RT>
+__global__ __launch_bounds__(256) void attn_split_kernel(AttnParams P) {
+    constexpr int KT = ATTN_KT;
+    constexpr int RPT = 256 / RT;  // threads per row
+    constexpr int SPT = KT / RPT;  // scores per thread per tile
+    constexpr int DPT = D / RPT;   // output dims per thread
+    constexpr int KP = D + 8;      // LDS row pitch of a K/V tile (halves)
+    static_assert(DPT >= 1 && D % RPT == 0 && D % 8 == 0, "head_dim must split over the row's threads");
+    __shared__ __attribute__((aligned(16))) float qs[RT][D];
+    __shared__ __attribute__((aligned(16))) __half ks[KT][KP];
+    __shared__ float ps[RT][KT];
+    const int split = blockIdx.x, rt = blockIdx.y, g = blockIdx.z;
+    const int G = P.qh / P.kh, R = G * P.m;
+    const int tid = threadIdx.x, row = tid / RPT, sub = tid % RPT;
+    const int rr = rt * RT + row;
+    const bool row_ok = rr < R;
+    const int gi = row_ok ? rr / P.m : 0, qr = row_ok ? rr % P.m : 0;
+    int klimit = P.len;  // keys [0, klimit) are visible to this row
+    if (P.causal) klimit = min(klimit, P.pos + qr + 1);
+    const int k0 = split * P.keys_per_split;
+    const int k1 = min(k0 + P.keys_per_split, P.key_end);
+    for (int i = tid; i < RT * D; i += 256) {
+        const int r = i / D, dd = i % D, row2 = rt * RT + r;
+        float val = 0.0f;
+        if (row2 < R) {
+            const int h2 = g * G + row2 / P.m, q2 = row2 % P.m;
+            val = __half2float(P.q[((size_t)h2 * P.m + q2) * D + dd]) * P.scale;
+        }
+        qs[r][dd] = val;
+    }
+    const __half* kbase = P.k + (size_t)g * P.cap * D;
+    const __half* vbase = P.v + (size_t)g * P.cap * D;
+    auto load_tile = [&](const __half* base, int kb) {
+        for (int i = tid; i < KT * (D / 8); i += 256) {
+            const int j = i / (D / 8), c = i % (D / 8), key = kb + j;
+            v4u val = v4u{0u, 0u, 0u, 0u};
+            if (key < k1) val = *reinterpret_cast<const v4u*>(base + (size_t)key * D + c * 8);
+            *reinterpret_cast<v4u*>(&ks[j][c * 8]) = val;
+        }
+    };
+    float mrun = -INFINITY, lrun = 0.0f;
+    float acc[DPT];
+#pragma unroll
+    for (int e = 0; e < DPT; ++e) acc[e] = 0.0f;
+    for (int kb = k0; kb < k1; kb += KT) {
+        __syncthreads();  // (previous tile's V reads done)
+        load_tile(kbase, kb);
+        __syncthreads();
+        float s[SPT];
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < SPT; ++i) {
+            const int j = sub + RPT * i;
+            float a = 0.0f;
+#pragma unroll 4
+            for (int c = 0; c < D; c += 8) {
+                const v4u kw = *reinterpret_cast<const v4u*>(&ks[j][c]);
+                const float4 q0 = *reinterpret_cast<const float4*>(&qs[row][c]);
+                const float4 q1 = *reinterpret_cast<const float4*>(&qs[row][c + 4]);
+                const float qv[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const unsigned w = kw[e >> 1];
+                    const float kf = __half2float(__ushort_as_half((unsigned short)((e & 1) ? (w >> 16) : (w & 0xffffu))));
+                    a = __builtin_fmaf(qv[e], kf, a);
+                }
+            }
+            const int key = kb + j;
+            s[i] = (row_ok && key < klimit && key < k1) ? a : -INFINITY;
+            tmax = fmaxf(tmax, s[i]);
+        }
+        tmax = group_max<RPT>(tmax);
+        const float mnew = fmaxf(mrun, tmax);
+        // (a row with no visible key yet keeps max -inf, sum 0, scale 1)
+        const float alpha = (mnew == -INFINITY) ? 1.0f : __expf(mrun - mnew);
+        float psum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < SPT; ++i) {
+            const float p = (s[i] == -INFINITY) ? 0.0f : __expf(s[i] - mnew);
+            ps[row][sub + RPT * i] = p;
+            psum += p;
+        }
+        psum = group_sum<RPT>(psum);
+        lrun = lrun * alpha + psum;
+        mrun = mnew;
+#pragma unroll
+        for (int e = 0; e < DPT; ++e) acc[e] *= alpha;
+        __syncthreads();  // (K reads done, p written)
+        load_tile(vbase, kb);
+        __syncthreads();
+#pragma unroll 4
+        for (int j = 0; j < KT; ++j) {
+            const float p = ps[row][j];
+#pragma unroll
+            for (int e = 0; e < DPT; ++e) acc[e] = __builtin_fmaf(p, __half2float(ks[j][sub * DPT + e]), acc[e]);
+        }
+    }
+    if (!row_ok) return;
+    const int h = g * G + gi;
+    if (P.splits == 1) {
+        const float inv = 1.0f / lrun;
+        const size_t o = ((size_t)h * P.m + qr) * D + sub * DPT;
+#pragma unroll
+        for (int e = 0; e < DPT; ++e) {
+            const float y = acc[e] * inv;
+            if (P.out_f16)
+                static_cast<__half*>(P.out)[o + e] = __float2half_rn(y);
+            else
+                static_cast<float*>(P.out)[o + e] = y;
+        }
+        return;
+    }
+    float* part = P.part + (((size_t)g * P.rows_pad + rr) * P.splits + split) * (D + 2);
+    if (sub == 0) {
+        part[0] = mrun;
+        part[1] = lrun;
+    }
+#pragma unroll
+    for (int e = 0; e < DPT; ++e) part[2 + sub * DPT + e] = acc[e];
+}
+
+// Combine the splits of one (KV head, row): block = one row, thread = dims.
+__global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams P, int D) {
+    const int rr = blockIdx.x, g = blockIdx.y;
+    const int G = P.qh / P.kh, R = G * P.m;
+    if (rr >= R) return;
+    const int h = g * G + rr / P.m, qr = rr % P.m;
+    const float* p0 = P.part + (((size_t)g * P.rows_pad + rr) * P.splits) * (D + 2);
+    float M = -INFINITY;
+    for (int s = 0; s < P.splits; ++s) M = fmaxf(M, p0[(size_t)s * (D + 2)]);
+    for (int dd = threadIdx.x; dd < D; dd += 256) {
+        float num = 0.0f, den = 0.0f;
+        for (int s = 0; s < P.splits; ++s) {
+            const float* ps = p0 + (size_t)s * (D + 2);
+            const float w = (ps[0] == -INFINITY) ? 0.0f : __expf(ps[0] - M);
+            num = __builtin_fmaf(w, ps[2 + dd], num);
+            den = __builtin_fmaf(w, ps[1], den);
+        }
+        const float y = num / den;
+        const size_t o = ((size_t)h * P.m + qr) * D + dd;
+        if (P.out_f16)
+            static_cast<__half*>(P.out)[o] = __float2half_rn(y);
+        else
+            static_cast<float*>(P.out)[o] = y;
+    }
+}
+
+
+// ---------------------------------------------------------------------------
+// Host side.
+// ---------------------------------------------------------------------------
+struct AttnCache {
+    uint32_t magic;
+    Domain* domain;
+    rk_npu_attention_f16_config cfg;
+    __half* k;
+    __half* v;
+    int length, capacity;
+    size_t bytes_each;  // of k and of v
+};
+
+struct AttnWork {
+    uint32_t magic;
+    Domain* domain;
+    rk_npu_attention_f16_config cfg;
+    __half* q;     // host-call staging [qh][max_query_rows][D]
+    float* out;    // host-call staging (f32; fp16 output uses the first half)
+    float* part;   // split partials
+    size_t q_bytes, out_bytes, part_bytes;
+    hipStream_t stream;
+    std::atomic<bool> busy;
+};
+
+// The reference's checks (src/npu.rs:714-728) plus this library's limits.
+static bool valid_config(const rk_npu_attention_f16_config* c) {
+    if (!c) return false;
+    const int d = c->head_dim;
+    return c->kv_heads >= 1 && c->kv_heads <= 32 && c->query_heads >= c->kv_heads &&
+           c->query_heads % c->kv_heads == 0 && c->query_heads <= 256 && d > 0 && d % 32 == 0 && d <= 256 &&
+           std::isfinite(c->softmax_scale) && c->softmax_scale > 0.0f && c->max_query_rows >= 1 &&
+           c->max_query_rows <= 256 && c->max_capacity >= 1 && c->initial_capacity >= 0 &&
+           c->initial_capacity <= c->max_capacity &&
+           (c->mask_mode == RK_NPU_ATTENTION_F16_CAUSAL || c->mask_mode == RK_NPU_ATTENTION_F16_NO_MASK);
+}
+
+// Head dims with a kernel instantiation.
+static bool supported_dim(int d) { return d == 64 || d == 128 || d == 256; }
+
+static size_t kv_bytes(const rk_npu_attention_f16_config* c, int capacity) {
+    return (size_t)c->kv_heads * (size_t)capacity * c->head_dim * sizeof(__half);
+}
+
+static size_t part_bytes(const rk_npu_attention_f16_config* c) {
+    return ATTN_PARTIAL_ROWS * (size_t)(c->head_dim + 2) * sizeof(float);
+}
+
+static AttnCache* as_cache(void* p) {
+    AttnCache* c = static_cast<AttnCache*>(p);
+    return (c && c->magic == MAGIC_ATTN_CACHE) ? c : nullptr;
+}
+static AttnWork* as_attn_work(void* p) {
+    AttnWork* w = static_cast<AttnWork*>(p);
+    return (w && w->magic == MAGIC_ATTN_WORK) ? w : nullptr;
+}
+
+// Grow to `capacity` rows (multiple of 32), keeping the rows held.
+static int cache_grow(AttnCache* c, int capacity) {
+    capacity = round_up(capacity, 32);
+    if (capacity <= c->capacity) return RK_NPU_OK;
+    if (capacity > round_up(c->cfg.max_capacity, 32)) return RK_NPU_ERR_PARAM;
+    const size_t nb = kv_bytes(&c->cfg, capacity);
+    __half* nk = static_cast<__half*>(domain_alloc(c->domain, nb));
+    __half* nv = nk ? static_cast<__half*>(domain_alloc(c->domain, nb)) : nullptr;
+    if (!nk || !nv) {
+        domain_free(c->domain, nk, nb);
+        return RK_NPU_ERR_NOMEM;
+    }
+    const size_t row = (size_t)c->cfg.head_dim * sizeof(__half);
+    bool ok = true;
+    if (c->length > 0) {
+        ok = hipMemcpy2D(nk, capacity * row, c->k, (size_t)c->capacity * row, (size_t)c->length * row,
+                         c->cfg.kv_heads, hipMemcpyDeviceToDevice) == hipSuccess &&
+             hipMemcpy2D(nv, capacity * row, c->v, (size_t)c->capacity * row, (size_t)c->length * row,
+                         c->cfg.kv_heads, hipMemcpyDeviceToDevice) == hipSuccess;
+    }
+    if (!ok) {
+        domain_free(c->domain, nk, nb);
+        domain_free(c->domain, nv, nb);
+        return RK_NPU_ERR_DEVICE;
+    }
+    domain_free(c->domain, c->k, c->bytes_each);
+    domain_free(c->domain, c->v, c->bytes_each);
+    c->k = nk;
+    c->v = nv;
+    c->capacity = capacity;
+    c->bytes_each = nb;
+    return RK_NPU_OK;
+}
+
+// Copy `rows` rows per KV head ([kv_heads][rows][D]) after the rows held.
+static int cache_put(AttnCache* c, const void* k, const void* v, int rows, hipMemcpyKind kind, hipStream_t s,
+                     bool async) {
+    const size_t row = (size_t)c->cfg.head_dim * sizeof(__half);
+    const size_t dpitch = (size_t)c->capacity * row, spitch = (size_t)rows * row;
+    __half* dk = c->k + (size_t)c->length * c->cfg.head_dim;
+    __half* dv = c->v + (size_t)c->length * c->cfg.head_dim;
+    hipError_t e1, e2;
+    if (async) {
+        e1 = hipMemcpy2DAsync(dk, dpitch, k, spitch, spitch, c->cfg.kv_heads, kind, s);
+        e2 = hipMemcpy2DAsync(dv, dpitch, v, spitch, spitch, c->cfg.kv_heads, kind, s);
+    } else {
+        e1 = hipMemcpy2D(dk, dpitch, k, spitch, spitch, c->cfg.kv_heads, kind);
+        e2 = hipMemcpy2D(dv, dpitch, v, spitch, spitch, c->cfg.kv_heads, kind);
+    }
+    if (e1 != hipSuccess || e2 != hipSuccess) return RK_NPU_ERR_DEVICE;
+    c->length += rows;
+    return RK_NPU_OK;
+}
+
+struct AttnPlan {
+    int rt, row_tiles, splits, keys_per_split, key_end;
+};
+
+// Rows per tile: 4 when a KV head has at most 4 query rows (decode: one row
+// of a 4-head group), else 16. Keys: enough splits that about 512 blocks run
+// (each split a whole number of 64-key tiles); with more than one split the
+// blocks write partials, at most 512 + row_tiles * kv_heads <= 1024 of them.
+static AttnPlan plan_attention(const rk_npu_attention_f16_config& c, int rows, int len, int pos) {
+    AttnPlan p;
+    const int G = c.query_heads / c.kv_heads, R = G * rows;
+    p.rt = R <= 4 ? 4 : 16;
+    p.row_tiles = (R + p.rt - 1) / p.rt;
+    p.key_end = (c.mask_mode == RK_NPU_ATTENTION_F16_CAUSAL) ? std::min(len, pos + rows) : len;
+    const int tiles = (p.key_end + ATTN_KT - 1) / ATTN_KT;
+    const int base = p.row_tiles * c.kv_heads;
+    int want = base >= 512 ? 1 : (512 + base - 1) / base;
+    want = std::max(1, std::min(want, tiles));
+    const int tiles_per_split = (tiles + want - 1) / want;
+    p.keys_per_split = tiles_per_split * ATTN_KT;
+    p.splits = (p.key_end + p.keys_per_split - 1) / p.keys_per_split;
+    if (p.splits < 1) p.splits = 1;
+    return p;
+}
+
+template <int D, int RT>
+static void launch_attn(const AttnParams& P, const AttnPlan& pl, int kh, hipStream_t s) {
+    hipLaunchKernelGGL((attn_split_kernel<D, RT>), dim3(pl.splits, pl.row_tiles, kh), dim3(256), 0, s, P);
+}
+
+static int enqueue_attention(AttnWork* w, AttnCache* c, const __half* q, int rows, int pos, void* out, int out_f16,
+                             hipStream_t s) {
+    const rk_npu_attention_f16_config& cfg = c->cfg;
+    const bool causal = cfg.mask_mode == RK_NPU_ATTENTION_F16_CAUSAL;
+    if (rows < 1 || rows > w->cfg.max_query_rows || pos < 0 || c->length < 1) return RK_NPU_ERR_PARAM;
+    if (causal && (long)pos + rows > c->length) return RK_NPU_ERR_PARAM;
+    const AttnPlan pl = plan_attention(cfg, rows, c->length, pos);
+    if (pl.splits > 1 && (size_t)pl.row_tiles * pl.rt * cfg.kv_heads * pl.splits > ATTN_PARTIAL_ROWS)
+        return RK_NPU_ERR_UNSUPPORTED;
+    AttnParams P;
+    P.q = q;
+    P.k = c->k;
+    P.v = c->v;
+    P.out = out;
+    P.out_f16 = out_f16;
+    P.part = w->part;
+    P.qh = cfg.query_heads;
+    P.kh = cfg.kv_heads;
+    P.m = rows;
+    P.cap = c->capacity;
+    P.len = c->length;
+    P.pos = pos;
+    P.causal = causal ? 1 : 0;
+    P.scale = cfg.softmax_scale;
+    P.splits = pl.splits;
+    P.keys_per_split = pl.keys_per_split;
+    P.row_tiles = pl.row_tiles;
+    P.key_end = pl.key_end;
+    P.rows_pad = pl.row_tiles * pl.rt;
+    const int D = cfg.head_dim;
+#define HM_ATTN(DD)                                                    \
+    if (pl.rt == 4)                                                    \
+        launch_attn<DD, 4>(P, pl, cfg.kv_heads, s);                    \
+    else                                                               \
+        launch_attn<DD, 16>(P, pl, cfg.kv_heads, s);
+    if (D == 64) {
+        HM_ATTN(64)
+    } else if (D == 128) {
+        HM_ATTN(128)
+    } else {
+        HM_ATTN(256)
+    }
+#undef HM_ATTN
+    if (pl.splits > 1) {
+        const int G = cfg.query_heads / cfg.kv_heads;
+        hipLaunchKernelGGL(attn_combine_kernel, dim3(G * rows, cfg.kv_heads), dim3(std::min(256, D)), 0, s, P, D);
+    }
+    return hipGetLastError() == hipSuccess ? RK_NPU_OK : RK_NPU_ERR_DEVICE;
+}
+
+static int run_host(rk_npu_attention_f16_workspace* workspace, rk_npu_attention_f16_cache* cache, const uint16_t* q,
+                    int rows, int pos, void* out, int out_f16, rk_npu_attention_f16_timings* t, const void* reserved) {
+    AttnWork* w = as_attn_work(workspace);
+    AttnCache* c = as_cache(cache);
+    if (!w || !c || !q || !out || reserved) return RK_NPU_ERR_PARAM;
+    if (w->cfg.query_heads != c->cfg.query_heads || w->cfg.kv_heads != c->cfg.kv_heads ||
+        w->cfg.head_dim != c->cfg.head_dim || w->cfg.mask_mode != c->cfg.mask_mode ||
+        w->cfg.softmax_scale != c->cfg.softmax_scale)
+        return RK_NPU_ERR_PARAM;
+    if (rows < 1 || rows > w->cfg.max_query_rows) return RK_NPU_ERR_PARAM;
+    bool expected = false;
+    if (!w->busy.compare_exchange_strong(expected, true)) return RK_NPU_ERR_BUSY;
+    const double t0 = now_us();
+    const size_t n = (size_t)c->cfg.query_heads * rows * c->cfg.head_dim;
+    int rc = RK_NPU_OK;
+    if (hipSetDevice(device_of(w->domain)) != hipSuccess ||
+        hipMemcpyAsync(w->q, q, n * sizeof(__half), hipMemcpyHostToDevice, w->stream) != hipSuccess ||
+        hipStreamSynchronize(w->stream) != hipSuccess)
+        rc = RK_NPU_ERR_DEVICE;
+    const double t1 = now_us();
+    if (rc == RK_NPU_OK) rc = enqueue_attention(w, c, w->q, rows, pos, w->out, out_f16, w->stream);
+    if (rc == RK_NPU_OK && hipStreamSynchronize(w->stream) != hipSuccess) rc = RK_NPU_ERR_DEVICE;
+    const double t2 = now_us();
+    if (rc == RK_NPU_OK &&
+        hipMemcpy(out, w->out, n * (out_f16 ? sizeof(__half) : sizeof(float)), hipMemcpyDeviceToHost) != hipSuccess)
+        rc = RK_NPU_ERR_DEVICE;
+    const double t3 = now_us();
+    if (t) {
+        t->upload_us = t1 - t0;
+        t->device_us = t2 - t1;
+        t->download_us = t3 - t2;
+        t->total_us = t3 - t0;
+    }
+    w->busy.store(false);
+    return rc;
+}
+
+}  // namespace hm
+
+using namespace hm;
+
+extern "C" {
+
+void rk_npu_attention_f16_config_init(rk_npu_attention_f16_config* c) {
+    if (!c) return;
+    std::memset(c, 0, sizeof(*c));
+    c->query_heads = 32;
+    c->kv_heads = 8;
+    c->head_dim = 128;
+    c->softmax_scale = 1.0f / std::sqrt(128.0f);
+    c->max_query_rows = 128;
+    c->max_capacity = 4096;
+    c->initial_capacity = 128;
+    c->kv_tile = 512;
+    c->flags = RK_NPU_ATTENTION_F16_STABLE_SOFTMAX;
+    c->mask_mode = RK_NPU_ATTENTION_F16_CAUSAL;
+}
+
+int rk_npu_attention_f16_query(const rk_npu_attention_f16_config* c, int32_t capacity, int32_t query_rows,
+                               int32_t kv_capacity, rk_npu_attention_f16_sizes* sizes) {
+    if (!valid_config(c) || !sizes || capacity < 0 || query_rows < 1 || query_rows > 256 || kv_capacity < 0)
+        return RK_NPU_ERR_PARAM;
+    const int cap = round_up(capacity, 32);
+    sizes->key_bytes = kv_bytes(c, cap);
+    sizes->value_bytes = kv_bytes(c, cap);
+    sizes->tail_bytes = 0;
+    sizes->workspace_bytes = (uint64_t)c->query_heads * query_rows * c->head_dim * (sizeof(__half) + sizeof(float)) +
+                             part_bytes(c);
+    sizes->active_core_mask = 1u;
+    return RK_NPU_OK;
+}
+
+int rk_npu_attention_f16_prepare(rk_npu_iommu_domain* domain, const rk_npu_attention_f16_config* config,
+                                 rk_npu_attention_f16_workspace** out) {
+    if (out) *out = nullptr;
+    Domain* d = static_cast<Domain*>(domain);
+    if (!d || !out || !valid_config(config)) return RK_NPU_ERR_PARAM;
+    if (!supported_dim(config->head_dim)) return RK_NPU_ERR_UNSUPPORTED;
+    if (hipSetDevice(device_of(d)) != hipSuccess) return RK_NPU_ERR_DEVICE;
+    AttnWork* w = new (std::nothrow) AttnWork();
+    if (!w) return RK_NPU_ERR_NOMEM;
+    w->magic = MAGIC_ATTN_WORK;
+    w->domain = d;
+    w->cfg = *config;
+    w->busy.store(false);
+    w->stream = nullptr;
+    const size_t n = (size_t)config->query_heads * config->max_query_rows * config->head_dim;
+    w->q_bytes = n * sizeof(__half);
+    w->out_bytes = n * sizeof(float);
+    w->part_bytes = part_bytes(config);
+    w->q = static_cast<__half*>(domain_alloc(d, w->q_bytes));
+    w->out = static_cast<float*>(domain_alloc(d, w->out_bytes));
+    w->part = static_cast<float*>(domain_alloc(d, w->part_bytes));
+    if (!w->q || !w->out || !w->part || hipStreamCreateWithFlags(&w->stream, hipStreamNonBlocking) != hipSuccess) {
+        rk_npu_attention_f16_workspace_free(reinterpret_cast<rk_npu_attention_f16_workspace*>(w));
+        return RK_NPU_ERR_NOMEM;
+    }
+    *out = reinterpret_cast<rk_npu_attention_f16_workspace*>(w);
+    return RK_NPU_OK;
+}
+
+void rk_npu_attention_f16_workspace_free(rk_npu_attention_f16_workspace* workspace) {
+    AttnWork* w = as_attn_work(workspace);
+    if (!w) return;
+    (void)hipSetDevice(device_of(w->domain));
+    if (w->stream) {
+        (void)hipStreamSynchronize(w->stream);
+        (void)hipStreamDestroy(w->stream);
+    }
+    domain_free(w->domain, w->q, w->q_bytes);
+    domain_free(w->domain, w->out, w->out_bytes);
+    domain_free(w->domain, w->part, w->part_bytes);
+    w->magic = 0;
+    delete w;
+}
+
+int rk_npu_attention_f16_cache_create(rk_npu_iommu_domain* domain, const rk_npu_attention_f16_config* config,
+                                      rk_npu_attention_f16_cache** out) {
+    if (out) *out = nullptr;
+    Domain* d = static_cast<Domain*>(domain);
+    if (!d || !out || !valid_config(config)) return RK_NPU_ERR_PARAM;
+    if (!supported_dim(config->head_dim)) return RK_NPU_ERR_UNSUPPORTED;
+    if (hipSetDevice(device_of(d)) != hipSuccess) return RK_NPU_ERR_DEVICE;
+    AttnCache* c = new (std::nothrow) AttnCache();
+    if (!c) return RK_NPU_ERR_NOMEM;
+    c->magic = MAGIC_ATTN_CACHE;
+    c->domain = d;
+    c->cfg = *config;
+    c->length = 0;
+    c->capacity = std::max(32, round_up(config->initial_capacity, 32));
+    c->bytes_each = kv_bytes(config, c->capacity);
+    c->k = static_cast<__half*>(domain_alloc(d, c->bytes_each));
+    c->v = c->k ? static_cast<__half*>(domain_alloc(d, c->bytes_each)) : nullptr;
+    if (!c->k || !c->v) {
+        rk_npu_attention_f16_cache_free(reinterpret_cast<rk_npu_attention_f16_cache*>(c));
+        return RK_NPU_ERR_NOMEM;
+    }
+    *out = reinterpret_cast<rk_npu_attention_f16_cache*>(c);
+    return RK_NPU_OK;
+}
+
+void rk_npu_attention_f16_cache_free(rk_npu_attention_f16_cache* cache) {
+    AttnCache* c = as_cache(cache);
+    if (!c) return;
+    (void)hipSetDevice(device_of(c->domain));
+    (void)hipDeviceSynchronize();
+    domain_free(c->domain, c->k, c->bytes_each);
+    domain_free(c->domain, c->v, c->bytes_each);
+    c->magic = 0;
+    delete c;
+}
+
+int rk_npu_attention_f16_cache_reserve(rk_npu_ctx* ctx, rk_npu_attention_f16_cache* cache, int32_t capacity) {
+    AttnCache* c = as_cache(cache);
+    if (!ctx || !c || capacity < 0) return RK_NPU_ERR_PARAM;
+    if (hipSetDevice(device_of(c->domain)) != hipSuccess || hipDeviceSynchronize() != hipSuccess)
+        return RK_NPU_ERR_DEVICE;
+    return cache_grow(c, capacity);
+}
+
+int rk_npu_attention_f16_cache_load(rk_npu_ctx* ctx, rk_npu_attention_f16_cache* cache, const uint16_t* k,
+                                    const uint16_t* v, int32_t rows) {
+    AttnCache* c = as_cache(cache);
+    if (!ctx || !c || rows < 0 || (rows > 0 && (!k || !v))) return RK_NPU_ERR_PARAM;
+    if (hipSetDevice(device_of(c->domain)) != hipSuccess || hipDeviceSynchronize() != hipSuccess)
+        return RK_NPU_ERR_DEVICE;
+    c->length = 0;
+    if (rows == 0) return RK_NPU_OK;
+    int rc = cache_grow(c, rows);
+    if (rc != RK_NPU_OK) return rc;
+    return cache_put(c, k, v, rows, hipMemcpyHostToDevice, nullptr, false);
+}
+
+int rk_npu_attention_f16_cache_append(rk_npu_ctx* ctx, rk_npu_attention_f16_cache* cache, const uint16_t* k,
+                                      const uint16_t* v, int32_t rows) {
+    AttnCache* c = as_cache(cache);
+    if (!ctx || !c || rows < 1 || !k || !v) return RK_NPU_ERR_PARAM;
+    if ((long)c->length + rows > round_up(c->cfg.max_capacity, 32)) return RK_NPU_ERR_PARAM;
+    if (hipSetDevice(device_of(c->domain)) != hipSuccess || hipDeviceSynchronize() != hipSuccess)
+        return RK_NPU_ERR_DEVICE;
+    if (c->length + rows > c->capacity) {
+        const int grown = std::min(round_up(c->cfg.max_capacity, 32), std::max(c->length + rows, 2 * c->capacity));
+        int rc = cache_grow(c, grown);
+        if (rc != RK_NPU_OK) return rc;
+    }
+    return cache_put(c, k, v, rows, hipMemcpyHostToDevice, nullptr, false);
+}
+
+int rk_npu_attention_f16_cache_truncate(rk_npu_attention_f16_cache* cache, int32_t length) {
+    AttnCache* c = as_cache(cache);
+    if (!c || length < 0 || length > c->length) return RK_NPU_ERR_PARAM;
+    c->length = length;
+    return RK_NPU_OK;
+}
+
+int rk_npu_attention_f16_cache_get_info(const rk_npu_attention_f16_cache* cache,
+                                        rk_npu_attention_f16_cache_info* info) {
+    AttnCache* c = as_cache(const_cast<rk_npu_attention_f16_cache*>(cache));
+    if (!c || !info) return RK_NPU_ERR_PARAM;
+    info->length = c->length;
+    info->capacity = c->capacity;
+    info->key_bytes = c->bytes_each;
+    info->value_bytes = c->bytes_each;
+    info->tail_bytes = 0;
+    return RK_NPU_OK;
+}
+
+int rk_npu_attention_f16_run(rk_npu_ctx* ctx, rk_npu_attention_f16_workspace* workspace,
+                             rk_npu_attention_f16_cache* cache, const uint16_t* q, int32_t rows, int32_t position,
+                             float* output, rk_npu_attention_f16_timings* timings, const void* reserved) {
+    if (!ctx) return RK_NPU_ERR_PARAM;
+    return run_host(workspace, cache, q, rows, position, output, 0, timings, reserved);
+}
+
+int rk_npu_attention_f16_run_half(rk_npu_ctx* ctx, rk_npu_attention_f16_workspace* workspace,
+                                  rk_npu_attention_f16_cache* cache, const uint16_t* q, int32_t rows,
+                                  int32_t position, uint16_t* output, rk_npu_attention_f16_timings* timings,
+                                  const void* reserved) {
+    if (!ctx) return RK_NPU_ERR_PARAM;
+    return run_host(workspace, cache, q, rows, position, output, 1, timings, reserved);
+}
+
+int rk_npu_hip_attention_cache_append(rk_npu_attention_f16_cache* cache, const void* k_dev, const void* v_dev,
+                                      int32_t rows, void* stream) {
+    AttnCache* c = as_cache(cache);
+    if (!c || rows < 1 || !k_dev || !v_dev) return RK_NPU_ERR_PARAM;
+    if ((long)c->length + rows > c->capacity) return RK_NPU_ERR_PARAM;  // (reserve first: no allocation here)
+    if (hipSetDevice(device_of(c->domain)) != hipSuccess) return RK_NPU_ERR_DEVICE;
+    return cache_put(c, k_dev, v_dev, rows, hipMemcpyDeviceToDevice, static_cast<hipStream_t>(stream), true);
+}
+
+int rk_npu_hip_attention_run(rk_npu_attention_f16_workspace* workspace, rk_npu_attention_f16_cache* cache,
+                             const void* q_dev, int32_t rows, int32_t position, void* out_dev, int32_t out_f16,
+                             void* stream) {
+    AttnWork* w = as_attn_work(workspace);
+    AttnCache* c = as_cache(cache);
+    if (!w || !c || !q_dev || !out_dev) return RK_NPU_ERR_PARAM;
+    if (w->cfg.query_heads != c->cfg.query_heads || w->cfg.kv_heads != c->cfg.kv_heads ||
+        w->cfg.head_dim != c->cfg.head_dim || w->cfg.mask_mode != c->cfg.mask_mode ||
+        w->cfg.softmax_scale != c->cfg.softmax_scale)
+        return RK_NPU_ERR_PARAM;
+    if (hipSetDevice(device_of(w->domain)) != hipSuccess) return RK_NPU_ERR_DEVICE;
+    return enqueue_attention(w, c, static_cast<const __half*>(q_dev), rows, position, out_dev, out_f16 ? 1 : 0,
+                             static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

@@ -69,6 +69,8 @@ class ModelOptions:
     tune: bool = False
     tune_search: bool = False
     compress_w8a8: bool = False
+    context: int = 4096        # KV rows an attention cache may hold
+    attention_tile: int = 512  # accepted and ignored (the kernel tiles by itself)
 
 
 def _ptr(a: np.ndarray, t):
@@ -159,6 +161,27 @@ class Backend:
         self.padding_in = np.zeros(0, np.float32)
         self.padding_out = np.zeros(0, np.float32)
         self.keys = set()
+        self._attention = None  # the shared attention workspace (src/npu.rs:330, 729-742)
+
+    # -- attention (src/npu.rs:442-466, 662-760; src/npu/attention.rs) ---------
+    def attention(self, query_heads: int, kv_heads: int, dimension: int, softmax_scale: float):
+        """A causal GQA KV cache on this backend."""
+        from . import attention as A
+        return A.attention_masked(self, query_heads, kv_heads, dimension, softmax_scale, False)
+
+    def noncausal_gqa(self, query_heads: int, kv_heads: int, dimension: int):
+        """Bidirectional GQA (src/npu.rs:694-705)."""
+        from . import attention as A
+        return A.attention_masked(self, query_heads, kv_heads, dimension, 1.0 / math.sqrt(dimension), True)
+
+    def full_attention(self, heads: int, dimension: int, rows: int):
+        from . import attention as A
+        return A.full_attention(self, heads, dimension, rows)
+
+    @staticmethod
+    def attention_cache_bytes(options, query_heads: int, kv_heads: int, dimension: int, softmax_scale: float) -> int:
+        from . import attention as A
+        return A.attention_cache_bytes(options, query_heads, kv_heads, dimension, softmax_scale)
 
     @property
     def domain(self):

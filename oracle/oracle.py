@@ -236,3 +236,34 @@ def concatenate(mats) -> np.ndarray:
     nsa = (ctypes.c_int * len(mats))(*ns)
     lib().orc_concatenate(arr, nsa, len(mats), k, _p(out, _i8p))
     return out
+
+
+def attention(q, k, v, scale: float, position: int, causal: bool) -> np.ndarray:
+    """Grouped-query attention over a KV cache, in float64 (numpy; no C
+    counterpart). Layouts of src/npu/attention.rs:240-262, 325-351: q
+    [query_heads][rows][head_dim], k and v [kv_heads][length][head_dim]
+    (fp16 values), query head h reads KV head h // (query_heads // kv_heads);
+    row r sits at absolute position ``position + r`` and, with the causal mask,
+    sees keys j <= position + r; the softmax subtracts the row max (the
+    STABLE_SOFTMAX flag of src/npu.rs:437) and the scores are
+    ``scale * (q . k)``. Parity unpinned against the reference: its attention
+    is a closed native library (only the call sites are in the repository);
+    tests pin this restatement by brute force on tiny inputs and by the
+    softmax invariants instead."""
+    q = np.asarray(q, np.float64)
+    k = np.asarray(k, np.float64)
+    v = np.asarray(v, np.float64)
+    qh, rows, d = q.shape
+    kh, length, _ = k.shape
+    group = qh // kh
+    out = np.empty((qh, rows, d), np.float64)
+    for h in range(qh):
+        kk, vv = k[h // group], v[h // group]
+        s = scale * (q[h] @ kk.T)  # [rows][length]
+        if causal:
+            limit = position + np.arange(rows)[:, None]
+            s = np.where(np.arange(length)[None, :] <= limit, s, -np.inf)
+        s = s - s.max(axis=1, keepdims=True)
+        p = np.exp(s)
+        out[h] = (p @ vv) / p.sum(axis=1, keepdims=True)
+    return out
