@@ -471,6 +471,76 @@ def run_moe(torch, ctx, steps, warmup, tokens_list=(512, 1)):
     return results
 
 
+def run_attention(torch, ctx, steps, layers=36, length=4096):
+    """FP16 GQA attention (Qwen3-4B geometry: 32 query heads over 8 KV heads,
+    head_dim 128) over per-layer KV caches of `length` rows, through the
+    device entry points: a decode step (one query row per layer at the last
+    position: every cached row read) in GB/s of K/V bytes, and a prefill block
+    (128 query rows per layer ending at the last position, causal) in TFLOP/s
+    of the QK and PV products. One cache per layer, so the K/V reads of a step
+    (36 x 16.8 MB) come from HBM, not from the 256 MB last-level cache."""
+    import ctypes
+    from open_rknpu2_lm_infer_amd import _ffi as F
+    L = F.lib()
+    qh, kh, d = 32, 8, 128
+    cfg = F.rk_npu_attention_f16_config()
+    L.rk_npu_attention_f16_config_init(ctypes.byref(cfg))
+    cfg.query_heads, cfg.kv_heads, cfg.head_dim = qh, kh, d
+    cfg.softmax_scale = d ** -0.5
+    cfg.max_query_rows, cfg.max_capacity, cfg.initial_capacity = 128, length, length
+    ws = ctypes.c_void_p()
+    assert L.rk_npu_attention_f16_prepare(ctx.domain, ctypes.byref(cfg), ctypes.byref(ws)) == 0
+    caches = []
+    g = torch.Generator(device="cuda")
+    g.manual_seed(11)
+    kd = torch.randn((kh, length, d), generator=g, device="cuda", dtype=torch.float32).half()
+    vd = torch.randn((kh, length, d), generator=g, device="cuda", dtype=torch.float32).half()
+    try:
+        for _ in range(layers):
+            c = ctypes.c_void_p()
+            assert L.rk_npu_attention_f16_cache_create(ctx.domain, ctypes.byref(cfg), ctypes.byref(c)) == 0
+            caches.append(c)
+            assert L.rk_npu_hip_attention_cache_append(c, kd.data_ptr(), vd.data_ptr(), length,
+                                                       torch.cuda.current_stream().cuda_stream) == 0
+        torch.cuda.synchronize()
+        q = torch.randn((qh, 128, d), generator=g, device="cuda", dtype=torch.float32).half()
+        out = torch.empty((qh, 128, d), dtype=torch.float32, device="cuda")
+        res = []
+        for rows, name in ((1, "decode"), (128, "prefill")):
+            pos = length - rows
+            qr = q[:, :rows].contiguous()
+            o = out[:, :rows].contiguous()
+
+            def step():
+                st = torch.cuda.current_stream().cuda_stream
+                for c in caches:
+                    L.rk_npu_hip_attention_run(ws, c, qr.data_ptr(), rows, pos, o.data_ptr(), 0, st)
+
+            assert L.rk_npu_hip_attention_run(ws, caches[0], qr.data_ptr(), rows, pos, o.data_ptr(), 0,
+                                              torch.cuda.current_stream().cuda_stream) == 0
+            ms, ms_eager, ms_graph, ok = best_time(torch, step, steps, 2, lambda: [o.clone()])
+            if rows == 1:
+                kv_bytes = layers * 2 * kh * length * d * 2
+                res.append({"workload": f"attention decode: GQA 32/8 heads, d=128, {length} cached rows, 1 query row, "
+                                        f"{layers} layers", "value": round(kv_bytes / (ms * 1e-3) / 1e9, 1),
+                            "unit": "GB/s", "ms_per_step": round(ms, 4), "us_per_layer": round(ms * 1e3 / layers, 2),
+                            "graph_matches_eager": ok})
+            else:
+                keys = sum(pos + r + 1 for r in range(rows))
+                flops = layers * 4.0 * qh * d * keys
+                res.append({"workload": f"attention prefill: GQA 32/8 heads, d=128, {rows} query rows ending at "
+                                        f"{length} cached rows, causal, {layers} layers",
+                            "value": round(flops / (ms * 1e-3) / 1e12, 2), "unit": "TFLOP/s",
+                            "ms_per_step": round(ms, 4), "us_per_layer": round(ms * 1e3 / layers, 2),
+                            "graph_matches_eager": ok})
+        return res
+    finally:
+        torch.cuda.synchronize()
+        for c in caches:
+            L.rk_npu_attention_f16_cache_free(c)
+        L.rk_npu_attention_f16_workspace_free(ws)
+
+
 def traffic_probe(torch, ctx, rows=1, reps=3):
     """Workload for the HBM-traffic counter runs (no timing): a plain 256 MiB
     device copy (known bytes: the calibration of FETCH_SIZE / WRITE_SIZE) and
@@ -502,7 +572,7 @@ def main():
     ap.add_argument("--primary-only", action="store_true", help="skip the secondary workloads")
     ap.add_argument("--decode-rows", type=int, default=1,
                     help="rows of the primary decode line (1 is the metric's configuration)")
-    ap.add_argument("--only", choices=["prefill", "ffn512", "up128", "moe"],
+    ap.add_argument("--only", choices=["prefill", "ffn512", "up128", "moe", "attention"],
                     help="run one secondary workload alone and print its result (for profiling)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only run the workload of the FETCH_SIZE / WRITE_SIZE counter runs")
@@ -522,7 +592,8 @@ def main():
         res = {"prefill": lambda: run_prefill(torch, ctx, 4096, steps, 2),
                "ffn512": lambda: run_ffn512(torch, ctx, steps, 2),
                "up128": lambda: run_up128(torch, ctx, args.steps, args.warmup),
-               "moe": lambda: run_moe(torch, ctx, steps, 2)}[args.only]()
+               "moe": lambda: run_moe(torch, ctx, steps, 2),
+               "attention": lambda: run_attention(torch, ctx, steps)}[args.only]()
         print(json.dumps(res), flush=True)
         return
     primary = run_decode(torch, ctx, args.decode_rows, args.steps, args.warmup, not args.no_cpu_baseline)
@@ -536,6 +607,7 @@ def main():
         secondary.append(run_ffn512(torch, ctx, max(4, args.steps // 2), 2))
         secondary.append(run_up128(torch, ctx, args.steps, args.warmup))
         secondary.extend(run_moe(torch, ctx, max(4, args.steps // 2), 2))
+        secondary.extend(run_attention(torch, ctx, max(4, args.steps // 2)))
     for s in secondary:
         s.pop("kernels", None)
         if "roofline" in s:

@@ -83,17 +83,28 @@ __device__ __forceinline__ float group_sum(float v) {
 
 // Block: 256 threads; RT query rows (RT = 4: 64 threads per row, RT = 16: 16
 // threads per row). Thread (row, sub) scores keys sub + RPT*i of each tile
-// and owns output dims [sub*DPT, sub*DPT + DPT) of its row.
+// and owns output dims [sub*DPT, sub*DPT + DPT) of its row. K/V tiles (64
+// keys, 32 at head_dim 256) go through two LDS buffers; the next tile's loads
+// are in flight (registers) while the current tile is computed. Scores are
+// v_dot2_f32_f16 sums over the fp16 q and k pairs (exact products, f32
+// accumulation) times the scale; p * v folds the fp16 conversion into the
+// multiply-add.
 template <int D, int RT>
 __global__ __launch_bounds__(256) void attn_split_kernel(AttnParams P) {
-    constexpr int KT = ATTN_KT;
-    constexpr int RPT = 256 / RT;  // threads per row
-    constexpr int SPT = KT / RPT;  // scores per thread per tile
-    constexpr int DPT = D / RPT;   // output dims per thread
-    constexpr int KP = D + 8;      // LDS row pitch of a K/V tile (halves)
-    static_assert(DPT >= 1 && D % RPT == 0 && D % 8 == 0, "head_dim must split over the row's threads");
-    __shared__ __attribute__((aligned(16))) float qs[RT][D];
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    constexpr int KT = D == 256 ? 32 : ATTN_KT;      // keys per tile
+    constexpr int RPT = 256 / RT;                    // threads per row
+    constexpr int SPT = KT >= RPT ? KT / RPT : 1;    // scores per thread per tile
+    constexpr int DPT = D / RPT;                     // output dims per thread
+    constexpr int KP = D + 8;                        // LDS row pitch of a K/V tile (halves)
+    constexpr int PER = (KT * (D / 8) + 255) / 256;  // 16-byte K (and V) pieces per thread per tile
+    constexpr int QPT = RT * D / 256;                // q halves per thread (2..16)
+    static_assert(DPT >= 1 && D % RPT == 0 && D % 8 == 0 && (QPT == 1 || QPT % 2 == 0),
+                  "head_dim must split over the threads");
+    constexpr int QW = QPT >= 2 ? QPT / 2 : 1;  // q words per thread (QPT = 1: one half)
+    __shared__ __attribute__((aligned(16))) __half qs[RT][D];
     __shared__ __attribute__((aligned(16))) __half ks[KT][KP];
+    __shared__ __attribute__((aligned(16))) __half vs[KT][KP];
     __shared__ float ps[RT][KT];
     const int split = blockIdx.x, rt = blockIdx.y, g = blockIdx.z;
     const int G = P.qh / P.kh, R = G * P.m;
@@ -105,54 +116,75 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnParams P) {
     if (P.causal) klimit = min(klimit, P.pos + qr + 1);
     const int k0 = split * P.keys_per_split;
     const int k1 = min(k0 + P.keys_per_split, P.key_end);
-    for (int i = tid; i < RT * D; i += 256) {
-        const int r = i / D, dd = i % D, row2 = rt * RT + r;
-        float val = 0.0f;
-        if (row2 < R) {
-            const int h2 = g * G + row2 / P.m, q2 = row2 % P.m;
-            val = __half2float(P.q[((size_t)h2 * P.m + q2) * D + dd]) * P.scale;
-        }
-        qs[r][dd] = val;
-    }
     const __half* kbase = P.k + (size_t)g * P.cap * D;
     const __half* vbase = P.v + (size_t)g * P.cap * D;
-    auto load_tile = [&](const __half* base, int kb) {
-        for (int i = tid; i < KT * (D / 8); i += 256) {
-            const int j = i / (D / 8), c = i % (D / 8), key = kb + j;
-            v4u val = v4u{0u, 0u, 0u, 0u};
-            if (key < k1) val = *reinterpret_cast<const v4u*>(base + (size_t)key * D + c * 8);
-            *reinterpret_cast<v4u*>(&ks[j][c * 8]) = val;
+    // q: thread's QPT halves of the [RT][D] tile, one load (rows past R: 0)
+    const int qe = tid * QPT, qrow = qe / D, qcol = qe % D, qrr = rt * RT + qrow;
+    const bool q_ok = qrr < R;
+    const __half* qsrc = P.q + ((size_t)(g * G + (q_ok ? qrr / P.m : 0)) * P.m + (q_ok ? qrr % P.m : 0)) * D + qcol;
+    unsigned qv[QW];
+#pragma unroll
+    for (int i = 0; i < QW; ++i)
+        qv[i] = QPT == 1 ? (unsigned)reinterpret_cast<const unsigned short*>(qsrc)[0]
+                         : reinterpret_cast<const unsigned*>(qsrc)[i];
+    v4u kr[PER], vr[PER];
+    auto issue = [&](int kb) {
+#pragma unroll
+        for (int t = 0; t < PER; ++t) {
+            const int i = tid + 256 * t, j = i / (D / 8), c = i % (D / 8), key = kb + j;
+            const bool ok = i < KT * (D / 8) && key < k1;
+            const size_t off = ok ? (size_t)key * D + c * 8 : 0;  // (masked: a valid row, zeroed at the store)
+            kr[t] = *reinterpret_cast<const v4u*>(kbase + off);
+            vr[t] = *reinterpret_cast<const v4u*>(vbase + off);
         }
     };
+    auto store = [&](int kb) {
+#pragma unroll
+        for (int t = 0; t < PER; ++t) {
+            const int i = tid + 256 * t, j = i / (D / 8), c = i % (D / 8), key = kb + j;
+            if (i < KT * (D / 8)) {
+                const bool ok = key < k1;
+                *reinterpret_cast<v4u*>(&ks[j][c * 8]) = ok ? kr[t] : v4u{0u, 0u, 0u, 0u};
+                *reinterpret_cast<v4u*>(&vs[j][c * 8]) = ok ? vr[t] : v4u{0u, 0u, 0u, 0u};
+            }
+        }
+    };
+    if (k0 < k1) issue(k0);
+    if constexpr (QPT == 1) {
+        reinterpret_cast<unsigned short*>(&qs[qrow][qcol])[0] = q_ok ? (unsigned short)qv[0] : (unsigned short)0;
+    } else {
+#pragma unroll
+        for (int i = 0; i < QW; ++i) reinterpret_cast<unsigned*>(&qs[qrow][qcol])[i] = q_ok ? qv[i] : 0u;
+    }
     float mrun = -INFINITY, lrun = 0.0f;
     float acc[DPT];
 #pragma unroll
     for (int e = 0; e < DPT; ++e) acc[e] = 0.0f;
     for (int kb = k0; kb < k1; kb += KT) {
-        __syncthreads();  // (previous tile's V reads done)
-        load_tile(kbase, kb);
+        __syncthreads();  // (the previous tile's reads are done)
+        store(kb);
         __syncthreads();
+        if (kb + KT < k1) issue(kb + KT);  // next tile in flight during this one
         float s[SPT];
         float tmax = -INFINITY;
 #pragma unroll
         for (int i = 0; i < SPT; ++i) {
             const int j = sub + RPT * i;
             float a = 0.0f;
+            if (j < KT) {
 #pragma unroll 4
-            for (int c = 0; c < D; c += 8) {
-                const v4u kw = *reinterpret_cast<const v4u*>(&ks[j][c]);
-                const float4 q0 = *reinterpret_cast<const float4*>(&qs[row][c]);
-                const float4 q1 = *reinterpret_cast<const float4*>(&qs[row][c + 4]);
-                const float qv[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+                for (int c = 0; c < D; c += 8) {
+                    const v4u kw = *reinterpret_cast<const v4u*>(&ks[j][c]);
+                    const v4u qw = *reinterpret_cast<const v4u*>(&qs[row][c]);
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const unsigned w = kw[e >> 1];
-                    const float kf = __half2float(__ushort_as_half((unsigned short)((e & 1) ? (w >> 16) : (w & 0xffffu))));
-                    a = __builtin_fmaf(qv[e], kf, a);
+                    for (int e = 0; e < 4; ++e) {
+                        const unsigned qu = qw[e], ku = kw[e];  // (copied out before the bit casts)
+                        a = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, qu), __builtin_bit_cast(h2, ku), a, false);
+                    }
                 }
             }
             const int key = kb + j;
-            s[i] = (row_ok && key < klimit && key < k1) ? a : -INFINITY;
+            s[i] = (row_ok && j < KT && key < klimit && key < k1) ? a * P.scale : -INFINITY;
             tmax = fmaxf(tmax, s[i]);
         }
         tmax = group_max<RPT>(tmax);
@@ -163,7 +195,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnParams P) {
 #pragma unroll
         for (int i = 0; i < SPT; ++i) {
             const float p = (s[i] == -INFINITY) ? 0.0f : __expf(s[i] - mnew);
-            ps[row][sub + RPT * i] = p;
+            if (sub + RPT * i < KT) ps[row][sub + RPT * i] = p;
             psum += p;
         }
         psum = group_sum<RPT>(psum);
@@ -171,14 +203,12 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnParams P) {
         mrun = mnew;
 #pragma unroll
         for (int e = 0; e < DPT; ++e) acc[e] *= alpha;
-        __syncthreads();  // (K reads done, p written)
-        load_tile(vbase, kb);
-        __syncthreads();
+        __syncthreads();  // (p written)
 #pragma unroll 4
         for (int j = 0; j < KT; ++j) {
             const float p = ps[row][j];
 #pragma unroll
-            for (int e = 0; e < DPT; ++e) acc[e] = __builtin_fmaf(p, __half2float(ks[j][sub * DPT + e]), acc[e]);
+            for (int e = 0; e < DPT; ++e) acc[e] = __builtin_fmaf(p, __half2float(vs[j][sub * DPT + e]), acc[e]);
         }
     }
     if (!row_ok) return;
@@ -205,24 +235,51 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnParams P) {
     for (int e = 0; e < DPT; ++e) part[2 + sub * DPT + e] = acc[e];
 }
 
-// Combine the splits of one (KV head, row): block = one row, thread = dims.
+// Combine the splits of one (KV head, row) for 64 of its dims: block = (row,
+// dim chunk), 256 threads = 64 dims x 4 groups of splits. The block takes the
+// max over the splits' maxima, the weights exp(m_s - M) into LDS and the
+// denominator sum_s w_s l_s, then each thread sums w_s * acc_s over its
+// group's splits (loads unrolled, independent) and the groups add in LDS.
+constexpr int ATTN_MAX_SPLITS = 256;
+
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams P, int D) {
-    const int rr = blockIdx.x, g = blockIdx.y;
+    __shared__ float w_s[ATTN_MAX_SPLITS];
+    __shared__ float red[4];
+    __shared__ float sums[4][64];
+    const int rr = blockIdx.x, g = blockIdx.y, d0 = blockIdx.z * 64;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int G = P.qh / P.kh, R = G * P.m;
-    if (rr >= R) return;
+    if (rr >= R) return;  // (uniform over the block)
     const int h = g * G + rr / P.m, qr = rr % P.m;
     const float* p0 = P.part + (((size_t)g * P.rows_pad + rr) * P.splits) * (D + 2);
-    float M = -INFINITY;
-    for (int s = 0; s < P.splits; ++s) M = fmaxf(M, p0[(size_t)s * (D + 2)]);
-    for (int dd = threadIdx.x; dd < D; dd += 256) {
-        float num = 0.0f, den = 0.0f;
-        for (int s = 0; s < P.splits; ++s) {
-            const float* ps = p0 + (size_t)s * (D + 2);
-            const float w = (ps[0] == -INFINITY) ? 0.0f : __expf(ps[0] - M);
-            num = __builtin_fmaf(w, ps[2 + dd], num);
-            den = __builtin_fmaf(w, ps[1], den);
-        }
-        const float y = num / den;
+    float mx = -INFINITY;
+    for (int s = tid; s < P.splits; s += 256) mx = fmaxf(mx, p0[(size_t)s * (D + 2)]);
+    mx = wave_max(mx);
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    float den = 0.0f;
+    for (int s = tid; s < P.splits; s += 256) {
+        const float* ps = p0 + (size_t)s * (D + 2);
+        const float w = (ps[0] == -INFINITY) ? 0.0f : __expf(ps[0] - M);
+        w_s[s] = w;
+        den = __builtin_fmaf(w, ps[1], den);
+    }
+    den = group_sum<64>(den);
+    if (lane == 0) red[wave] = den;
+    __syncthreads();
+    const float inv = 1.0f / ((red[0] + red[1]) + (red[2] + red[3]));
+    const int dd = d0 + lane;  // (wave = group of splits s = wave + 4k)
+    float num = 0.0f;
+    if (dd < D) {
+#pragma unroll 8
+        for (int s = wave; s < P.splits; s += 4) num = __builtin_fmaf(w_s[s], p0[(size_t)s * (D + 2) + 2 + dd], num);
+    }
+    sums[wave][lane] = num;
+    __syncthreads();
+    if (wave == 0 && dd < D) {
+        const float y = ((sums[0][lane] + sums[1][lane]) + (sums[2][lane] + sums[3][lane])) * inv;
         const size_t o = ((size_t)h * P.m + qr) * D + dd;
         if (P.out_f16)
             static_cast<__half*>(P.out)[o] = __float2half_rn(y);
@@ -230,7 +287,6 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams P, int D) 
             static_cast<float*>(P.out)[o] = y;
     }
 }
-
 
 // ---------------------------------------------------------------------------
 // Host side.
@@ -357,12 +413,13 @@ static AttnPlan plan_attention(const rk_npu_attention_f16_config& c, int rows, i
     p.rt = R <= 4 ? 4 : 16;
     p.row_tiles = (R + p.rt - 1) / p.rt;
     p.key_end = (c.mask_mode == RK_NPU_ATTENTION_F16_CAUSAL) ? std::min(len, pos + rows) : len;
-    const int tiles = (p.key_end + ATTN_KT - 1) / ATTN_KT;
+    const int kt = c.head_dim == 256 ? 32 : ATTN_KT;  // keys per tile of the kernel
+    const int tiles = (p.key_end + kt - 1) / kt;
     const int base = p.row_tiles * c.kv_heads;
     int want = base >= 512 ? 1 : (512 + base - 1) / base;
-    want = std::max(1, std::min(want, tiles));
+    want = std::max(1, std::min(std::min(want, tiles), ATTN_MAX_SPLITS));
     const int tiles_per_split = (tiles + want - 1) / want;
-    p.keys_per_split = tiles_per_split * ATTN_KT;
+    p.keys_per_split = tiles_per_split * kt;
     p.splits = (p.key_end + p.keys_per_split - 1) / p.keys_per_split;
     if (p.splits < 1) p.splits = 1;
     return p;
@@ -418,7 +475,7 @@ static int enqueue_attention(AttnWork* w, AttnCache* c, const __half* q, int row
 #undef HM_ATTN
     if (pl.splits > 1) {
         const int G = cfg.query_heads / cfg.kv_heads;
-        hipLaunchKernelGGL(attn_combine_kernel, dim3(G * rows, cfg.kv_heads), dim3(std::min(256, D)), 0, s, P, D);
+        hipLaunchKernelGGL(attn_combine_kernel, dim3(G * rows, cfg.kv_heads, (D + 63) / 64), dim3(256), 0, s, P, D);
     }
     return hipGetLastError() == hipSuccess ? RK_NPU_OK : RK_NPU_ERR_DEVICE;
 }
