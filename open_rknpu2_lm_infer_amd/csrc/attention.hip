@@ -35,8 +35,10 @@ namespace hm {
 constexpr uint32_t MAGIC_ATTN_CACHE = 0x43414841u;
 constexpr uint32_t MAGIC_ATTN_WORK = 0x57414841u;
 constexpr int ATTN_KT = 64;              // keys per tile
-// Blocks that write partials: at most 1024 (see plan_attention), RT <= 16 rows each.
-constexpr size_t ATTN_PARTIAL_ROWS = 1024 * 16;
+// Partial rows a workspace holds: plan_attention launches fewer than 1024
+// blocks when it splits the keys, each with at most 64 query rows (head_dim
+// 64 and 128, MFMA tiles) or 16 (head_dim 256).
+static inline size_t attn_partial_rows(int head_dim) { return (size_t)1024 * (head_dim <= 128 ? 64 : 16); }
 
 struct AttnParams {
     const __half* q;  // [qh][m][D]
@@ -235,6 +237,182 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnParams P) {
     for (int e = 0; e < DPT; ++e) part[2 + sub * DPT + e] = acc[e];
 }
 
+// MFMA variant for 16 or more query rows per KV head (head_dim 64 or 128):
+// block = 4 waves x 16 query rows; per 64-key tile, S = Q K^T with
+// v_mfma_f32_16x16x16f16 (fp16 operands, f32 accumulation; Q fragments stay
+// in registers, K tile row-major in LDS), the online softmax on S in the
+// accumulator layout (row-wise reductions over 16 lanes), P rounded to fp16
+// and staged through the wave's LDS rows as the A operand, and O += P V with
+// V stored transposed in LDS. Operand layouts (16x16x16, wave64): A lane l =
+// row l%16, k 4(l/16)..+3; B lane l = column l%16, k 4(l/16)..+3; C lane l =
+// rows 4(l/16)..+3 of column l%16.
+template <int D>
+__global__ __launch_bounds__(256) void attn_mfma_kernel(AttnParams P) {
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    typedef unsigned u2 __attribute__((ext_vector_type(2)));
+    constexpr int KT = ATTN_KT, RT = 64, KS = D / 16, NB = D / 16;
+    constexpr int KP = D + 8, VP = KT + 8, PP = KT + 8;
+    constexpr int PER = KT * (D / 8) / 256;  // 16-byte K (and V) pieces per thread per tile
+    static_assert(D == 64 || D == 128, "MFMA attention: head_dim 64 or 128");
+    __shared__ __attribute__((aligned(16))) __half ks[KT][KP];
+    __shared__ __attribute__((aligned(16))) __half vt[D][VP];
+    __shared__ __attribute__((aligned(16))) __half pl[4][16][PP];
+    const int split = blockIdx.x, rt = blockIdx.y, g = blockIdx.z;
+    const int G = P.qh / P.kh, R = G * P.m;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lo = lane & 15, hi = lane >> 4;
+    const int row0 = rt * RT + wave * 16;
+    const int k0 = split * P.keys_per_split;
+    const int k1 = min(k0 + P.keys_per_split, P.key_end);
+    const __half* kbase = P.k + (size_t)g * P.cap * D;
+    const __half* vbase = P.v + (size_t)g * P.cap * D;
+    // A fragments of Q: row row0 + lo, dims 16*ks + 4*hi .. +3
+    h4 qa[KS];
+    {
+        const int rr = row0 + lo;
+        const bool ok = rr < R;
+        const __half* qrow = P.q + ((size_t)(g * G + (ok ? rr / P.m : 0)) * P.m + (ok ? rr % P.m : 0)) * D;
+#pragma unroll
+        for (int k = 0; k < KS; ++k) {
+            const u2 w = ok ? *reinterpret_cast<const u2*>(qrow + 16 * k + 4 * hi) : u2{0u, 0u};
+            qa[k] = __builtin_bit_cast(h4, w);
+        }
+    }
+    // rows this lane holds in the accumulator layout, and their key limits
+    int climit[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int rr = row0 + 4 * hi + r;
+        int lim = 0;
+        if (rr < R) {
+            lim = P.len;
+            if (P.causal) lim = min(lim, P.pos + rr % P.m + 1);
+        }
+        climit[r] = lim;
+    }
+    // K pieces: piece i = key i / (D/8), dims 8*(i % (D/8)); V pieces: key i % KT, dims 8*(i / KT)
+    v4u kr[PER], vr[PER];
+    auto issue = [&](int kb) {
+#pragma unroll
+        for (int t = 0; t < PER; ++t) {
+            const int i = tid + 256 * t;
+            const int kj = i / (D / 8), kc = i % (D / 8), vj = i % KT, vc = i / KT;
+            const int kkey = kb + kj, vkey = kb + vj;
+            kr[t] = *reinterpret_cast<const v4u*>(kbase + (kkey < k1 ? (size_t)kkey * D + kc * 8 : 0));
+            vr[t] = *reinterpret_cast<const v4u*>(vbase + (vkey < k1 ? (size_t)vkey * D + vc * 8 : 0));
+        }
+    };
+    auto store = [&](int kb) {
+#pragma unroll
+        for (int t = 0; t < PER; ++t) {
+            const int i = tid + 256 * t;
+            const int kj = i / (D / 8), kc = i % (D / 8), vj = i % KT, vc = i / KT;
+            *reinterpret_cast<v4u*>(&ks[kj][kc * 8]) = (kb + kj < k1) ? kr[t] : v4u{0u, 0u, 0u, 0u};
+            const v4u w = (kb + vj < k1) ? vr[t] : v4u{0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const unsigned word = w[e >> 1];
+                reinterpret_cast<unsigned short*>(&vt[vc * 8 + e][vj])[0] =
+                    (unsigned short)((e & 1) ? (word >> 16) : (word & 0xffffu));
+            }
+        }
+    };
+    f4 o[NB];
+#pragma unroll
+    for (int n = 0; n < NB; ++n) o[n] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    float mrun[4], lrun[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        mrun[r] = -INFINITY;
+        lrun[r] = 0.0f;
+    }
+    if (k0 < k1) issue(k0);
+    for (int kb = k0; kb < k1; kb += KT) {
+        __syncthreads();  // (the previous tile's reads are done)
+        store(kb);
+        __syncthreads();
+        if (kb + KT < k1) issue(kb + KT);
+        f4 sacc[4];
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) {
+            sacc[cb] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int k = 0; k < KS; ++k) {
+                const u2 w = *reinterpret_cast<const u2*>(&ks[cb * 16 + lo][16 * k + 4 * hi]);
+                sacc[cb] = __builtin_amdgcn_mfma_f32_16x16x16f16(qa[k], __builtin_bit_cast(h4, w), sacc[cb], 0, 0, 0);
+            }
+        }
+        float alpha[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            float tmax = -INFINITY;
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb) {
+                const int key = kb + cb * 16 + lo;
+                const float sv = (key < climit[r] && key < k1) ? sacc[cb][r] * P.scale : -INFINITY;
+                sacc[cb][r] = sv;
+                tmax = fmaxf(tmax, sv);
+            }
+            tmax = group_max<16>(tmax);
+            const float mnew = fmaxf(mrun[r], tmax);
+            alpha[r] = (mnew == -INFINITY) ? 1.0f : __expf(mrun[r] - mnew);
+            float psum = 0.0f;
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb) {
+                const float pv = (sacc[cb][r] == -INFINITY) ? 0.0f : __expf(sacc[cb][r] - mnew);
+                const _Float16 ph = (_Float16)pv;
+                pl[wave][4 * hi + r][cb * 16 + lo] = __builtin_bit_cast(__half, ph);
+                psum += (float)ph;  // the weights P V uses
+            }
+            psum = group_sum<16>(psum);
+            lrun[r] = lrun[r] * alpha[r] + psum;
+            mrun[r] = mnew;
+        }
+#pragma unroll
+        for (int n = 0; n < NB; ++n)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o[n][r] *= alpha[r];
+        wait_lgkmcnt0();  // (P rows written by this wave's lanes, read back below)
+#pragma unroll
+        for (int k = 0; k < KT / 16; ++k) {
+            const u2 aw = *reinterpret_cast<const u2*>(&pl[wave][lo][16 * k + 4 * hi]);
+            const h4 a = __builtin_bit_cast(h4, aw);
+#pragma unroll
+            for (int n = 0; n < NB; ++n) {
+                const u2 bw = *reinterpret_cast<const u2*>(&vt[16 * n + lo][16 * k + 4 * hi]);
+                o[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, __builtin_bit_cast(h4, bw), o[n], 0, 0, 0);
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int rr = row0 + 4 * hi + r;
+        if (rr >= R) continue;
+        const int h = g * G + rr / P.m, qr = rr % P.m;
+        if (P.splits == 1) {
+            const float inv = 1.0f / lrun[r];
+            const size_t o0 = ((size_t)h * P.m + qr) * D;
+#pragma unroll
+            for (int n = 0; n < NB; ++n) {
+                const float y = o[n][r] * inv;
+                if (P.out_f16)
+                    static_cast<__half*>(P.out)[o0 + 16 * n + lo] = __float2half_rn(y);
+                else
+                    static_cast<float*>(P.out)[o0 + 16 * n + lo] = y;
+            }
+        } else {
+            float* part = P.part + (((size_t)g * P.rows_pad + rr) * P.splits + split) * (D + 2);
+            if (lo == 0) {
+                part[0] = mrun[r];
+                part[1] = lrun[r];
+            }
+#pragma unroll
+            for (int n = 0; n < NB; ++n) part[2 + 16 * n + lo] = o[n][r];
+        }
+    }
+}
+
 // Combine the splits of one (KV head, row) for 64 of its dims: block = (row,
 // dim chunk), 256 threads = 64 dims x 4 groups of splits. The block takes the
 // max over the splits' maxima, the weights exp(m_s - M) into LDS and the
@@ -333,7 +511,7 @@ static size_t kv_bytes(const rk_npu_attention_f16_config* c, int capacity) {
 }
 
 static size_t part_bytes(const rk_npu_attention_f16_config* c) {
-    return ATTN_PARTIAL_ROWS * (size_t)(c->head_dim + 2) * sizeof(float);
+    return attn_partial_rows(c->head_dim) * (size_t)(c->head_dim + 2) * sizeof(float);
 }
 
 static AttnCache* as_cache(void* p) {
@@ -400,6 +578,7 @@ static int cache_put(AttnCache* c, const void* k, const void* v, int rows, hipMe
 }
 
 struct AttnPlan {
+    bool mfma;  // attn_mfma_kernel (64-row tiles) instead of attn_split_kernel
     int rt, row_tiles, splits, keys_per_split, key_end;
 };
 
@@ -410,7 +589,8 @@ struct AttnPlan {
 static AttnPlan plan_attention(const rk_npu_attention_f16_config& c, int rows, int len, int pos) {
     AttnPlan p;
     const int G = c.query_heads / c.kv_heads, R = G * rows;
-    p.rt = R <= 4 ? 4 : 16;
+    p.mfma = R >= 16 && (c.head_dim == 64 || c.head_dim == 128);
+    p.rt = p.mfma ? 64 : (R <= 4 ? 4 : 16);
     p.row_tiles = (R + p.rt - 1) / p.rt;
     p.key_end = (c.mask_mode == RK_NPU_ATTENTION_F16_CAUSAL) ? std::min(len, pos + rows) : len;
     const int kt = c.head_dim == 256 ? 32 : ATTN_KT;  // keys per tile of the kernel
@@ -437,7 +617,7 @@ static int enqueue_attention(AttnWork* w, AttnCache* c, const __half* q, int row
     if (rows < 1 || rows > w->cfg.max_query_rows || pos < 0 || c->length < 1) return RK_NPU_ERR_PARAM;
     if (causal && (long)pos + rows > c->length) return RK_NPU_ERR_PARAM;
     const AttnPlan pl = plan_attention(cfg, rows, c->length, pos);
-    if (pl.splits > 1 && (size_t)pl.row_tiles * pl.rt * cfg.kv_heads * pl.splits > ATTN_PARTIAL_ROWS)
+    if (pl.splits > 1 && (size_t)pl.row_tiles * pl.rt * cfg.kv_heads * pl.splits > attn_partial_rows(cfg.head_dim))
         return RK_NPU_ERR_UNSUPPORTED;
     AttnParams P;
     P.q = q;
@@ -465,7 +645,11 @@ static int enqueue_attention(AttnWork* w, AttnCache* c, const __half* q, int row
         launch_attn<DD, 4>(P, pl, cfg.kv_heads, s);                    \
     else                                                               \
         launch_attn<DD, 16>(P, pl, cfg.kv_heads, s);
-    if (D == 64) {
+    if (pl.mfma && D == 64) {
+        hipLaunchKernelGGL(attn_mfma_kernel<64>, dim3(pl.splits, pl.row_tiles, cfg.kv_heads), dim3(256), 0, s, P);
+    } else if (pl.mfma && D == 128) {
+        hipLaunchKernelGGL(attn_mfma_kernel<128>, dim3(pl.splits, pl.row_tiles, cfg.kv_heads), dim3(256), 0, s, P);
+    } else if (D == 64) {
         HM_ATTN(64)
     } else if (D == 128) {
         HM_ATTN(128)
