@@ -20,6 +20,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <new>
 
@@ -35,10 +36,11 @@ namespace hm {
 constexpr uint32_t MAGIC_ATTN_CACHE = 0x43414841u;
 constexpr uint32_t MAGIC_ATTN_WORK = 0x57414841u;
 constexpr int ATTN_KT = 64;              // keys per tile
-// Partial rows a workspace holds: plan_attention launches fewer than 1024
+constexpr int ATTN_MAX_SPLITS = 256;     // key splits per (KV head, row tile)
+// Partial rows a workspace holds: plan_attention launches at most 2048
 // blocks when it splits the keys, each with at most 64 query rows (head_dim
 // 64 and 128, MFMA tiles) or 16 (head_dim 256).
-static inline size_t attn_partial_rows(int head_dim) { return (size_t)1024 * (head_dim <= 128 ? 64 : 16); }
+static inline size_t attn_partial_rows(int head_dim) { return (size_t)2048 * (head_dim <= 128 ? 64 : 16); }
 
 struct AttnParams {
     const __half* q;  // [qh][m][D]
@@ -237,232 +239,364 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnParams P) {
     for (int e = 0; e < DPT; ++e) part[2 + sub * DPT + e] = acc[e];
 }
 
-// MFMA variant for 16 or more query rows per KV head (head_dim 64 or 128):
-// block = 4 waves x 16 query rows; per 64-key tile, S = Q K^T with
-// v_mfma_f32_16x16x16f16 (fp16 operands, f32 accumulation; Q fragments stay
-// in registers, K tile row-major in LDS), the online softmax on S in the
-// accumulator layout (row-wise reductions over 16 lanes), P rounded to fp16
-// and staged through the wave's LDS rows as the A operand, and O += P V with
-// V stored transposed in LDS. Operand layouts (16x16x16, wave64): A lane l =
-// row l%16, k 4(l/16)..+3; B lane l = column l%16, k 4(l/16)..+3; C lane l =
-// rows 4(l/16)..+3 of column l%16.
+// Matrix-core variant for 16 or more query rows per KV head (head_dim 64 or
+// 128). Block = 4 waves, each owning 16 query rows of one KV head, over
+// 64-key tiles of its key split; the K/V tile is shared by the block (K
+// row-major, V transposed in LDS; the next tile's loads are in flight in
+// registers meanwhile). Per tile, with v_mfma_f32_16x16x32_f16 (fp16
+// operands, f32 accumulation):
+//   S^T = K Q^T   A = K rows from LDS, B = Q fragments held in registers;
+//                 the accumulator gives lane l the raw scores of query row
+//                 l%16 for keys 4(l/16)..+3 of each 16-key block,
+//   softmax       row max over the lane's 16 scores and the 3 other lanes of
+//                 its row; weights p = 2^(s c - m) with c = scale * log2(e)
+//                 and m the running max in those units, rounded to fp16 in
+//                 place; m moves only when a row's max grows by more than
+//                 ATTN_LAZY (so p <= 2^ATTN_LAZY, which fp16 holds), and only
+//                 then are the accumulators and sums rescaled,
+//   O^T += V^T P^T  A = V^T rows from LDS, B = the weights as they lie (the
+//                 accumulator layout of S^T is the B layout of P^T once each
+//                 lane's 8 k-slots name keys {4(l/16)..+3, 16+4(l/16)..+3} of
+//                 a 32-key step, which A reads to match),
+// so a lane's O^T accumulators all belong to its own query row and every
+// rescale is lane-local; each lane keeps a partial sum of its own weights
+// (v_dot2 against ones: the fp16 weights summed exactly in f32), added over
+// the row's 4 lanes at the end. Masks (causal, keys past the split) apply
+// only on tiles that cross them.
+// Operand layouts (16x16x32, wave64): A lane l = row l%16, k-slots
+// 8(l/16)..+7; B lane l = column l%16, same k-slots; C lane l = rows
+// 4(l/16)..+3 of column l%16.
+constexpr float ATTN_LAZY = 8.0f;
+
 template <int D>
 __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnParams P) {
-    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+    typedef _Float16 hh2 __attribute__((ext_vector_type(2)));
     typedef float f4 __attribute__((ext_vector_type(4)));
     typedef unsigned u2 __attribute__((ext_vector_type(2)));
-    constexpr int KT = ATTN_KT, RT = 64, KS = D / 16, NB = D / 16;
-    constexpr int KP = D + 8, VP = KT + 8, PP = KT + 8;
-    constexpr int PER = KT * (D / 8) / 256;  // 16-byte K (and V) pieces per thread per tile
+    constexpr int KT = ATTN_KT, KS = D / 32, NB = D / 16;
+    constexpr int KP = D + 8, VP = KT + 8;
+    constexpr int KPIECES = KT * (D / 8);        // 16-byte K pieces per tile
+    constexpr int VPIECES = (KT / 4) * (D / 8);  // 4 keys x 8 dims V pieces per tile
+    constexpr int KPT = KPIECES / 256;
     static_assert(D == 64 || D == 128, "MFMA attention: head_dim 64 or 128");
+    static_assert(KT == 64 && KPIECES % 256 == 0 && VPIECES <= 256, "tile shape");
     __shared__ __attribute__((aligned(16))) __half ks[KT][KP];
     __shared__ __attribute__((aligned(16))) __half vt[D][VP];
-    __shared__ __attribute__((aligned(16))) __half pl[4][16][PP];
     const int split = blockIdx.x, rt = blockIdx.y, g = blockIdx.z;
     const int G = P.qh / P.kh, R = G * P.m;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int lo = lane & 15, hi = lane >> 4;
-    const int row0 = rt * RT + wave * 16;
     const int k0 = split * P.keys_per_split;
     const int k1 = min(k0 + P.keys_per_split, P.key_end);
+    const float c = P.scale * 1.4426950408889634f;
     const __half* kbase = P.k + (size_t)g * P.cap * D;
     const __half* vbase = P.v + (size_t)g * P.cap * D;
-    // A fragments of Q: row row0 + lo, dims 16*ks + 4*hi .. +3
-    h4 qa[KS];
+    // this lane's query row, its key limit and Q fragments
+    const int rr = rt * 64 + wave * 16 + lo;
+    const bool row_ok = rr < R;
+    int lim = 0;
+    if (row_ok) {
+        lim = P.len;
+        if (P.causal) lim = min(lim, P.pos + rr % P.m + 1);
+    }
+    // keys below `open` are visible to every row of this wave (rows past R
+    // are discarded, so they do not count)
+    int open = row_ok ? lim : 0x7fffffff;
+    open = min(open, __shfl_xor(open, 1));
+    open = min(open, __shfl_xor(open, 2));
+    open = min(open, __shfl_xor(open, 4));
+    open = min(open, __shfl_xor(open, 8));
+    open = min(open, k1);
+    h8 qf[KS];
     {
-        const int rr = row0 + lo;
-        const bool ok = rr < R;
-        const __half* qrow = P.q + ((size_t)(g * G + (ok ? rr / P.m : 0)) * P.m + (ok ? rr % P.m : 0)) * D;
+        const __half* qp = P.q + ((size_t)(g * G + (row_ok ? rr / P.m : 0)) * P.m + (row_ok ? rr % P.m : 0)) * D;
 #pragma unroll
         for (int k = 0; k < KS; ++k) {
-            const u2 w = ok ? *reinterpret_cast<const u2*>(qrow + 16 * k + 4 * hi) : u2{0u, 0u};
-            qa[k] = __builtin_bit_cast(h4, w);
+            const v4u x = row_ok ? *reinterpret_cast<const v4u*>(qp + 32 * k + 8 * hi) : v4u{0u, 0u, 0u, 0u};
+            qf[k] = __builtin_bit_cast(h8, x);
         }
     }
-    // rows this lane holds in the accumulator layout, and their key limits
-    int climit[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int rr = row0 + 4 * hi + r;
-        int lim = 0;
-        if (rr < R) {
-            lim = P.len;
-            if (P.causal) lim = min(lim, P.pos + rr % P.m + 1);
-        }
-        climit[r] = lim;
-    }
-    // K pieces: piece i = key i / (D/8), dims 8*(i % (D/8)); V pieces: key i % KT, dims 8*(i / KT)
-    v4u kr[PER], vr[PER];
+    // K piece i: key i / (D/8), dims 8 (i % (D/8)); V piece (tid): keys
+    // 4 (tid % 16)..+3, dims 8 (tid / 16)..+7
+    const bool vthread = tid < VPIECES;
+    const int vj = tid & 15, vc = tid >> 4;
+    v4u kr[KPT], vr[4];
     auto issue = [&](int kb) {
+        const bool full = kb + KT <= k1;
 #pragma unroll
-        for (int t = 0; t < PER; ++t) {
+        for (int t = 0; t < KPT; ++t) {
             const int i = tid + 256 * t;
-            const int kj = i / (D / 8), kc = i % (D / 8), vj = i % KT, vc = i / KT;
-            const int kkey = kb + kj, vkey = kb + vj;
-            kr[t] = *reinterpret_cast<const v4u*>(kbase + (kkey < k1 ? (size_t)kkey * D + kc * 8 : 0));
-            vr[t] = *reinterpret_cast<const v4u*>(vbase + (vkey < k1 ? (size_t)vkey * D + vc * 8 : 0));
+            const int key = kb + i / (D / 8);
+            kr[t] = *reinterpret_cast<const v4u*>(
+                kbase + ((full || key < k1) ? (size_t)key * D + (i % (D / 8)) * 8 : 0));
+        }
+        if (vthread) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int key = kb + 4 * vj + t;
+                vr[t] = *reinterpret_cast<const v4u*>(vbase + ((full || key < k1) ? (size_t)key * D + vc * 8 : 0));
+            }
         }
     };
     auto store = [&](int kb) {
+        if (kb + KT > k1) {  // (block-uniform) zero the keys past the split
 #pragma unroll
-        for (int t = 0; t < PER; ++t) {
+            for (int t = 0; t < KPT; ++t)
+                if (kb + (tid + 256 * t) / (D / 8) >= k1) kr[t] = v4u{0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                if (kb + 4 * vj + t >= k1) vr[t] = v4u{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int t = 0; t < KPT; ++t) {
             const int i = tid + 256 * t;
-            const int kj = i / (D / 8), kc = i % (D / 8), vj = i % KT, vc = i / KT;
-            *reinterpret_cast<v4u*>(&ks[kj][kc * 8]) = (kb + kj < k1) ? kr[t] : v4u{0u, 0u, 0u, 0u};
-            const v4u w = (kb + vj < k1) ? vr[t] : v4u{0u, 0u, 0u, 0u};
+            *reinterpret_cast<v4u*>(&ks[i / (D / 8)][(i % (D / 8)) * 8]) = kr[t];
+        }
+        if (vthread) {
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const unsigned word = w[e >> 1];
-                reinterpret_cast<unsigned short*>(&vt[vc * 8 + e][vj])[0] =
-                    (unsigned short)((e & 1) ? (word >> 16) : (word & 0xffffu));
+                const int cw = e >> 1;
+                u2 x;
+                if (e & 1) {
+                    x[0] = (vr[0][cw] >> 16) | (vr[1][cw] & 0xffff0000u);
+                    x[1] = (vr[2][cw] >> 16) | (vr[3][cw] & 0xffff0000u);
+                } else {
+                    x[0] = (vr[0][cw] & 0xffffu) | (vr[1][cw] << 16);
+                    x[1] = (vr[2][cw] & 0xffffu) | (vr[3][cw] << 16);
+                }
+                *reinterpret_cast<u2*>(&vt[vc * 8 + e][4 * vj]) = x;
             }
         }
     };
     f4 o[NB];
 #pragma unroll
     for (int n = 0; n < NB; ++n) o[n] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-    float mrun[4], lrun[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        mrun[r] = -INFINITY;
-        lrun[r] = 0.0f;
-    }
+    float mrun = -INFINITY, lpart = 0.0f;
+    const hh2 ones = {(_Float16)1.0f, (_Float16)1.0f};
     if (k0 < k1) issue(k0);
     for (int kb = k0; kb < k1; kb += KT) {
-        __syncthreads();  // (the previous tile's reads are done)
+        __syncthreads();  // (the previous tile's LDS reads are done)
         store(kb);
         __syncthreads();
         if (kb + KT < k1) issue(kb + KT);
         f4 sacc[4];
 #pragma unroll
         for (int cb = 0; cb < 4; ++cb) {
+            h8 a[KS];
+#pragma unroll
+            for (int k = 0; k < KS; ++k)
+                a[k] = __builtin_bit_cast(h8, *reinterpret_cast<const v4u*>(&ks[cb * 16 + lo][32 * k + 8 * hi]));
             sacc[cb] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int k = 0; k < KS; ++k) {
-                const u2 w = *reinterpret_cast<const u2*>(&ks[cb * 16 + lo][16 * k + 4 * hi]);
-                sacc[cb] = __builtin_amdgcn_mfma_f32_16x16x16f16(qa[k], __builtin_bit_cast(h4, w), sacc[cb], 0, 0, 0);
-            }
+            for (int k = 0; k < KS; ++k)
+                sacc[cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[k], qf[k], sacc[cb], 0, 0, 0);
         }
-        float alpha[4];
+        if (kb + KT > open) {  // (wave-uniform) the tile crosses a mask
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            float tmax = -INFINITY;
+            for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
-            for (int cb = 0; cb < 4; ++cb) {
-                const int key = kb + cb * 16 + lo;
-                const float sv = (key < climit[r] && key < k1) ? sacc[cb][r] * P.scale : -INFINITY;
-                sacc[cb][r] = sv;
-                tmax = fmaxf(tmax, sv);
+                for (int r = 0; r < 4; ++r) {
+                    const int key = kb + cb * 16 + 4 * hi + r;
+                    if (!(key < lim && key < k1)) sacc[cb][r] = -INFINITY;
+                }
+        }
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb)
+            tmax = fmaxf(fmaxf(tmax, fmaxf(sacc[cb][0], sacc[cb][1])), fmaxf(sacc[cb][2], sacc[cb][3]));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+        const float tm = tmax * c;
+        const bool grow = tm > mrun + ATTN_LAZY;
+        if (__any(grow)) {  // (wave-uniform)
+            float alpha = 1.0f;
+            if (grow) {
+                alpha = __builtin_amdgcn_exp2f(mrun - tm);  // (0 from -inf)
+                mrun = tm;
             }
-            tmax = group_max<16>(tmax);
-            const float mnew = fmaxf(mrun[r], tmax);
-            alpha[r] = (mnew == -INFINITY) ? 1.0f : __expf(mrun[r] - mnew);
-            float psum = 0.0f;
+            lpart *= alpha;
 #pragma unroll
-            for (int cb = 0; cb < 4; ++cb) {
-                const float pv = (sacc[cb][r] == -INFINITY) ? 0.0f : __expf(sacc[cb][r] - mnew);
-                const _Float16 ph = (_Float16)pv;
-                pl[wave][4 * hi + r][cb * 16 + lo] = __builtin_bit_cast(__half, ph);
-                psum += (float)ph;  // the weights P V uses
+            for (int n = 0; n < NB; ++n) o[n] *= alpha;
+        }
+        const float msub = (mrun == -INFINITY) ? 0.0f : mrun;  // (no visible key yet: all scores -inf)
+        h8 pb[2];
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) {
+#pragma unroll
+            for (int r = 0; r < 4; r += 2) {
+                const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[cb][r], c, -msub));
+                const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[cb][r + 1], c, -msub));
+                const hh2 ph = {(_Float16)p0, (_Float16)p1};
+                pb[cb >> 1][(cb & 1) * 4 + r] = ph[0];
+                pb[cb >> 1][(cb & 1) * 4 + r + 1] = ph[1];
+                lpart = __builtin_amdgcn_fdot2(ph, ones, lpart, false);
             }
-            psum = group_sum<16>(psum);
-            lrun[r] = lrun[r] * alpha[r] + psum;
-            mrun[r] = mnew;
         }
 #pragma unroll
         for (int n = 0; n < NB; ++n)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) o[n][r] *= alpha[r];
-        wait_lgkmcnt0();  // (P rows written by this wave's lanes, read back below)
-#pragma unroll
-        for (int k = 0; k < KT / 16; ++k) {
-            const u2 aw = *reinterpret_cast<const u2*>(&pl[wave][lo][16 * k + 4 * hi]);
-            const h4 a = __builtin_bit_cast(h4, aw);
-#pragma unroll
-            for (int n = 0; n < NB; ++n) {
-                const u2 bw = *reinterpret_cast<const u2*>(&vt[16 * n + lo][16 * k + 4 * hi]);
-                o[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, __builtin_bit_cast(h4, bw), o[n], 0, 0, 0);
+            for (int k = 0; k < 2; ++k) {
+                const u2 a0 = *reinterpret_cast<const u2*>(&vt[16 * n + lo][32 * k + 4 * hi]);
+                const u2 a1 = *reinterpret_cast<const u2*>(&vt[16 * n + lo][32 * k + 16 + 4 * hi]);
+                const h8 a = __builtin_bit_cast(h8, v4u{a0[0], a0[1], a1[0], a1[1]});
+                o[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb[k], o[n], 0, 0, 0);
             }
+    }
+    float l = lpart;
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    if (!row_ok) return;
+    const int h = g * G + rr / P.m, qr = rr % P.m;
+    if (P.splits == 1) {
+        const float inv = 1.0f / l;
+        const size_t o0 = ((size_t)h * P.m + qr) * D + 4 * hi;
+#pragma unroll
+        for (int n = 0; n < NB; ++n) {
+            const f4 y = o[n] * inv;
+            if (P.out_f16) {
+                const unsigned short b0 = __half_as_ushort(__float2half_rn(y[0]));
+                const unsigned short b1 = __half_as_ushort(__float2half_rn(y[1]));
+                const unsigned short b2 = __half_as_ushort(__float2half_rn(y[2]));
+                const unsigned short b3 = __half_as_ushort(__float2half_rn(y[3]));
+                *reinterpret_cast<u2*>(static_cast<__half*>(P.out) + o0 + 16 * n) =
+                    u2{b0 | ((unsigned)b1 << 16), b2 | ((unsigned)b3 << 16)};
+            } else {
+                *reinterpret_cast<f4*>(static_cast<float*>(P.out) + o0 + 16 * n) = y;
+            }
+        }
+    } else {
+        // partial: running max in natural-log units as the combine expects
+        float* part = P.part + (((size_t)g * P.rows_pad + rr) * P.splits + split) * (D + 2);
+        if (hi == 0) {
+            part[0] = (mrun == -INFINITY) ? -INFINITY : mrun * 0.6931471805599453f;
+            part[1] = l;
+        }
+#pragma unroll
+        for (int n = 0; n < NB; ++n)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) part[2 + 16 * n + 4 * hi + r] = o[n][r];
+    }
+}
+
+// Combine the key splits of one (KV head, row): block = (row, KV head).
+// Thread t takes split t for the max M and the weight w_t = exp(m_t - M) (0
+// for a split that saw no key) and the denominator sum_t w_t l_t; then wave w
+// takes splits w, w + 4, ... for all head dims (lane + 64 j), loading up to 16
+// splits at once so their latencies overlap; the 4 waves' sums meet in LDS:
+// out = sum_s w_s acc_s / sum_s w_s l_s.
+template <int D>
+__global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams P) {
+    constexpr int ND = D / 64;  // dims per lane
+    constexpr int B = 16;       // splits loaded at once per wave
+    constexpr size_t STRIDE = D + 2;
+    static_assert(ATTN_MAX_SPLITS <= 256, "one thread per split");
+    __shared__ float w_s[256];
+    __shared__ float red[2][4];
+    __shared__ float sums[4][D];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int rr = blockIdx.x, g = blockIdx.y;
+    const int G = P.qh / P.kh, R = G * P.m;
+    if (rr >= R) return;  // (block-uniform)
+    const int h = g * G + rr / P.m, qr = rr % P.m;
+    const int S = P.splits;
+    const float* p0 = P.part + ((size_t)g * P.rows_pad + rr) * S * STRIDE;
+    const float m = tid < S ? p0[tid * STRIDE] : -INFINITY;
+    const float l = tid < S ? p0[tid * STRIDE + 1] : 0.0f;
+    float mx = group_max<64>(m);
+    if (lane == 0) red[0][wave] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+    const float w = (m == -INFINITY) ? 0.0f : __expf(m - mx);
+    w_s[tid] = w;
+    const float den = group_sum<64>(w * l);
+    if (lane == 0) red[1][wave] = den;
+    __syncthreads();
+    float num[ND];
+#pragma unroll
+    for (int d = 0; d < ND; ++d) num[d] = 0.0f;
+    for (int s0 = wave; s0 < S; s0 += 4 * B) {
+        float v[B][ND];
+#pragma unroll
+        for (int u = 0; u < B; ++u) {
+            const int sp = min(s0 + 4 * u, S - 1);
+#pragma unroll
+            for (int d = 0; d < ND; ++d) v[u][d] = p0[sp * STRIDE + 2 + lane + 64 * d];
+        }
+#pragma unroll
+        for (int u = 0; u < B; ++u) {
+            const int sp = s0 + 4 * u;
+            const float wi = sp < S ? w_s[sp] : 0.0f;
+#pragma unroll
+            for (int d = 0; d < ND; ++d) num[d] = __builtin_fmaf(wi, v[u][d], num[d]);
         }
     }
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int rr = row0 + 4 * hi + r;
-        if (rr >= R) continue;
-        const int h = g * G + rr / P.m, qr = rr % P.m;
-        if (P.splits == 1) {
-            const float inv = 1.0f / lrun[r];
-            const size_t o0 = ((size_t)h * P.m + qr) * D;
+    for (int d = 0; d < ND; ++d) sums[wave][lane + 64 * d] = num[d];
+    __syncthreads();
+    if (wave == 0) {
+        const float inv = 1.0f / ((red[1][0] + red[1][1]) + (red[1][2] + red[1][3]));
+        const size_t o = ((size_t)h * P.m + qr) * D + lane;
 #pragma unroll
-            for (int n = 0; n < NB; ++n) {
-                const float y = o[n][r] * inv;
-                if (P.out_f16)
-                    static_cast<__half*>(P.out)[o0 + 16 * n + lo] = __float2half_rn(y);
-                else
-                    static_cast<float*>(P.out)[o0 + 16 * n + lo] = y;
-            }
-        } else {
-            float* part = P.part + (((size_t)g * P.rows_pad + rr) * P.splits + split) * (D + 2);
-            if (lo == 0) {
-                part[0] = mrun[r];
-                part[1] = lrun[r];
-            }
-#pragma unroll
-            for (int n = 0; n < NB; ++n) part[2 + 16 * n + lo] = o[n][r];
+        for (int d = 0; d < ND; ++d) {
+            const int dd = lane + 64 * d;
+            const float y = ((sums[0][dd] + sums[1][dd]) + (sums[2][dd] + sums[3][dd])) * inv;
+            if (P.out_f16)
+                static_cast<__half*>(P.out)[o + 64 * d] = __float2half_rn(y);
+            else
+                static_cast<float*>(P.out)[o + 64 * d] = y;
         }
     }
 }
 
-// Combine the splits of one (KV head, row) for 64 of its dims: block = (row,
-// dim chunk), 256 threads = 64 dims x 4 groups of splits. The block takes the
-// max over the splits' maxima, the weights exp(m_s - M) into LDS and the
-// denominator sum_s w_s l_s, then each thread sums w_s * acc_s over its
-// group's splits (loads unrolled, independent) and the groups add in LDS.
-constexpr int ATTN_MAX_SPLITS = 256;
-
-__global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams P, int D) {
-    __shared__ float w_s[ATTN_MAX_SPLITS];
-    __shared__ float red[4];
-    __shared__ float sums[4][64];
-    const int rr = blockIdx.x, g = blockIdx.y, d0 = blockIdx.z * 64;
+// The same combine for few splits (at most 64) over many rows: one wave per
+// row, lane s holds split s's weight; the splits' accumulators are loaded 16
+// at a time (dims lane + 64 j) and each weight is broadcast from its lane.
+template <int D>
+__global__ __launch_bounds__(256) void attn_combine_rows_kernel(AttnParams P) {
+    constexpr int ND = D / 64;
+    constexpr int B = 16;
+    constexpr size_t STRIDE = D + 2;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int rr = blockIdx.x * 4 + wave, g = blockIdx.y;
     const int G = P.qh / P.kh, R = G * P.m;
-    if (rr >= R) return;  // (uniform over the block)
+    if (rr >= R) return;  // (wave-uniform; no barrier below)
     const int h = g * G + rr / P.m, qr = rr % P.m;
-    const float* p0 = P.part + (((size_t)g * P.rows_pad + rr) * P.splits) * (D + 2);
-    float mx = -INFINITY;
-    for (int s = tid; s < P.splits; s += 256) mx = fmaxf(mx, p0[(size_t)s * (D + 2)]);
-    mx = wave_max(mx);
-    if (lane == 0) red[wave] = mx;
-    __syncthreads();
-    const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    __syncthreads();
-    float den = 0.0f;
-    for (int s = tid; s < P.splits; s += 256) {
-        const float* ps = p0 + (size_t)s * (D + 2);
-        const float w = (ps[0] == -INFINITY) ? 0.0f : __expf(ps[0] - M);
-        w_s[s] = w;
-        den = __builtin_fmaf(w, ps[1], den);
+    const int S = P.splits;
+    const float* p0 = P.part + ((size_t)g * P.rows_pad + rr) * S * STRIDE;
+    const float m = lane < S ? p0[lane * STRIDE] : -INFINITY;
+    const float l = lane < S ? p0[lane * STRIDE + 1] : 0.0f;
+    const float mx = group_max<64>(m);
+    const float w = (m == -INFINITY) ? 0.0f : __expf(m - mx);
+    const float den = group_sum<64>(w * l);
+    float num[ND];
+#pragma unroll
+    for (int d = 0; d < ND; ++d) num[d] = 0.0f;
+    for (int s0 = 0; s0 < S; s0 += B) {
+        float v[B][ND];
+#pragma unroll
+        for (int u = 0; u < B; ++u) {
+            const int sp = min(s0 + u, S - 1);
+#pragma unroll
+            for (int d = 0; d < ND; ++d) v[u][d] = p0[sp * STRIDE + 2 + lane + 64 * d];
+        }
+#pragma unroll
+        for (int u = 0; u < B; ++u) {
+            // (lanes past S hold weight 0)
+            const float wi = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), s0 + u));
+#pragma unroll
+            for (int d = 0; d < ND; ++d) num[d] = __builtin_fmaf(wi, v[u][d], num[d]);
+        }
     }
-    den = group_sum<64>(den);
-    if (lane == 0) red[wave] = den;
-    __syncthreads();
-    const float inv = 1.0f / ((red[0] + red[1]) + (red[2] + red[3]));
-    const int dd = d0 + lane;  // (wave = group of splits s = wave + 4k)
-    float num = 0.0f;
-    if (dd < D) {
-#pragma unroll 8
-        for (int s = wave; s < P.splits; s += 4) num = __builtin_fmaf(w_s[s], p0[(size_t)s * (D + 2) + 2 + dd], num);
-    }
-    sums[wave][lane] = num;
-    __syncthreads();
-    if (wave == 0 && dd < D) {
-        const float y = ((sums[0][lane] + sums[1][lane]) + (sums[2][lane] + sums[3][lane])) * inv;
-        const size_t o = ((size_t)h * P.m + qr) * D + dd;
+    const float inv = 1.0f / den;
+    const size_t o = ((size_t)h * P.m + qr) * D + lane;
+#pragma unroll
+    for (int d = 0; d < ND; ++d) {
+        const float y = num[d] * inv;
         if (P.out_f16)
-            static_cast<__half*>(P.out)[o] = __float2half_rn(y);
+            static_cast<__half*>(P.out)[o + 64 * d] = __float2half_rn(y);
         else
-            static_cast<float*>(P.out)[o] = y;
+            static_cast<float*>(P.out)[o + 64 * d] = y;
     }
 }
 
@@ -586,17 +720,25 @@ struct AttnPlan {
 // of a 4-head group), else 16. Keys: enough splits that about 512 blocks run
 // (each split a whole number of 64-key tiles); with more than one split the
 // blocks write partials, at most 512 + row_tiles * kv_heads <= 1024 of them.
+// Override for measurement: HM_ATTN_BLOCKS (blocks the key splits aim at).
+static int attn_env(const char* name, int fallback) {
+    const char* v = std::getenv(name);
+    return v ? std::atoi(v) : fallback;
+}
+
 static AttnPlan plan_attention(const rk_npu_attention_f16_config& c, int rows, int len, int pos) {
     AttnPlan p;
     const int G = c.query_heads / c.kv_heads, R = G * rows;
     p.mfma = R >= 16 && (c.head_dim == 64 || c.head_dim == 128);
+    static const int env_blocks = attn_env("HM_ATTN_BLOCKS", 512);
     p.rt = p.mfma ? 64 : (R <= 4 ? 4 : 16);
     p.row_tiles = (R + p.rt - 1) / p.rt;
     p.key_end = (c.mask_mode == RK_NPU_ATTENTION_F16_CAUSAL) ? std::min(len, pos + rows) : len;
     const int kt = c.head_dim == 256 ? 32 : ATTN_KT;  // keys per tile of the kernel
     const int tiles = (p.key_end + kt - 1) / kt;
     const int base = p.row_tiles * c.kv_heads;
-    int want = base >= 512 ? 1 : (512 + base - 1) / base;
+    const int target = std::min(std::max(env_blocks, 64), 1024);
+    int want = base >= target ? 1 : (target + base - 1) / base;
     want = std::max(1, std::min(std::min(want, tiles), ATTN_MAX_SPLITS));
     const int tiles_per_split = (tiles + want - 1) / want;
     p.keys_per_split = tiles_per_split * kt;
@@ -645,10 +787,11 @@ static int enqueue_attention(AttnWork* w, AttnCache* c, const __half* q, int row
         launch_attn<DD, 4>(P, pl, cfg.kv_heads, s);                    \
     else                                                               \
         launch_attn<DD, 16>(P, pl, cfg.kv_heads, s);
+    const dim3 grid(pl.splits, pl.row_tiles, cfg.kv_heads);
     if (pl.mfma && D == 64) {
-        hipLaunchKernelGGL(attn_mfma_kernel<64>, dim3(pl.splits, pl.row_tiles, cfg.kv_heads), dim3(256), 0, s, P);
+        hipLaunchKernelGGL(attn_mfma_kernel<64>, grid, dim3(256), 0, s, P);
     } else if (pl.mfma && D == 128) {
-        hipLaunchKernelGGL(attn_mfma_kernel<128>, dim3(pl.splits, pl.row_tiles, cfg.kv_heads), dim3(256), 0, s, P);
+        hipLaunchKernelGGL(attn_mfma_kernel<128>, grid, dim3(256), 0, s, P);
     } else if (D == 64) {
         HM_ATTN(64)
     } else if (D == 128) {
@@ -659,7 +802,25 @@ static int enqueue_attention(AttnWork* w, AttnCache* c, const __half* q, int row
 #undef HM_ATTN
     if (pl.splits > 1) {
         const int G = cfg.query_heads / cfg.kv_heads;
-        hipLaunchKernelGGL(attn_combine_kernel, dim3(G * rows, cfg.kv_heads, (D + 63) / 64), dim3(256), 0, s, P, D);
+        // few splits: a wave per row; many: a block per row (measured: 8
+        // splits over 4096 rows 2 us faster by wave, 64 splits over 32 rows
+        // 14 us faster by block)
+        const bool by_wave = pl.splits <= 16;
+        const dim3 cgrid(by_wave ? (G * rows + 3) / 4 : G * rows, cfg.kv_heads);
+        if (by_wave) {
+            if (D == 64)
+                hipLaunchKernelGGL(attn_combine_rows_kernel<64>, cgrid, dim3(256), 0, s, P);
+            else if (D == 128)
+                hipLaunchKernelGGL(attn_combine_rows_kernel<128>, cgrid, dim3(256), 0, s, P);
+            else
+                hipLaunchKernelGGL(attn_combine_rows_kernel<256>, cgrid, dim3(256), 0, s, P);
+        } else if (D == 64) {
+            hipLaunchKernelGGL(attn_combine_kernel<64>, cgrid, dim3(256), 0, s, P);
+        } else if (D == 128) {
+            hipLaunchKernelGGL(attn_combine_kernel<128>, cgrid, dim3(256), 0, s, P);
+        } else {
+            hipLaunchKernelGGL(attn_combine_kernel<256>, cgrid, dim3(256), 0, s, P);
+        }
     }
     return hipGetLastError() == hipSuccess ? RK_NPU_OK : RK_NPU_ERR_DEVICE;
 }
