@@ -130,6 +130,39 @@ def test_bidirectional_gqa_matches_oracle(qh, kh, d):
         pos += rows
 
 
+@pytest.mark.parametrize("causal", [True, False])
+def test_growing_scores_match_oracle(causal):
+    """Keys whose magnitude grows along the sequence, so a row's running max
+    rises many times over the tiles of one key split (scaled scores up to
+    ~50, far past what unshifted fp16 weights hold). 32 query heads over 8
+    KV heads with 128 query rows over 2048 keys: the matrix-core path splits
+    the keys 8 ways, 4 tiles each, so its deferred rescaling runs inside a
+    split; then a 1-row decode step over the same cache."""
+    be = npu.Backend(npu.ModelOptions(chunk=128, context=2048))
+    qh, kh, d, length = 32, 8, 128, 2048
+    scale = d ** -0.5
+    att = be.attention(qh, kh, d, scale) if causal else be.noncausal_gqa(qh, kh, d)
+    rng = np.random.default_rng(9)
+    grow = (0.2 + np.arange(length) / 300.0)[:, None, None]
+    k_all = (rng.standard_normal((length, kh, d)) * grow).astype(np.float16)
+    v_all = rng.standard_normal((length, kh, d)).astype(np.float16)
+    prefix = length - 128
+    for i in range(0, prefix, 128):
+        att.append(k_all[i:i + 128].astype(np.float32), v_all[i:i + 128].astype(np.float32), 128, i)
+    for rows in (128, 1):
+        pos = att.info().length
+        if rows == 1:
+            att.truncate(pos - 1)
+            pos -= 1
+        print(f"growing scores causal={causal} rows={rows} position={pos}", flush=True)
+        q = (rng.standard_normal((rows, qh, d)) * 2.0).astype(np.float32)
+        out = np.empty((rows, qh, d), np.float32)
+        att.run(q, k_all[pos:pos + rows].astype(np.float32), v_all[pos:pos + rows].astype(np.float32), out, rows, pos)
+        want = oracle.attention(heads_major(q.astype(np.float16)), heads_major(k_all[:pos + rows]),
+                                heads_major(v_all[:pos + rows]), float(np.float32(scale)), pos, causal)
+        close(heads_major(out), want)
+
+
 def test_full_attention_f32_and_half():
     """FullAttention.run_full / run_full_half (src/npu/attention.rs:45-205):
     the fp16 output is the f32 result rounded to nearest."""
