@@ -26,6 +26,11 @@ HIPCC_FLAGS = [
     "-Wall",
 ]
 
+# Per-source additions. attention.hip: matrix-core results in VGPRs, so the
+# attention kernel's output accumulators (rescaled on the VALU between
+# products) are not copied to and from accumulation registers every tile.
+EXTRA_FLAGS = {"attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
 
 def hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", "hipcc"):
@@ -42,7 +47,7 @@ def build(verbose: bool = False, jobs: int = 2) -> str:
     procs = []
     for src in SOURCES:
         obj = os.path.join(build_dir, os.path.splitext(src)[0] + ".o")
-        cmd = [hipcc(), *HIPCC_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+        cmd = [hipcc(), *HIPCC_FLAGS, *EXTRA_FLAGS.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj]
         if verbose:
             print(" ".join(cmd), flush=True)
         procs.append((cmd, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)))

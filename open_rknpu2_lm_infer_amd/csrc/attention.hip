@@ -275,7 +275,7 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnParams P) {
     typedef float f4 __attribute__((ext_vector_type(4)));
     typedef unsigned u2 __attribute__((ext_vector_type(2)));
     constexpr int KT = ATTN_KT, KS = D / 32, NB = D / 16;
-    constexpr int KP = D + 8, VP = KT + 8;
+    constexpr int KP = D + 8, VP = KT + 4;  // row pads: fragment reads of 16 lanes hit distinct banks
     constexpr int KPIECES = KT * (D / 8);        // 16-byte K pieces per tile
     constexpr int VPIECES = (KT / 4) * (D / 8);  // 4 keys x 8 dims V pieces per tile
     constexpr int KPT = KPIECES / 256;
@@ -307,7 +307,7 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnParams P) {
     open = min(open, __shfl_xor(open, 2));
     open = min(open, __shfl_xor(open, 4));
     open = min(open, __shfl_xor(open, 8));
-    open = min(open, k1);
+    open = __builtin_amdgcn_readfirstlane(min(open, k1));  // (uniform: a scalar branch below)
     h8 qf[KS];
     {
         const __half* qp = P.q + ((size_t)(g * G + (row_ok ? rr / P.m : 0)) * P.m + (row_ok ? rr % P.m : 0)) * D;
@@ -321,21 +321,38 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnParams P) {
     // 4 (tid % 16)..+3, dims 8 (tid / 16)..+7
     const bool vthread = tid < VPIECES;
     const int vj = tid & 15, vc = tid >> 4;
+    // byte offsets within a tile (the tile base is uniform): K piece t, V row t
+    unsigned koff[KPT], voff[4];
+#pragma unroll
+    for (int t = 0; t < KPT; ++t) {
+        const int i = tid + 256 * t;
+        koff[t] = (unsigned)((i / (D / 8)) * D + (i % (D / 8)) * 8) * 2u;
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) voff[t] = (unsigned)((4 * vj + t) * D + vc * 8) * 2u;
     v4u kr[KPT], vr[4];
     auto issue = [&](int kb) {
-        const bool full = kb + KT <= k1;
+        const char* kt = reinterpret_cast<const char*>(kbase + (size_t)kb * D);
+        const char* vtp = reinterpret_cast<const char*>(vbase + (size_t)kb * D);
+        if (kb + KT <= k1) {  // (uniform) whole tile inside the split
 #pragma unroll
-        for (int t = 0; t < KPT; ++t) {
-            const int i = tid + 256 * t;
-            const int key = kb + i / (D / 8);
-            kr[t] = *reinterpret_cast<const v4u*>(
-                kbase + ((full || key < k1) ? (size_t)key * D + (i % (D / 8)) * 8 : 0));
-        }
-        if (vthread) {
+            for (int t = 0; t < KPT; ++t) kr[t] = *reinterpret_cast<const v4u*>(kt + koff[t]);
+            if (vthread) {
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const int key = kb + 4 * vj + t;
-                vr[t] = *reinterpret_cast<const v4u*>(vbase + ((full || key < k1) ? (size_t)key * D + vc * 8 : 0));
+                for (int t = 0; t < 4; ++t) vr[t] = *reinterpret_cast<const v4u*>(vtp + voff[t]);
+            }
+        } else {  // keys past the split read the tile's first row (zeroed in store)
+#pragma unroll
+            for (int t = 0; t < KPT; ++t) {
+                const int key = kb + (tid + 256 * t) / (D / 8);
+                kr[t] = *reinterpret_cast<const v4u*>(kt + (key < k1 ? koff[t] : 0u));
+            }
+            if (vthread) {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const int key = kb + 4 * vj + t;
+                    vr[t] = *reinterpret_cast<const v4u*>(vtp + (key < k1 ? voff[t] : 0u));
+                }
             }
         }
     };
@@ -392,7 +409,7 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnParams P) {
             for (int k = 0; k < KS; ++k)
                 sacc[cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[k], qf[k], sacc[cb], 0, 0, 0);
         }
-        if (kb + KT > open) {  // (wave-uniform) the tile crosses a mask
+        if (__builtin_expect(kb + KT > open, 0)) {  // (uniform) the tile crosses a mask
 #pragma unroll
             for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
@@ -409,7 +426,7 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnParams P) {
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
         const float tm = tmax * c;
         const bool grow = tm > mrun + ATTN_LAZY;
-        if (__any(grow)) {  // (wave-uniform)
+        if (__builtin_expect(__builtin_amdgcn_ballot_w64(grow) != 0, 0)) {  // (uniform, rare after the first tile)
             float alpha = 1.0f;
             if (grow) {
                 alpha = __builtin_amdgcn_exp2f(mrun - tm);  // (0 from -inf)
