@@ -163,11 +163,13 @@ def test_growing_scores_match_oracle(causal):
         close(heads_major(out), want)
 
 
-def test_full_attention_f32_and_half():
+@pytest.mark.parametrize("heads,d,rows", [(4, 64, 100), (4, 64, 48), (2, 128, 40)])
+def test_full_attention_f32_and_half(heads, d, rows):
     """FullAttention.run_full / run_full_half (src/npu/attention.rs:45-205):
-    the fp16 output is the f32 result rounded to nearest."""
+    the fp16 output is the f32 result rounded to nearest. 100 keys take two
+    key splits and the combine; 40-48 keys fit one split, where the
+    matrix-core kernel writes both outputs itself."""
     be = npu.Backend(npu.ModelOptions(chunk=32, context=512))
-    heads, d, rows = 4, 64, 100
     fa = be.full_attention(heads, d, rows)
     rng = np.random.default_rng(6)
     q, k, v = (rng.standard_normal((rows, heads, d)).astype(np.float32) for _ in range(3))
