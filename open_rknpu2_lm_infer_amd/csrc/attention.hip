@@ -397,18 +397,22 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnParams P) {
         store(kb);
         __syncthreads();
         if (kb + KT < k1) issue(kb + KT);
+        // (k outermost: the 4 key blocks' products are independent, so they
+        // issue back to back instead of waiting on each other)
         f4 sacc[4];
+        h8 ka[4][KS];
 #pragma unroll
-        for (int cb = 0; cb < 4; ++cb) {
-            h8 a[KS];
+        for (int k = 0; k < KS; ++k)
 #pragma unroll
-            for (int k = 0; k < KS; ++k)
-                a[k] = __builtin_bit_cast(h8, *reinterpret_cast<const v4u*>(&ks[cb * 16 + lo][32 * k + 8 * hi]));
-            sacc[cb] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+            for (int cb = 0; cb < 4; ++cb)
+                ka[cb][k] = __builtin_bit_cast(h8, *reinterpret_cast<const v4u*>(&ks[cb * 16 + lo][32 * k + 8 * hi]));
 #pragma unroll
-            for (int k = 0; k < KS; ++k)
-                sacc[cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[k], qf[k], sacc[cb], 0, 0, 0);
-        }
+        for (int cb = 0; cb < 4; ++cb) sacc[cb] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int k = 0; k < KS; ++k)
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb)
+                sacc[cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[cb][k], qf[k], sacc[cb], 0, 0, 0);
         if (__builtin_expect(kb + KT > open, 0)) {  // (uniform) the tile crosses a mask
 #pragma unroll
             for (int cb = 0; cb < 4; ++cb)
@@ -451,14 +455,17 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnParams P) {
             }
         }
 #pragma unroll
-        for (int n = 0; n < NB; ++n)
+        for (int k = 0; k < 2; ++k) {  // (k outermost: the NB products are independent)
+            h8 va[NB];
 #pragma unroll
-            for (int k = 0; k < 2; ++k) {
+            for (int n = 0; n < NB; ++n) {
                 const u2 a0 = *reinterpret_cast<const u2*>(&vt[16 * n + lo][32 * k + 4 * hi]);
                 const u2 a1 = *reinterpret_cast<const u2*>(&vt[16 * n + lo][32 * k + 16 + 4 * hi]);
-                const h8 a = __builtin_bit_cast(h8, v4u{a0[0], a0[1], a1[0], a1[1]});
-                o[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb[k], o[n], 0, 0, 0);
+                va[n] = __builtin_bit_cast(h8, v4u{a0[0], a0[1], a1[0], a1[1]});
             }
+#pragma unroll
+            for (int n = 0; n < NB; ++n) o[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[n], pb[k], o[n], 0, 0, 0);
+        }
     }
     float l = lpart;
     l += __shfl_xor(l, 16);
@@ -581,6 +588,15 @@ __global__ __launch_bounds__(256) void attn_combine_rows_kernel(AttnParams P) {
     const int h = g * G + rr / P.m, qr = rr % P.m;
     const int S = P.splits;
     const float* p0 = P.part + ((size_t)g * P.rows_pad + rr) * S * STRIDE;
+    // the first 16 splits' accumulators are loaded together with the maxima
+    // and sums (one memory round trip for up to 16 splits)
+    float v[B][ND];
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+        const int sp = min(u, S - 1);
+#pragma unroll
+        for (int d = 0; d < ND; ++d) v[u][d] = p0[sp * STRIDE + 2 + lane + 64 * d];
+    }
     const float m = lane < S ? p0[lane * STRIDE] : -INFINITY;
     const float l = lane < S ? p0[lane * STRIDE + 1] : 0.0f;
     const float mx = group_max<64>(m);
@@ -590,12 +606,13 @@ __global__ __launch_bounds__(256) void attn_combine_rows_kernel(AttnParams P) {
 #pragma unroll
     for (int d = 0; d < ND; ++d) num[d] = 0.0f;
     for (int s0 = 0; s0 < S; s0 += B) {
-        float v[B][ND];
+        if (s0 > 0) {
 #pragma unroll
-        for (int u = 0; u < B; ++u) {
-            const int sp = min(s0 + u, S - 1);
+            for (int u = 0; u < B; ++u) {
+                const int sp = min(s0 + u, S - 1);
 #pragma unroll
-            for (int d = 0; d < ND; ++d) v[u][d] = p0[sp * STRIDE + 2 + lane + 64 * d];
+                for (int d = 0; d < ND; ++d) v[u][d] = p0[sp * STRIDE + 2 + lane + 64 * d];
+            }
         }
 #pragma unroll
         for (int u = 0; u < B; ++u) {
