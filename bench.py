@@ -321,7 +321,7 @@ def run_prefill(torch, ctx, rows, steps, warmup):
            "frac_of_int8_peak": round(ops / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4),
            "ms_eager": round(ms_eager, 3), "ms_graph": round(ms_graph, 3), "graph_matches_eager": ok,
            "roofline": roofline(work / (per_us * 1e-6) / 1e12, "mfma",
-                                f"gemm_kernel<256,256,2,4,W4,SwiGLU> gate_up 2560x19456, M={rows}", per_us, work,
+                                f"gemm_kernel<128,128,2,2,W4,SwiGLU> gate_up 2560x19456, M={rows}", per_us, work,
                                 launches, "graph of 36 back-to-back quantization + GEMM launch pairs, HIP events "
                                 "on the replay stream"),
            "vendor_ref": vendor_int8_gemm(torch, rows, H, 2 * F)}

@@ -314,9 +314,15 @@ constexpr int GEMV_MAX_LDS = 60 * 1024;
 // tile 32x64) leads, since more, smaller tiles keep every CU busy (M = 512:
 // 36 us vs 47 us for 128x128 and 110 us for 256x256 on the 9728x2560 down
 // projection); up to M = 2048 the 4-wave 128x128 tile (the 256x256 tile
-// leaves CUs idle on N = 2560); above that the 8-wave 256x256 tile, 5% ahead
-// of 128x128 over the whole M = 4096 projection set. Rows <= 32 take the
-// 32x128 tile.
+// leaves CUs idle on N = 2560). Above 2048 rows the 128x128 tile (two blocks
+// per CU, one's epilogue under the other's main loop) still leads on most
+// shapes (M = 4096: qkv 2560x6144 104 -> 97 us, gate_up 2560x19456 + SwiGLU
+// 247 -> 233 us, o 4096x2560 75 -> 74 us; M = 3072: every projection); the
+// 8-wave 256x256 tile wins where its higher reuse is not paid for by idle
+// CUs: very wide outputs (lm_head 2560x151936 at M = 4096: 2045 -> 1864 us)
+// and long K once the 128x128 tiles overflow one round of two per CU
+// (9728x2560 down at M = 4096: 176 -> 165 us; at M = 3072, 480 tiles fit a
+// round and 128x128 wins, 148 -> 120 us). Rows <= 32 take the 32x128 tile.
 // Split-K (two launches: partials, then sum + epilogue) when the tiles leave
 // CUs idle and K is long: measured on 9728x2560 it takes M=512 from 45 to
 // 38 us (3 pieces) and M=64 from 38 to 22 us (6 pieces); with K <= 4096 or
@@ -344,7 +350,13 @@ static Plan plan_gemm(int rows, const Geometry& g, int variant) {
         if (forced >= 0 && forced <= 4)
             v = forced;
         else
-            v = rows <= 32 ? V32x128 : rows <= 1024 ? V64x128 : rows <= 2048 ? V128x128 : V256x256;
+            v = rows <= 32 ? V32x128 : rows <= 1024 ? V64x128 : V128x128;
+        if (v == V128x128 && rows > 2048 && forced < 0) {
+            const int cus = device_cus();
+            const long long t256 = (long long)((rows + 255) / 256) * (g.N_pad / 256);
+            const long long t128 = (long long)((rows + 127) / 128) * (g.N_pad / 128);
+            if (t256 >= 8LL * cus || (g.K_pad >= 8192 && t128 > 2LL * cus)) v = V256x256;
+        }
     }
     p.variant = v;
     p.bm = kBM[v];

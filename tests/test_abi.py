@@ -107,9 +107,10 @@ def test_plans():
     # a K too long for the GEMV's quantized rows in LDS (8 x 9728 bytes) takes the GEMM
     assert L.rk_npu_hip_linear_plan(8, 9728, 2560, 8, ctypes.byref(plan)) == 0
     assert (plan.kind, plan.block_m, plan.block_n) == (1, 32, 128)
-    # 64x128 tiles up to 1024 rows, 128x128 up to 2048, then 256x256; K split
-    # in pieces when the tiles leave CUs idle and K is long (256 CUs assumed
-    # without a GPU)
+    # 64x128 tiles up to 1024 rows, then 128x128; above 2048 rows 256x256 for
+    # very wide outputs and for long K once 128x128 tiles overflow two per CU;
+    # K split in pieces when the tiles leave CUs idle and K is long (256 CUs
+    # assumed without a GPU)
     assert L.rk_npu_hip_linear_plan(512, 9728, 2560, 8, ctypes.byref(plan)) == 0
     assert (plan.kind, plan.block_m, plan.block_n, plan.k_splits, plan.grid) == (1, 64, 128, 3, 8 * 20 * 3)
     assert L.rk_npu_hip_linear_plan(512, 4096, 2560, 8, ctypes.byref(plan)) == 0
@@ -117,7 +118,13 @@ def test_plans():
     assert L.rk_npu_hip_linear_plan(2048, 9728, 2560, 8, ctypes.byref(plan)) == 0
     assert (plan.kind, plan.block_m, plan.block_n, plan.k_splits, plan.grid) == (1, 128, 128, 1, 16 * 20)
     assert L.rk_npu_hip_linear_plan(4096, 2560, 9728, 8, ctypes.byref(plan)) == 0
+    assert (plan.kind, plan.block_m, plan.block_n, plan.k_splits) == (1, 128, 128, 1)
+    assert L.rk_npu_hip_linear_plan(4096, 2560, 151936, 8, ctypes.byref(plan)) == 0
     assert (plan.kind, plan.block_m, plan.block_n, plan.k_splits) == (1, 256, 256, 1)
+    assert L.rk_npu_hip_linear_plan(4096, 9728, 2560, 8, ctypes.byref(plan)) == 0
+    assert (plan.kind, plan.block_m, plan.block_n, plan.k_splits, plan.grid) == (1, 256, 256, 1, 16 * 10)
+    assert L.rk_npu_hip_linear_plan(3072, 9728, 2560, 8, ctypes.byref(plan)) == 0
+    assert (plan.kind, plan.block_m, plan.block_n, plan.k_splits, plan.grid) == (1, 128, 128, 1, 24 * 20)
     assert L.rk_npu_hip_linear_plan(0, 2560, 9728, 8, ctypes.byref(plan)) == F.RK_NPU_ERR_PARAM
 
 

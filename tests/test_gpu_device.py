@@ -43,9 +43,12 @@ def test_device_linear_matches_oracle_f32_and_f16(ctx, bits, rows):
 
 
 @pytest.mark.parametrize("bits", [4, 8])
-@pytest.mark.parametrize("rows", [1100, 2100])
-def test_device_linear_large_row_tiles(ctx, bits, rows):
-    """Row counts that select the 128x128 (<= 2048 rows) and 256x256 tiles."""
+@pytest.mark.parametrize("rows,variant", [(1100, None), (2100, None), (2100, "0"), (4100, "0")])
+def test_device_linear_large_row_tiles(ctx, bits, rows, variant, monkeypatch):
+    """Row counts that select the 128x128 tile, and the 256x256 tile (chosen by
+    the plan for very wide outputs or long K; forced here at a small shape)."""
+    if variant is not None:
+        monkeypatch.setenv("HM_GEMM_VARIANT", variant)
     k, n = 640, 768
     codes, scales = R.weights(5, f"dl{bits}", bits, k, n)
     w = ctx.weights(bits, dev(codes), dev(scales))
