@@ -8,8 +8,9 @@ activations resident in HBM. value = algorithmic bytes / wall time (GB/s).
 
 Secondary workloads (same JSON line, "secondary"): M=4 decode, the M=4096
 W8A8/W4A8 prefill projection set x36 + lm_head (int8 TOPS), the M=512 FFN
-block x36, the M=128 W8A8 up projection, and the 35B-A3B-class MoE at T=512
-and T=1.
+block x36, the M=128 W8A8 up projection, the 35B-A3B-class MoE at T=512
+and T=1, the attention lines, and the PCIe-inclusive rates of the reference's
+host-buffer signatures (decode set and M=128 up projection).
 
 Timing (every workload): the step runs eagerly (host launches between two
 synchronizations) and as a HIP graph replay (checked bit-exact against eager
@@ -396,6 +397,70 @@ def run_up128(torch, ctx, steps, warmup, rows=128):
             "gbs": round(lin_bytes(8, H, F, rows) / (ms * 1e-3) / 1e9, 1)}
 
 
+def run_host_abi(layers=4, reps=20):
+    """The reference's own host-buffer signatures, through the host mirror of
+    src/npu.rs: rk_npu_w4a8_run_f32 / rk_npu_w4a8_run_swiglu_f32 (decode set,
+    M=1, `layers` distinct layers, the f32 SwiGLU middle handed back to the
+    host and into the down projection as the reference's callers do) and
+    rk_npu_f32i8f32_run_dynamic (W8A8 M=128 up projection). A and C are host
+    f32 buffers copied in and out before each call returns, so these rates
+    include PCIe and the per-call synchronization; they are reported beside
+    the HBM-resident lines, never as the headline value."""
+    import numpy as np
+    from open_rknpu2_lm_infer_amd import npu
+    g = np.random.default_rng(0x5EED0001)
+    backend = npu.Backend(npu.ModelOptions(chunk=256))
+
+    def qm(bits, k, n):
+        lo, hi = (-8, 8) if bits == 4 else (-127, 128)
+        return npu.QuantMatrix(bits, k, n, g.integers(lo, hi, size=(k, n), dtype=np.int8),
+                               g.uniform(0.001, 0.01, n).astype(np.float32))
+
+    shapes = (("qkv", H, Q + 2 * KV), ("o", Q, H), ("gate_up", H, 2 * F), ("down", F, H))
+    lay = [{name: backend.load(qm(4, k, n)) for name, k, n in shapes} for _ in range(layers)]
+    x = g.standard_normal((1, H)).astype(np.float16).astype(np.float32)
+    xo = g.standard_normal((1, Q)).astype(np.float16).astype(np.float32)
+    y_qkv, y_o = np.empty((1, Q + 2 * KV), np.float32), np.empty((1, H), np.float32)
+    mid, y_ffn = np.empty((1, F), np.float32), np.empty((1, H), np.float32)
+
+    def step():
+        for L in lay:
+            L["qkv"].run(x, y_qkv, 1)
+            L["o"].run(xo, y_o, 1)
+            assert L["gate_up"].run_swiglu(x, mid, 1)
+            L["down"].run(mid, y_ffn, 1)
+
+    for _ in range(3):
+        step()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        step()
+    us_layer = (time.perf_counter() - t0) * 1e6 / (reps * layers)
+    bytes_layer = sum(lin_bytes(4, k, n, 1) for _, k, n in shapes)
+    del lay
+    up = backend.load(qm(8, H, F))
+    xu = g.standard_normal((128, H)).astype(np.float32)
+    xu[:, g.choice(H, math.ceil(0.005 * H), replace=False)] *= 20.0
+    xu = xu.astype(np.float16).astype(np.float32)
+    yu = np.empty((128, F), np.float32)
+    for _ in range(3):
+        up.run(xu, yu, 128)
+    t0 = time.perf_counter()
+    for _ in range(reps * 5):
+        up.run(xu, yu, 128)
+    us_up = (time.perf_counter() - t0) * 1e6 / (reps * 5)
+    res = [{"workload": f"host-buffer C ABI (rk_npu_w4a8_run_f32 / _run_swiglu_f32, f32 A and C in host memory): "
+                        f"decode M=1 W4A8 set, {layers} layers",
+            "value": round(bytes_layer / (us_layer * 1e-6) / 1e9, 1), "unit": "GB/s", "us_per_layer": round(us_layer, 2),
+            "note": "PCIe-inclusive, one synchronization per call"},
+           {"workload": "host-buffer C ABI (rk_npu_f32i8f32_run_dynamic): W8A8 linear M=128 K=2560 N=9728",
+            "value": round(2.0 * 128 * H * F / (us_up * 1e-6) / 1e12, 2), "unit": "TOPS", "us_per_call": round(us_up, 2),
+            "note": "PCIe-inclusive: 1.3 MB of f32 A in, 5.0 MB of f32 C out per call"}]
+    log(f"[bench] host ABI: {res[0]['value']} GB/s decode ({us_layer:.1f} us/layer), "
+        f"{res[1]['value']} TOPS up M=128 ({us_up:.1f} us/call)")
+    return res
+
+
 def run_moe(torch, ctx, steps, warmup, tokens_list=(512, 1)):
     """Config 4: hidden 2048, 128 experts, top-8, I=768, routed W4 gate_up +
     W8 down; shared W8 FFN of intermediate 2048 through the dense path."""
@@ -572,7 +637,7 @@ def main():
     ap.add_argument("--primary-only", action="store_true", help="skip the secondary workloads")
     ap.add_argument("--decode-rows", type=int, default=1,
                     help="rows of the primary decode line (1 is the metric's configuration)")
-    ap.add_argument("--only", choices=["prefill", "ffn512", "up128", "moe", "attention"],
+    ap.add_argument("--only", choices=["prefill", "ffn512", "up128", "moe", "attention", "host"],
                     help="run one secondary workload alone and print its result (for profiling)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only run the workload of the FETCH_SIZE / WRITE_SIZE counter runs")
@@ -593,7 +658,8 @@ def main():
                "ffn512": lambda: run_ffn512(torch, ctx, steps, 2),
                "up128": lambda: run_up128(torch, ctx, args.steps, args.warmup),
                "moe": lambda: run_moe(torch, ctx, steps, 2),
-               "attention": lambda: run_attention(torch, ctx, steps)}[args.only]()
+               "attention": lambda: run_attention(torch, ctx, steps),
+               "host": lambda: run_host_abi()}[args.only]()
         print(json.dumps(res), flush=True)
         return
     primary = run_decode(torch, ctx, args.decode_rows, args.steps, args.warmup, not args.no_cpu_baseline)
@@ -606,6 +672,7 @@ def main():
         secondary.append(run_prefill(torch, ctx, 4096, max(4, args.steps // 2), 2))
         secondary.append(run_ffn512(torch, ctx, max(4, args.steps // 2), 2))
         secondary.append(run_up128(torch, ctx, args.steps, args.warmup))
+        secondary.extend(run_host_abi())
         secondary.extend(run_moe(torch, ctx, max(4, args.steps // 2), 2))
         secondary.extend(run_attention(torch, ctx, max(4, args.steps // 2)))
     for s in secondary:

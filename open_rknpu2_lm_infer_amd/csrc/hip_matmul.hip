@@ -434,6 +434,8 @@ Workspace* workspace_create(Domain* d, int bits, int M, int K, int N) {
     ws->domain = d;
     ws->busy.store(false);
     ws->stream = nullptr;
+    ws->host_stage = nullptr;
+    ws->host_stage_bytes = 0;
     const WsLayout L = ws_layout(ws->g, M);
     ws->bytes = L.total;
     uint8_t* base = static_cast<uint8_t*>(domain_alloc(d, L.total));
@@ -479,6 +481,7 @@ void workspace_destroy(Workspace* ws) {
         (void)hipStreamDestroy(ws->stream);
     }
     domain_free(ws->domain, ws->a_f32, ws->bytes);
+    if (ws->host_stage) (void)hipHostFree(ws->host_stage);
     if (ws->magic == MAGIC_WS8)
         delete static_cast<rk_npu_matmul_workspace*>(ws);
     else
@@ -897,6 +900,55 @@ int enqueue_ffn(Workspace* gws, const Weights* gw, Workspace* dws, const Weights
     return rc;
 }
 
+// Pinned staging for the host-buffer calls. Copies between pageable caller
+// memory and the device go through the runtime's own staging, which costs
+// tens of microseconds per call at decode sizes (a few KB); the workspace
+// instead keeps one pinned buffer, allocated on the first host call, that the
+// caller's A is copied into and C out of by the CPU. Transfers above the cap
+// (and a failed pinned allocation) keep the direct pageable copies.
+constexpr size_t HOST_STAGE_CAP = 8u << 20;
+
+float* host_stage(Workspace* ws, size_t bytes) {
+    if (bytes == 0 || bytes > HOST_STAGE_CAP) return nullptr;
+    if (ws->host_stage_bytes < bytes) {
+        if (ws->host_stage) (void)hipHostFree(ws->host_stage);
+        ws->host_stage = nullptr;
+        ws->host_stage_bytes = 0;
+        const size_t want = std::min(HOST_STAGE_CAP, std::max(bytes, (size_t)64 << 10));
+        if (hipHostMalloc(&ws->host_stage, want, hipHostMallocDefault) != hipSuccess) {
+            ws->host_stage = nullptr;
+            (void)hipGetLastError();
+            return nullptr;
+        }
+        ws->host_stage_bytes = want;
+    }
+    return static_cast<float*>(ws->host_stage);
+}
+
+// Host A -> device through the stage `st` (sized for the whole call by the
+// caller beforehand, so it is never reallocated under a pending copy), or
+// directly when there is none. The stream orders the upload before any later
+// download into the same stage.
+static bool upload_host(float* st, float* dst, const float* A, size_t bytes, hipStream_t s) {
+    if (st) {
+        std::memcpy(st, A, bytes);
+        return hipMemcpyAsync(dst, st, bytes, hipMemcpyHostToDevice, s) == hipSuccess;
+    }
+    return hipMemcpyAsync(dst, A, bytes, hipMemcpyHostToDevice, s) == hipSuccess;
+}
+
+// Device -> host C (through the stage when there is one), then synchronize.
+static bool download_host(float* st, float* C, const float* src, size_t bytes, hipStream_t s) {
+    if (st) {
+        if (hipMemcpyAsync(st, src, bytes, hipMemcpyDeviceToHost, s) != hipSuccess ||
+            hipStreamSynchronize(s) != hipSuccess)
+            return false;
+        std::memcpy(C, st, bytes);
+        return true;
+    }
+    return hipMemcpyAsync(C, src, bytes, hipMemcpyDeviceToHost, s) == hipSuccess && hipStreamSynchronize(s) == hipSuccess;
+}
+
 }  // namespace hm
 
 using namespace hm;
@@ -1095,8 +1147,11 @@ static int run_host(Workspace* ws, const Weights* w, const float* A, float* C, i
     if (hipSetDevice(device_of(ws->domain)) != hipSuccess) return RK_NPU_ERR_DEVICE;
     const int M = ws->M, K = w->g.K, N = w->g.N;
     const int width = epi == EPI_PLAIN ? N : N / 2;
-    if (hipMemcpyAsync(ws->a_f32, A, (size_t)M * K * 4, hipMemcpyHostToDevice, ws->stream) != hipSuccess)
+    float* st = host_stage(ws, std::max((size_t)M * K * 4, (size_t)M * width * 4));
+    if (!upload_host(st, ws->a_f32, A, (size_t)M * K * 4, ws->stream)) {
+        (void)hipStreamSynchronize(ws->stream);
         return RK_NPU_ERR_DEVICE;
+    }
     const double t1 = now_us();
     int rc = enqueue_linear(ws, w, ws->a_f32, DT_F32, K, M, QUANT_DENSE, RowMax{nullptr, 0}, ws->c_f32, DT_F32,
                             width, epi, nullptr, ws->stream);
@@ -1106,9 +1161,7 @@ static int run_host(Workspace* ws, const Weights* w, const float* A, float* C, i
     }
     if (timings && hipStreamSynchronize(ws->stream) != hipSuccess) return RK_NPU_ERR_DEVICE;
     const double t2 = now_us();
-    if (hipMemcpyAsync(C, ws->c_f32, (size_t)M * width * 4, hipMemcpyDeviceToHost, ws->stream) != hipSuccess ||
-        hipStreamSynchronize(ws->stream) != hipSuccess)
-        return RK_NPU_ERR_DEVICE;
+    if (!download_host(st, C, ws->c_f32, (size_t)M * width * 4, ws->stream)) return RK_NPU_ERR_DEVICE;
     if (timings) {
         const double t3 = now_us();
         timings->upload_us = t1 - t0;
@@ -1236,8 +1289,12 @@ int rk_npu_w4a8_run_ffn_f32(rk_npu_w4a8_workspace* gate_up_workspace, const rk_n
     if (hipSetDevice(device_of(gws->domain)) != hipSuccess) return RK_NPU_ERR_DEVICE;
     const int M = gws->M, H = gw->g.K;
     hipStream_t s = gws->stream;
-    if (hipMemcpyAsync(gws->a_f32, A, (size_t)M * H * 4, hipMemcpyHostToDevice, s) != hipSuccess)
+    float* st_in = host_stage(gws, (size_t)M * H * 4);
+    float* st_out = host_stage(dws, (size_t)M * H * 4);
+    if (!upload_host(st_in, gws->a_f32, A, (size_t)M * H * 4, s)) {
+        (void)hipStreamSynchronize(s);
         return RK_NPU_ERR_DEVICE;
+    }
     const double t1 = now_us();
     rc = enqueue_ffn(gws, gw, dws, dw, gws->a_f32, DT_F32, dws->c_f32, DT_F32, M, QUANT_DENSE, s);
     if (rc != RK_NPU_OK) {
@@ -1246,9 +1303,7 @@ int rk_npu_w4a8_run_ffn_f32(rk_npu_w4a8_workspace* gate_up_workspace, const rk_n
     }
     if (timings && hipStreamSynchronize(s) != hipSuccess) return RK_NPU_ERR_DEVICE;
     const double t2 = now_us();
-    if (hipMemcpyAsync(C, dws->c_f32, (size_t)M * H * 4, hipMemcpyDeviceToHost, s) != hipSuccess ||
-        hipStreamSynchronize(s) != hipSuccess)
-        return RK_NPU_ERR_DEVICE;
+    if (!download_host(st_out, C, dws->c_f32, (size_t)M * H * 4, s)) return RK_NPU_ERR_DEVICE;
     if (timings) {
         const double t3 = now_us();
         timings->upload_us = t1 - t0;

@@ -640,10 +640,27 @@ int rk_npu_moe_w8_run_f32(rk_npu_moe_w8_workspace* workspace, const rk_npu_moe_w
     if (hipSetDevice(device_of(ws->domain)) != hipSuccess) return RK_NPU_ERR_DEVICE;
     hipStream_t s = ws->stream;
     float* x = ws->xws->a_f32;
-    if (hipMemcpyAsync(x, input, (size_t)rows * ws->h * 4, hipMemcpyHostToDevice, s) != hipSuccess ||
-        hipMemcpyAsync(ws->ids, ids, (size_t)A * 4, hipMemcpyHostToDevice, s) != hipSuccess ||
-        hipMemcpyAsync(ws->routes, routes, (size_t)A * 4, hipMemcpyHostToDevice, s) != hipSuccess)
+    // Inputs (rows, ids, routes) and later the output pass through the input
+    // workspace's pinned stage when they fit it, else straight from pageable memory.
+    const size_t xb = (size_t)rows * ws->h * 4, ab = (size_t)A * 4;
+    uint8_t* st = reinterpret_cast<uint8_t*>(host_stage(ws->xws, xb + 2 * ab));
+    const void* src_x = input;
+    const void* src_ids = ids;
+    const void* src_routes = routes;
+    if (st) {
+        std::memcpy(st, input, xb);
+        std::memcpy(st + xb, ids, ab);
+        std::memcpy(st + xb + ab, routes, ab);
+        src_x = st;
+        src_ids = st + xb;
+        src_routes = st + xb + ab;
+    }
+    if (hipMemcpyAsync(x, src_x, xb, hipMemcpyHostToDevice, s) != hipSuccess ||
+        hipMemcpyAsync(ws->ids, src_ids, ab, hipMemcpyHostToDevice, s) != hipSuccess ||
+        hipMemcpyAsync(ws->routes, src_routes, ab, hipMemcpyHostToDevice, s) != hipSuccess) {
+        (void)hipStreamSynchronize(s);
         return RK_NPU_ERR_DEVICE;
+    }
     const double t1 = now_us();
     int rc = enqueue_moe(ws, weights, rows, x, ws->ids, ws->routes, ws->out, s);
     if (rc != RK_NPU_OK) {
@@ -652,9 +669,11 @@ int rk_npu_moe_w8_run_f32(rk_npu_moe_w8_workspace* workspace, const rk_npu_moe_w
     }
     if (timings && hipStreamSynchronize(s) != hipSuccess) return RK_NPU_ERR_DEVICE;
     const double t2 = now_us();
-    if (hipMemcpyAsync(output, ws->out, (size_t)rows * ws->h * 4, hipMemcpyDeviceToHost, s) != hipSuccess ||
+    if (hipMemcpyAsync(st ? static_cast<void*>(st) : static_cast<void*>(output), ws->out, xb, hipMemcpyDeviceToHost,
+                       s) != hipSuccess ||
         hipStreamSynchronize(s) != hipSuccess)
         return RK_NPU_ERR_DEVICE;
+    if (st) std::memcpy(output, st, xb);
     if (timings) {
         std::memset(timings, 0, sizeof(*timings));
         const double t3 = now_us();

@@ -86,11 +86,18 @@ struct Workspace {
     int* split_part;        // split-K int32 partials [pieces][tiles][tile ints]
     size_t split_part_ints; // partial ints available
     unsigned long long* kacc;  // split-K GEMV column slots [N_pad] + row code-sum slot, kept zero between calls
+    // pinned host staging of the host-buffer calls (allocated on first use)
+    void* host_stage;
+    size_t host_stage_bytes;
 };
 
 size_t workspace_bytes(const Geometry& g, int M);
 Workspace* workspace_create(Domain* d, int bits, int M, int K, int N);
 void workspace_destroy(Workspace* ws);
+// The workspace's pinned host stage of at least `bytes` (allocated or grown
+// on demand, up to 8 MiB), or nullptr when the request is larger or the
+// allocation fails; the caller then copies pageable memory directly.
+float* host_stage(Workspace* ws, size_t bytes);
 
 Weights* weights_create(Domain* d, int bits, int K, int N, const int8_t* codes, const float* scales,
                         bool device_codes);

@@ -225,3 +225,19 @@ def test_allocation_failure_calls_reclaim_then_retries():
     x = R.activations(0, "oom-x", 1, 128)
     linear.run(x, out, 1)
     assert np.array_equal(out, oracle.linear(codes, scales, x))
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_host_call_staging_small_and_large(backend, bits):
+    """Host-buffer calls below the 8 MiB pinned stage (A and C copied through
+    it) and above it (direct pageable copies), back to back on the same
+    workspace: both bit-exact against the oracle."""
+    n = 128
+    for rows, k in ((1, 8256), (256, 8256), (3, 8256)):
+        print(f"bits={bits} rows={rows} k={k} a_bytes={rows * k * 4}", flush=True)
+        codes, scales = R.weights(7, f"stage{bits}", bits, k, n)
+        x = R.activations(7, f"stage-x{rows}", rows, k)
+        linear = backend.load(npu.QuantMatrix(bits, k, n, codes, scales))
+        out = np.full((rows, n), np.nan, np.float32)
+        linear.run(x, out, rows)
+        assert np.array_equal(out, oracle.linear(codes, scales, x))
