@@ -104,6 +104,21 @@ int rk_npu_hip_workspace_codes(void* workspace, int bits, int rows, int8_t* code
  * callback still runs first). Returns the previous count. */
 int rk_npu_hip_inject_alloc_failures(int count);
 
+/* Plan switches for tests and measurements. Each starts from the environment
+ * variable of the same name, read once per process; this call sets one for
+ * the rest of the process (later plans and workspace sizing use it) and
+ * stores the value it replaces in *previous (may be NULL). Names and values:
+ *   HM_GEMM_VARIANT  -1 by shape; 0..4 forces the 256x256, 256x128, 128x128,
+ *                    64x128 or 32x128 GEMM tile
+ *   HM_SPLITS        0 by shape; n > 0 forces n K pieces per GEMM tile
+ *   HM_FORCE_GEMM    1: rows <= 8 take the MFMA GEMM instead of the GEMV
+ *   HM_GEMV_QW       -1 by shape; 0 never, 1 always (when the rows fit) a
+ *                    quantization wave in the GEMV blocks
+ *   HM_GEMV_SPLITS   0 by shape; n > 0 forces n K pieces of the one-row GEMV
+ *                    after a SwiGLU
+ * Unknown names return RK_NPU_ERR_PARAM. */
+int rk_npu_hip_set_switch(const char* name, int value, int* previous);
+
 /* Kernel timing for measurement tools. Between profile_begin and
  * profile_end every GEMM/GEMV/quantization launch of the library is
  * bracketed by two HIP events recorded on the stream it is launched on (at

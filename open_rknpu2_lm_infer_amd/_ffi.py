@@ -278,6 +278,7 @@ SIGNATURES = {
                                                         c_int]),
     "rk_npu_hip_workspace_codes": (c_int, [c_void_p, c_int, c_int, i8p, f32p, i32p]),
     "rk_npu_hip_inject_alloc_failures": (c_int, [c_int]),
+    "rk_npu_hip_set_switch": (c_int, [c_char_p, c_int, POINTER(c_int)]),
     "rk_npu_hip_linear_plan": (c_int, [c_int, c_int, c_int, c_int, P(rk_npu_hip_plan)]),
     "rk_npu_hip_profile_begin": (c_int, [c_int]),
     "rk_npu_hip_profile_end": (c_int, []),

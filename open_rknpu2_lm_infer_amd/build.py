@@ -39,7 +39,7 @@ def hipcc() -> str:
     return "hipcc"
 
 
-def build(verbose: bool = False, jobs: int = 2) -> str:
+def build(verbose: bool = False, jobs: int = 3) -> str:
     """Compile every HIP source to an object, then link the shared library."""
     build_dir = os.path.join(PKG_DIR, "_build")
     os.makedirs(build_dir, exist_ok=True)

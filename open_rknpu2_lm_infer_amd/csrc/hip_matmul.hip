@@ -301,10 +301,30 @@ enum GemmVariant { V256x256 = 0, V256x128 = 1, V128x128 = 2, V64x128 = 3, V32x12
 static const int kBM[] = {256, 256, 128, 64, 32};
 static const int kBN[] = {256, 128, 128, 128, 128};
 
-static int env_int(const char* name, int fallback) {
-    const char* v = std::getenv(name);
-    return v ? std::atoi(v) : fallback;
+// Plan switches for tests and measurements. Each starts from its environment
+// variable, read once when the library first plans a launch; afterwards only
+// rk_npu_hip_set_switch changes it, so no launch reads the environment.
+enum SwitchId { SW_GEMM_VARIANT, SW_SPLITS, SW_FORCE_GEMM, SW_GEMV_QW, SW_GEMV_SPLITS, SW_COUNT };
+struct SwitchDef {
+    const char* name;
+    int fallback;
+};
+static const SwitchDef kSwitches[SW_COUNT] = {
+    {"HM_GEMM_VARIANT", -1}, {"HM_SPLITS", 0}, {"HM_FORCE_GEMM", 0}, {"HM_GEMV_QW", -1}, {"HM_GEMV_SPLITS", 0}};
+
+static std::atomic<int>* switch_table() {
+    static std::atomic<int> table[SW_COUNT];
+    static std::once_flag once;
+    std::call_once(once, [] {
+        for (int i = 0; i < SW_COUNT; ++i) {
+            const char* v = std::getenv(kSwitches[i].name);
+            table[i].store(v ? std::atoi(v) : kSwitches[i].fallback);
+        }
+    });
+    return table;
 }
+
+static int switch_value(SwitchId id) { return switch_table()[id].load(std::memory_order_relaxed); }
 
 // Activation codes of the whole K live in the GEMV's LDS.
 constexpr int GEMV_MAX_LDS = 60 * 1024;
@@ -346,7 +366,7 @@ static Plan plan_gemm(int rows, const Geometry& g, int variant) {
     p.kind = 1;
     int v = variant;
     if (v < 0) {
-        const int forced = env_int("HM_GEMM_VARIANT", -1);
+        const int forced = switch_value(SW_GEMM_VARIANT);
         if (forced >= 0 && forced <= 4)
             v = forced;
         else
@@ -367,7 +387,7 @@ static Plan plan_gemm(int rows, const Geometry& g, int variant) {
     int f = 1;
     if ((v == V64x128 || v == V128x128) && p.tiles < cus && KT >= 128)
         f = std::max(1, std::min(std::min((3 * cus / 2 + p.tiles - 1) / p.tiles, KT / 24), 8));
-    const int forced_f = env_int("HM_SPLITS", 0);
+    const int forced_f = switch_value(SW_SPLITS);
     p.ksplit = forced_f > 0 ? std::min(forced_f, KT) : f;
     p.grid = p.tiles * p.ksplit;
     return p;
@@ -375,7 +395,7 @@ static Plan plan_gemm(int rows, const Geometry& g, int variant) {
 
 Plan plan_linear(int rows, const Geometry& g) {
     const int mr = rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : 8;
-    if (rows <= 8 && g.K_pad * mr <= GEMV_MAX_LDS && env_int("HM_FORCE_GEMM", 0) == 0) {
+    if (rows <= 8 && g.K_pad * mr <= GEMV_MAX_LDS && switch_value(SW_FORCE_GEMM) == 0) {
         Plan p{};
         p.kind = 0;
         p.mr = mr;
@@ -777,7 +797,7 @@ int enqueue_linear(Workspace* ws, const Weights* w, const void* x, int x_type, l
         const int x_chunks = (g.K_pad / 16) * pv.mr;
         const int qb = x_type == DT_F32 ? gemv_qb<float>() : gemv_qb<__half>();
         // HM_GEMV_QW: 0 never, 1 whenever the rows fit (tests, experiments).
-        const int qw_env = env_int("HM_GEMV_QW", -1);
+        const int qw_env = switch_value(SW_GEMV_QW);
         const bool qw_fits = !preq && pv.mr <= 2 && x_chunks <= 64 * qb && w_rounds <= 8;
         int qwn = 0;
         if (qw_fits && (qw_env == 1 || (qw_env < 0 && w_rounds >= 5))) qwn = 1;
@@ -792,7 +812,7 @@ int enqueue_linear(Workspace* ws, const Weights* w, const void* x, int x_type, l
         // 64-k units, at least 8 of them; HM_GEMV_SPLITS forces a count.
         const int units = g.K_pad / 64;
         int ksplit = 1;
-        const int forced_splits = env_int("HM_GEMV_SPLITS", 0);
+        const int forced_splits = switch_value(SW_GEMV_SPLITS);
         if (!preq && qwn == 0 && pv.mr == 1 && epi == EPI_PLAIN && in_max.p && (w_rounds > 8 || forced_splits > 0)) {
             ksplit = forced_splits > 0 ? forced_splits : (1280 + grid / 2) / grid;
             ksplit = std::max(1, std::min(std::min(ksplit, 8), units / 8));
@@ -1530,6 +1550,17 @@ int rk_npu_hip_profile_read(rk_npu_hip_kernel_stat* stats, int capacity, int* co
 }
 
 int rk_npu_hip_inject_alloc_failures(int count) { return g_fail_allocs.exchange(count < 0 ? 0 : count); }
+
+int rk_npu_hip_set_switch(const char* name, int value, int* previous) {
+    if (!name) return RK_NPU_ERR_PARAM;
+    for (int i = 0; i < SW_COUNT; ++i) {
+        if (std::strcmp(name, kSwitches[i].name) != 0) continue;
+        const int was = switch_table()[i].exchange(value);
+        if (previous) *previous = was;
+        return RK_NPU_OK;
+    }
+    return RK_NPU_ERR_PARAM;
+}
 
 int rk_npu_hip_linear_plan(int rows, int K, int N, int bits, rk_npu_hip_plan* plan) {
     if (!plan || rows < 1 || K < 1 || N < 1 || (bits != 4 && bits != 8)) return RK_NPU_ERR_PARAM;

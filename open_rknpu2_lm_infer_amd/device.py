@@ -5,6 +5,7 @@ hip_matmul kernel launched through the C ABI on torch's current stream.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 from typing import Dict, List, Optional, Tuple
 
@@ -131,6 +132,19 @@ def ffn(ctx: DeviceContext, gate_up: DeviceWeights, down: DeviceWeights, x, out,
                                     ctypes.c_void_p(x.data_ptr()), _dtype_code(x), ctypes.c_void_p(out.data_ptr()),
                                     _dtype_code(out), rows, stream if stream is not None else current_stream())
     check(rc, "device FFN")
+
+
+@contextlib.contextmanager
+def plan_switch(name: str, value: int):
+    """Sets one of the library's plan switches (rk_npu_hip_set_switch, e.g.
+    HM_GEMM_VARIANT) for the body of the with-block, then restores it."""
+    L = F.lib()
+    prev = ctypes.c_int()
+    check(L.rk_npu_hip_set_switch(name.encode(), int(value), ctypes.byref(prev)), f"set switch {name}")
+    try:
+        yield
+    finally:
+        check(L.rk_npu_hip_set_switch(name.encode(), prev.value, None), f"restore switch {name}")
 
 
 class KernelProfile:

@@ -43,14 +43,20 @@ def test_device_linear_matches_oracle_f32_and_f16(ctx, bits, rows):
 
 
 @pytest.mark.parametrize("bits", [4, 8])
-@pytest.mark.parametrize("rows,variant", [(1100, None), (2100, None), (2100, "0"), (4100, "0")])
-def test_device_linear_large_row_tiles(ctx, bits, rows, variant, monkeypatch):
+@pytest.mark.parametrize("rows,variant,n", [(1100, None, 768), (2100, None, 768), (2100, "0", 768),
+                                            (4100, "0", 768), (2100, "0", 640), (300, "0", 896)])
+def test_device_linear_large_row_tiles(ctx, bits, rows, variant, n):
     """Row counts that select the 128x128 tile, and the 256x256 tile (chosen by
-    the plan for very wide outputs or long K; forced here at a small shape)."""
-    if variant is not None:
-        monkeypatch.setenv("HM_GEMM_VARIANT", variant)
-    k, n = 640, 768
-    codes, scales = R.weights(5, f"dl{bits}", bits, k, n)
+    the plan for very wide outputs or long K; forced here at a small shape).
+    n = 640 and 896 leave 128 padded columns in the last 256-wide tile, as the
+    2560x151936 lm_head does (plain and SwiGLU stores masked at the edge)."""
+    with D.plan_switch("HM_GEMM_VARIANT", -1 if variant is None else int(variant)):
+        _large_row_tiles(ctx, bits, rows, n)
+
+
+def _large_row_tiles(ctx, bits, rows, n):
+    k = 640
+    codes, scales = R.weights(5, f"dl{bits}-{n}", bits, k, n)
     w = ctx.weights(bits, dev(codes), dev(scales))
     x = R.activations(5, f"dlL-x{rows}", rows, k)
     y = torch.empty(rows, n, dtype=torch.float32, device="cuda")
@@ -83,9 +89,13 @@ def test_unaligned_output_matches_oracle(ctx, bits, dtype):
 
 
 @pytest.mark.parametrize("splits", [2, 3])
-def test_split_k_switch_is_bit_exact(ctx, splits, monkeypatch):
+def test_split_k_switch_is_bit_exact(ctx, splits):
     """HM_SPLITS: K pieces per tile sum through int32 partials; same result."""
-    monkeypatch.setenv("HM_SPLITS", str(splits))
+    with D.plan_switch("HM_SPLITS", splits):
+        _split_k(splits)
+
+
+def _split_k(splits):
     local = D.DeviceContext(3)  # workspaces sized under the switch
     rows, k, n = 300, 640, 768
     for bits in (4, 8):
@@ -133,15 +143,18 @@ def test_gemv_window_configurations_match_oracle(ctx, bits):
 
 
 @pytest.mark.parametrize("qw", ["default", "0", "1"])
-def test_gemv_quantization_wave_matches_oracle(ctx, qw, monkeypatch):
+def test_gemv_quantization_wave_matches_oracle(ctx, qw):
     """One-row GEMVs with K = 2560 (5 rounds of 256 weight chunks per tile
     group: the shapes the block's dedicated quantization wave serves), fp16
     and f32 rows, W4 and W8, plain and SwiGLU: equal to the oracle with the
     wave (default rule or HM_GEMV_QW=1) and without it (HM_GEMV_QW=0); the
     workspace diagnostics hold the row's codes, scale and code sum."""
+    with D.plan_switch("HM_GEMV_QW", -1 if qw == "default" else int(qw)):
+        _quantization_wave(ctx, qw)
+
+
+def _quantization_wave(ctx, qw):
     from tests.test_gpu_linear import read_codes
-    if qw != "default":
-        monkeypatch.setenv("HM_GEMV_QW", qw)
     k = 2560
     for bits, n, swiglu in ((4, 1024, True), (8, 512, False), (4, 4096, False), (8, 1024, True)):
         codes, scales = R.weights(9, f"dqw{bits}-{n}", bits, k, n)
@@ -168,15 +181,19 @@ def test_gemv_quantization_wave_matches_oracle(ctx, qw, monkeypatch):
 
 
 @pytest.mark.parametrize("splits", [1, 2, 3, 4])
-def test_gemv_split_k_down_is_bit_exact(ctx, splits, monkeypatch):
+def test_gemv_split_k_down_is_bit_exact(ctx, splits):
     """One-row FFN whose down GEMV (K = 2240: 35 units of 64, uneven pieces)
     splits K (HM_GEMV_SPLITS forces the piece count): the pieces' int32 sums
     meet through device-scope atomics and the last piece writes the tile and
     clears the accumulators, so three calls in a row must each equal the
     oracle; the down workspace's diagnostics hold the middle row's codes,
     scale and code sum."""
+    with D.plan_switch("HM_GEMV_SPLITS", splits):
+        _gemv_split_k_down(ctx, splits)
+
+
+def _gemv_split_k_down(ctx, splits):
     from tests.test_gpu_linear import read_codes
-    monkeypatch.setenv("HM_GEMV_SPLITS", str(splits))
     h, f = 256, 2240
     for dbits in (4, 8):
         gc, gs = R.weights(7, "dsk-g", 4, h, 2 * f)
