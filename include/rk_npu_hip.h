@@ -38,6 +38,26 @@ extern "C" {
 int rk_npu_hip_linear_run(void* workspace, const void* weights, int bits, const void* A, int a_type,
                           void* C, int c_type, int rows, int epilogue, void* stream);
 
+/* Allocation-free linear. No counterpart in the reference: it is for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc). Arguments, semantics and
+ * results are those of rk_npu_hip_linear_run without the workspace: the
+ * call's scratch (activation codes, row scales, code sums and maxima, partial
+ * sums) is a slice of one RK_NPU_HIP_STATIC_SCRATCH_BYTES array per GPU inside
+ * the library, set up by rk_npu_open for its device (RK_NPU_ERR_DEVICE if that
+ * failed). The call allocates nothing and calls no allocating routine.
+ * Limits: 1 <= rows <= RK_NPU_HIP_STATIC_MAX_ROWS, and the shape's buffers,
+ * about 256 * round_up(K, 64) + 12 * round_up(N, 256) + 4 KiB bytes, must fit
+ * the array (K up to about 60000 at small N); otherwise RK_NPU_ERR_PARAM and
+ * nothing is enqueued. Every such call on one GPU shares that GPU's array,
+ * which keeps the last call's contents: calls that overlap on one GPU (other
+ * streams or threads) race and give wrong results, so serialize them (e.g. on
+ * one stream). */
+#define RK_NPU_HIP_STATIC_SCRATCH_BYTES (16u << 20)
+#define RK_NPU_HIP_STATIC_MAX_ROWS 256
+int rk_npu_hip_linear_run_static(const void* weights, int bits, const void* A, int a_type, void* C,
+                                 int c_type, int rows, int epilogue, void* stream);
+
 /* Fused FFN on device buffers: gate_up (bits gu_bits, N = 2F) -> SwiGLU ->
  * dense requant of the middle -> down (bits dn_bits). Semantics of
  * rk_npu_w4a8_run_ffn_f32. */

@@ -37,6 +37,8 @@ RK_NPU_HIP_PLAIN = 0
 RK_NPU_HIP_SWIGLU = 1
 RK_NPU_HIP_PACK_QUANTIZED = 0
 RK_NPU_HIP_INT_QUANTIZED = 1
+RK_NPU_HIP_STATIC_SCRATCH_BYTES = 16 << 20
+RK_NPU_HIP_STATIC_MAX_ROWS = 256
 RK_NPU_ATTENTION_F16_CAUSAL = 0
 RK_NPU_ATTENTION_F16_NO_MASK = 1
 RK_NPU_ATTENTION_F16_STABLE_SOFTMAX = 1
@@ -266,6 +268,8 @@ SIGNATURES = {
     "rk_npu_moe_quant_swap_slots": (c_int, [c_void_p, c_int, c_void_p, c_int]),
     "rk_npu_hip_linear_run": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_int, c_void_p, c_int, c_int, c_int,
                                       c_void_p]),
+    "rk_npu_hip_linear_run_static": (c_int, [c_void_p, c_int, c_void_p, c_int, c_void_p, c_int, c_int, c_int,
+                                             c_void_p]),
     "rk_npu_hip_ffn_run": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_int, c_void_p, c_int,
                                    c_void_p, c_int, c_int, c_void_p]),
     "rk_npu_hip_moe_run": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),

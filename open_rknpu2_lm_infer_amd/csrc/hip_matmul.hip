@@ -920,6 +920,91 @@ int enqueue_ffn(Workspace* gws, const Weights* gw, Workspace* dws, const Weights
     return rc;
 }
 
+// --- allocation-free linear (rk_npu_hip_linear_run_static) ----------------------
+// The buffers a linear call needs besides its inputs and outputs (activation
+// codes, row scales, code sums and maxima, GEMV partial maxima, split-K
+// partials and slots) in one file-scope device array instead of a workspace.
+// Each GPU holds its own copy until the process ends; in host code the name
+// `scratch` is only a stand-in, so host code uses the device address that
+// hipGetSymbolAddress returns for the current GPU, kept per device.
+constexpr size_t STATIC_SCRATCH_BYTES = (size_t)RK_NPU_HIP_STATIC_SCRATCH_BYTES;
+constexpr int STATIC_MAX_ROWS = RK_NPU_HIP_STATIC_MAX_ROWS;
+static __device__ __attribute__((aligned(256))) uint8_t scratch[STATIC_SCRATCH_BYTES];
+
+struct ScratchTable {
+    std::mutex mu;
+    std::vector<uint8_t*> ptr;  // by device ordinal
+};
+static ScratchTable& scratch_table() {
+    static ScratchTable t;
+    return t;
+}
+
+// Once per device, with that device current (rk_npu_open): look up this
+// GPU's copy of the array and zero it (the split-K slots must start at zero;
+// every call leaves them zero again).
+static int scratch_init(int dev) {
+    ScratchTable& t = scratch_table();
+    std::lock_guard<std::mutex> lock(t.mu);
+    if (dev < 0) return RK_NPU_ERR_PARAM;
+    if ((size_t)dev < t.ptr.size() && t.ptr[dev]) return RK_NPU_OK;
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) {
+        (void)hipGetLastError();
+        return RK_NPU_ERR_DEVICE;
+    }
+    if (hipMemset(p, 0, STATIC_SCRATCH_BYTES) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
+        (void)hipGetLastError();
+        return RK_NPU_ERR_DEVICE;
+    }
+    if (t.ptr.size() <= (size_t)dev) t.ptr.resize((size_t)dev + 1, nullptr);
+    t.ptr[dev] = static_cast<uint8_t*>(p);
+    return RK_NPU_OK;
+}
+
+static uint8_t* scratch_of(int dev) {
+    ScratchTable& t = scratch_table();
+    std::lock_guard<std::mutex> lock(t.mu);
+    return (dev >= 0 && (size_t)dev < t.ptr.size()) ? t.ptr[dev] : nullptr;
+}
+
+// A workspace view of the scratch array for `rows` rows of w's shape (no
+// allocation: every buffer is a slice of the array); false when the rows or
+// the shape's buffers exceed the array.
+static bool scratch_workspace(uint8_t* base, const Weights* w, int rows, Workspace& ws) {
+    if (rows < 1 || rows > STATIC_MAX_ROWS) return false;
+    const Geometry& g = w->g;
+    ws.magic = g.bits == 8 ? MAGIC_WS8 : MAGIC_WS4;
+    ws.g = g;
+    ws.M = rows;
+    ws.M_alloc = round_up(rows, 256);
+    ws.domain = w->domain;
+    ws.stream = nullptr;
+    ws.busy.store(false);
+    ws.host_stage = nullptr;
+    ws.host_stage_bytes = 0;
+    ws.a_f32 = nullptr;
+    ws.c_f32 = nullptr;
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        uint8_t* p = base + off;
+        off += round_up_z(bytes, 256);
+        return p;
+    };
+    ws.codes = reinterpret_cast<int8_t*>(take((size_t)(g.K_pad / 16) * ws.M_alloc * 16));
+    ws.rowscale = reinterpret_cast<float*>(take((size_t)ws.M_alloc * 4));
+    ws.rowsum = reinterpret_cast<int*>(take((size_t)ws.M_alloc * 4));
+    ws.rowmax = reinterpret_cast<unsigned*>(take((size_t)ws.M_alloc * 4));
+    ws.partmax = reinterpret_cast<float*>(take((size_t)g.N_pad * 4));
+    ws.kacc = reinterpret_cast<unsigned long long*>(take(((size_t)g.N_pad + 8) * 8));
+    if (off > STATIC_SCRATCH_BYTES) return false;
+    // the rest holds split-K partials; plans whose partials do not fit run unsplit
+    ws.split_part = reinterpret_cast<int*>(base + off);
+    ws.split_part_ints = (STATIC_SCRATCH_BYTES - off) / 4;
+    ws.bytes = STATIC_SCRATCH_BYTES;
+    return true;
+}
+
 // Pinned staging for the host-buffer calls. Copies between pageable caller
 // memory and the device go through the runtime's own staging, which costs
 // tens of microseconds per call at decode sizes (a few KB); the workspace
@@ -1017,6 +1102,9 @@ rk_npu_ctx* rk_npu_open(const char* device) {
         return nullptr;
     }
     if (hipSetDevice(dev) != hipSuccess) return nullptr;
+    // (a failure leaves rk_npu_hip_linear_run_static returning RK_NPU_ERR_DEVICE
+    // on this device; the context itself stays usable)
+    (void)scratch_init(dev);
     rk_npu_ctx* ctx = new (std::nothrow) rk_npu_ctx();
     if (ctx) ctx->device = dev;
     return ctx;
@@ -1421,6 +1509,25 @@ int rk_npu_hip_linear_run(void* workspace, const void* weights, int bits, const 
     const int width = epi == EPI_PLAIN ? w->g.N : w->g.N / 2;
     return enqueue_linear(ws, w, A, a_type, w->g.K, rows, QUANT_DENSE, RowMax{nullptr, 0}, C, c_type, width, epi,
                           nullptr, s);
+}
+
+int rk_npu_hip_linear_run_static(const void* weights, int bits, const void* A, int a_type, void* C, int c_type,
+                                 int rows, int epilogue, void* stream) {
+    const Weights* w = as_w(weights, bits);
+    if (!w || !A || !C) return RK_NPU_ERR_PARAM;
+    if ((a_type != DT_F32 && a_type != DT_F16) || (c_type != DT_F32 && c_type != DT_F16)) return RK_NPU_ERR_PARAM;
+    if (epilogue != RK_NPU_HIP_PLAIN && epilogue != RK_NPU_HIP_SWIGLU) return RK_NPU_ERR_PARAM;
+    const int epi = epilogue == RK_NPU_HIP_SWIGLU ? EPI_SWIGLU_MAX : EPI_PLAIN;
+    if (epi != EPI_PLAIN && !w->g.half) return RK_NPU_ERR_UNSUPPORTED;  // SwiGLU needs N % 64 == 0
+    const int dev = device_of(w->domain);
+    uint8_t* base = scratch_of(dev);
+    if (!base) return RK_NPU_ERR_DEVICE;
+    Workspace ws;
+    if (!scratch_workspace(base, w, rows, ws)) return RK_NPU_ERR_PARAM;  // rows or shape beyond the array
+    if (hipSetDevice(dev) != hipSuccess) return RK_NPU_ERR_DEVICE;
+    const int width = epi == EPI_PLAIN ? w->g.N : w->g.N / 2;
+    return enqueue_linear(&ws, w, A, a_type, w->g.K, rows, QUANT_DENSE, RowMax{nullptr, 0}, C, c_type, width, epi,
+                          nullptr, static_cast<hipStream_t>(stream));
 }
 
 int rk_npu_hip_ffn_run(void* gate_up_workspace, const void* gate_up, int gu_bits, void* down_workspace,
