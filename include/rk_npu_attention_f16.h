@@ -47,7 +47,7 @@ typedef struct rk_npu_attention_f16_config {
     uint32_t core_mask;       /* accepted and ignored (one GPU) */
     int32_t kv_tile;          /* accepted and ignored: the kernel tiles by itself */
     uint32_t flags;           /* RK_NPU_ATTENTION_F16_STABLE_SOFTMAX */
-    int32_t mask_mode;        /* RK_NPU_ATTENTION_F16_CAUSAL or _NO_MASK */
+    uint32_t mask_mode;       /* RK_NPU_ATTENTION_F16_CAUSAL or _NO_MASK */
 } rk_npu_attention_f16_config;
 
 typedef struct rk_npu_attention_f16_sizes {
@@ -59,8 +59,12 @@ typedef struct rk_npu_attention_f16_sizes {
 } rk_npu_attention_f16_sizes;
 
 typedef struct rk_npu_attention_f16_cache_info {
-    int32_t length;   /* rows held */
-    int32_t capacity; /* rows allocated */
+    int32_t length;       /* rows held */
+    int32_t capacity;     /* rows allocated */
+    int32_t max_capacity; /* rows the cache may grow to: config max_capacity rounded up to 32
+                             (src/npu/vision_tests.rs:201) */
+    uint64_t generation;  /* changes whenever the K/V storage is reallocated or reloaded, not on
+                             append or truncate (src/npu.rs:1789) */
     uint64_t key_bytes;
     uint64_t value_bytes;
     uint64_t tail_bytes;

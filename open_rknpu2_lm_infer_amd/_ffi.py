@@ -163,7 +163,7 @@ class rk_npu_hip_checkpoint_part(Structure):
 class rk_npu_attention_f16_config(Structure):
     _fields_ = [("query_heads", c_int32), ("kv_heads", c_int32), ("head_dim", c_int32), ("softmax_scale", c_float),
                 ("max_query_rows", c_int32), ("max_capacity", c_int32), ("initial_capacity", c_int32),
-                ("core_mask", c_uint32), ("kv_tile", c_int32), ("flags", c_uint32), ("mask_mode", c_int32)]
+                ("core_mask", c_uint32), ("kv_tile", c_int32), ("flags", c_uint32), ("mask_mode", c_uint32)]
 
 
 class rk_npu_attention_f16_sizes(Structure):
@@ -172,8 +172,8 @@ class rk_npu_attention_f16_sizes(Structure):
 
 
 class rk_npu_attention_f16_cache_info(Structure):
-    _fields_ = [("length", c_int32), ("capacity", c_int32), ("key_bytes", c_uint64), ("value_bytes", c_uint64),
-                ("tail_bytes", c_uint64)]
+    _fields_ = [("length", c_int32), ("capacity", c_int32), ("max_capacity", c_int32), ("generation", c_uint64),
+                ("key_bytes", c_uint64), ("value_bytes", c_uint64), ("tail_bytes", c_uint64)]
 
 
 class rk_npu_attention_f16_timings(Structure):
@@ -188,6 +188,51 @@ i32p = P(c_int32)
 
 # name: (restype, argtypes)
 SIGNATURES = {
+    # non-hot operator families (rk_npu_mm_tune.h, rk_npu_mm_gelu.h,
+    # rk_npu_mla_f16.h, rk_npu_gdn.h): report RK_NPU_ERR_UNSUPPORTED
+    "rk_npu_mm_autotune_config_init": (None, [c_void_p, c_int32, c_int32, c_int32]),
+    "rk_npu_mm_autotune_cache_load": (c_int, [c_void_p, c_void_p, c_char_p, c_void_p, c_void_p]),
+    "rk_npu_mm_autotune_cached": (c_int, [c_void_p, c_void_p, c_char_p, c_int32, c_void_p, c_void_p, c_void_p]),
+    "rk_npu_mm_autotune": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p]),
+    "rk_npu_mm_strategy_default": (c_int, [c_void_p, c_void_p]),
+    "rk_npu_mm_tuned_weights_match": (c_int, [c_void_p, c_void_p]),
+    "rk_npu_mm_tuned_workspace_create": (c_int, [c_void_p, c_void_p, c_void_p]),
+    "rk_npu_mm_tuned_workspace_free": (None, [c_void_p]),
+    "rk_npu_mm_tuned_weights_create": (c_int, [c_void_p, c_void_p, c_void_p, c_uint64, c_char_p, c_void_p]),
+    "rk_npu_mm_tuned_weights_free": (None, [c_void_p]),
+    "rk_npu_mm_tuned_run_weights": (c_int, [c_void_p, c_void_p, c_uint64, c_void_p, c_void_p, c_void_p, c_uint64]),
+    "rk_npu_mm_desc_init": (None, [c_void_p, c_int32, c_int32, c_int32, c_int32]),
+    "rk_npu_mm_options_init": (None, [c_void_p]),
+    "rk_npu_mm_plan_create": (c_int, [c_void_p, c_void_p, c_void_p]),
+    "rk_npu_mm_plan_free": (None, [c_void_p]),
+    "rk_npu_mm_workspace_create": (c_int, [c_void_p, c_void_p, c_uint32, c_void_p]),
+    "rk_npu_mm_workspace_free": (None, [c_void_p]),
+    "rk_npu_mm_packed_b_create": (c_int, [c_void_p, c_void_p, c_void_p, c_uint64, c_void_p]),
+    "rk_npu_mm_packed_b_free": (None, [c_void_p]),
+    "rk_npu_mm_run_packed_b": (c_int, [c_void_p, c_void_p, c_uint64, c_void_p, c_void_p, c_uint64]),
+    "rk_npu_mm_gelu_config_init": (None, [c_void_p, c_int32, c_int32, c_int32]),
+    "rk_npu_mm_gelu_prepare": (c_int, [c_void_p, c_void_p, c_void_p]),
+    "rk_npu_mm_gelu_free": (None, [c_void_p]),
+    "rk_npu_mm_gelu_run_weights": (c_int, [c_void_p, c_void_p, c_uint64, c_void_p, c_void_p, c_void_p]),
+    "rk_npu_mla_f16_config_init": (None, [c_void_p]),
+    "rk_npu_mla_f16_weights_create": (c_int, [c_void_p, c_void_p, c_void_p]),
+    "rk_npu_mla_f16_weights_free": (None, [c_void_p]),
+    "rk_npu_mla_f16_cache_create": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p]),
+    "rk_npu_mla_f16_cache_free": (None, [c_void_p]),
+    "rk_npu_mla_f16_prepare": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p]),
+    "rk_npu_mla_f16_workspace_free": (None, [c_void_p]),
+    "rk_npu_mla_f16_cache_get_info": (c_int, [c_void_p, c_void_p]),
+    "rk_npu_mla_f16_cache_reserve": (c_int, [c_void_p, c_void_p, c_int32]),
+    "rk_npu_mla_f16_cache_load": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int32]),
+    "rk_npu_mla_f16_cache_truncate": (c_int, [c_void_p, c_int32]),
+    "rk_npu_mla_f16_cache_append": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int32]),
+    "rk_npu_mla_f16_run": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_void_p,
+                                   c_void_p, c_void_p]),
+    "rk_npu_gdn_config_init": (None, [c_void_p, c_int32]),
+    "rk_npu_gdn_prepare": (c_int, [c_void_p, c_void_p, c_void_p]),
+    "rk_npu_gdn_workspace_free": (None, [c_void_p]),
+    "rk_npu_gdn_run_projected_strided": (c_int, [c_void_p, c_void_p, c_uint64, c_void_p, c_void_p, c_void_p,
+                                                 c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "rk_npu_strerror": (c_char_p, [c_int]),
     "rk_npu_open": (c_void_p, [c_char_p]),
     "rk_npu_close": (None, [c_void_p]),

@@ -645,6 +645,7 @@ struct AttnCache {
     __half* v;
     int length, capacity;
     size_t bytes_each;  // of k and of v
+    uint64_t generation;  // bumped whenever the K/V storage is replaced or reloaded
 };
 
 struct AttnWork {
@@ -721,6 +722,7 @@ static int cache_grow(AttnCache* c, int capacity) {
     c->k = nk;
     c->v = nv;
     c->capacity = capacity;
+    c->generation += 1;
     c->bytes_each = nb;
     return RK_NPU_OK;
 }
@@ -988,6 +990,7 @@ int rk_npu_attention_f16_cache_create(rk_npu_iommu_domain* domain, const rk_npu_
     c->domain = d;
     c->cfg = *config;
     c->length = 0;
+    c->generation = 0;
     c->capacity = std::max(32, round_up(config->initial_capacity, 32));
     c->bytes_each = kv_bytes(config, c->capacity);
     c->k = static_cast<__half*>(domain_alloc(d, c->bytes_each));
@@ -1026,6 +1029,7 @@ int rk_npu_attention_f16_cache_load(rk_npu_ctx* ctx, rk_npu_attention_f16_cache*
     if (hipSetDevice(device_of(c->domain)) != hipSuccess || hipDeviceSynchronize() != hipSuccess)
         return RK_NPU_ERR_DEVICE;
     c->length = 0;
+    c->generation += 1;  // the contents are replaced (a reset when rows == 0)
     if (rows == 0) return RK_NPU_OK;
     int rc = cache_grow(c, rows);
     if (rc != RK_NPU_OK) return rc;
@@ -1060,6 +1064,8 @@ int rk_npu_attention_f16_cache_get_info(const rk_npu_attention_f16_cache* cache,
     if (!c || !info) return RK_NPU_ERR_PARAM;
     info->length = c->length;
     info->capacity = c->capacity;
+    info->max_capacity = round_up(c->cfg.max_capacity, 32);
+    info->generation = c->generation;
     info->key_bytes = c->bytes_each;
     info->value_bytes = c->bytes_each;
     info->tail_bytes = 0;

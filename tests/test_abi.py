@@ -173,3 +173,109 @@ def test_router_mirror_matches_oracle():
         oi, ow = oracle.routes(logits, 8)
         assert ids == oi.tolist()
         assert np.allclose(w, ow, rtol=0, atol=2e-7)
+
+
+# ---- the binding surface the reference's unchanged crate needs -----------------
+
+# Constants whose Rust type the reference's code fixes outside a field or
+# argument: error codes compared with i32 return codes (src/npu.rs:195,
+# 1592, 1778, src/npu/floating.rs:197), the blob version returned as u32
+# (src/npu/moe.rs:283-285), the domain count compared with a u32 id
+# (src/npu.rs:484).
+TYPED_CONSTANTS = {"RK_NPU_ERR_PARAM": "i32", "RK_NPU_ERR_CACHE_MISS": "i32",
+                   "RK_NPU_MOE_QUANT_BLOB_VERSION": "u32", "RK_NPU_IOMMU_DOMAIN_COUNT": "u32"}
+
+
+@pytest.fixture(scope="module")
+def headers():
+    from tests import c_abi_model
+    if c_abi_model.clang() is None:
+        pytest.skip("no clang to parse the headers")
+    return c_abi_model.Headers()
+
+
+@pytest.fixture(scope="module")
+def uses():
+    import json
+    return json.load(open(os.path.join(ROOT, "tests", "golden", "reference_ffi_uses.json")))
+
+
+def test_headers_declare_every_identifier_the_reference_uses(headers, uses):
+    """Every rk_npu_* / RK_NPU_* name the reference's src/ takes from its
+    bindings (build.rs:138-158 headers, src/npu.rs and src/npu/*.rs users,
+    extracted by tests/golden/extract_ffi_uses.py) is declared here, and the
+    four non-hot headers build.rs:141-144 names exist."""
+    for h in ("rk_npu_quant_matmul.h", "rk_npu_w4a8_tune.h", "rk_npu_attention_f16.h", "rk_npu_mla_f16.h",
+              "rk_npu_mm_tune.h", "rk_npu_mm_gelu.h", "rk_npu_gdn.h", "rk_npu_moe_w8.h"):
+        assert os.path.exists(os.path.join(ROOT, "include", h)), h
+    missing = sorted(set(uses["identifiers"]) - headers.declared_names())
+    assert not missing, f"used by the reference, not declared: {missing}"
+
+
+def test_struct_fields_the_reference_reads_and_writes_exist(headers, uses):
+    missing = [(t, f) for t, f in uses["fields"] if headers.field_type(t, f) is None]
+    assert not missing, f"fields the reference's Rust code uses but the headers lack: {missing}"
+
+
+def test_call_arity_matches_the_reference_call_sites(headers, uses):
+    bad = {name: (len(headers.functions[name][1]), arities) for name, arities in uses["call_arity"].items()
+           if name in headers.functions and len(headers.functions[name][1]) not in arities}
+    assert not bad, f"parameter counts differ from the reference's calls: {bad}"
+    assert set(uses["call_arity"]) <= set(headers.functions)
+
+
+def test_constants_have_the_rust_type_of_their_fields_and_parameters(headers, uses):
+    """bindgen types a non-negative #define u32 and an enumerator as its enum's
+    underlying type, so `cfg.field = RK_NPU_X` (and ==) only compiles when the
+    field's Rust type is that type; the same for a constant passed as an
+    argument."""
+    bad = []
+    for t, f, const, _ in uses["field_constants"]:
+        ft, ct = headers.rust_type(headers.field_type(t, f)), headers.constant_type(const)
+        if ft != ct:
+            bad.append((t, f, ft, const, ct))
+    for field, const, _ in uses["named_field_constants"]:
+        ct = headers.constant_type(const)
+        for rec_name, rec in headers.records.items():
+            if rec and field in rec and headers.rust_type(rec[field]) != ct:
+                bad.append((rec_name, field, headers.rust_type(rec[field]), const, ct))
+    for fn, idx, const in uses["constant_arguments"]:
+        pt, ct = headers.rust_type(headers.functions[fn][1][idx]), headers.constant_type(const)
+        if pt != ct:
+            bad.append((fn, idx, pt, const, ct))
+    for const, want in TYPED_CONSTANTS.items():
+        if headers.constant_type(const) != want:
+            bad.append((const, headers.constant_type(const), want))
+    assert not bad, f"constant / field type mismatches bindgen would reject: {bad}"
+
+
+def test_free_functions_take_one_mutable_handle(headers, uses):
+    """Handle<T> keeps `free: unsafe extern "C" fn(*mut T)` (src/npu.rs:163-166)."""
+    for name in uses["identifiers"]:
+        if name.endswith("_free") and name in headers.functions:
+            ret, params = headers.functions[name]
+            assert ret == "void" and len(params) == 1 and headers.rust_type(params[0]).startswith("*mut "), name
+
+
+def test_non_hot_entry_points_report_unsupported_without_a_device():
+    """The stubs create nothing and say so: a creator returns
+    RK_NPU_ERR_UNSUPPORTED and leaves its out-pointer NULL, config_init
+    fills defaults, free accepts NULL."""
+    L = F.lib()
+    out = ctypes.c_void_p(1)
+    assert L.rk_npu_mm_plan_create(None, None, ctypes.byref(out)) == F.RK_NPU_ERR_UNSUPPORTED and not out.value
+    out = ctypes.c_void_p(1)
+    assert L.rk_npu_mla_f16_weights_create(None, None, ctypes.byref(out)) == F.RK_NPU_ERR_UNSUPPORTED
+    assert not out.value
+    out = ctypes.c_void_p(1)
+    assert L.rk_npu_gdn_prepare(None, None, ctypes.byref(out)) == F.RK_NPU_ERR_UNSUPPORTED and not out.value
+    out = ctypes.c_void_p(1)
+    assert L.rk_npu_mm_gelu_prepare(None, None, ctypes.byref(out)) == F.RK_NPU_ERR_UNSUPPORTED and not out.value
+    assert L.rk_npu_mm_autotune_cache_load(None, ctypes.c_void_p(1), None, None, None) == F.RK_NPU_ERR_CACHE_MISS
+    assert L.rk_npu_mla_f16_run(None, None, None, None, None, 1, 0, None, None, None) == F.RK_NPU_ERR_UNSUPPORTED
+    cfg = (ctypes.c_int32 * 32)()
+    L.rk_npu_gdn_config_init(cfg, 64)
+    assert cfg[0] == 64
+    for name in ("rk_npu_mm_plan_free", "rk_npu_mm_workspace_free", "rk_npu_mla_f16_cache_free",
+                 "rk_npu_gdn_workspace_free", "rk_npu_mm_gelu_free", "rk_npu_mm_tuned_weights_free"):
+        getattr(L, name)(None)

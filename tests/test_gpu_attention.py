@@ -192,12 +192,17 @@ def test_cache_bookkeeping():
     att = be.attention(qh, kh, d, scale)
     rng = np.random.default_rng(7)
     k_all, v_all = run_sequence(att, qh, kh, d, (40, 30), rng, scale)
-    cap0 = att.info().capacity
+    info0 = att.info()
+    cap0, gen0 = info0.capacity, info0.generation
+    assert info0.max_capacity == 256  # the context, a multiple of 32
     att.reserve(256)
     assert att.info().capacity == 256 and att.info().length == 70 and att.bytes() == 2 * 2 * 256 * 64 * 2
+    # generation: changed by a reallocation, kept by truncate (src/npu.rs:1789)
+    gen1 = att.info().generation
+    assert (gen1 != gen0) == (cap0 < 256)
     # contents survive the growth: a decode step still matches
     att.truncate(50)
-    assert att.info().length == 50
+    assert att.info().length == 50 and att.info().generation == gen1
     q = rng.standard_normal((1, qh, d)).astype(np.float32)
     k = rng.standard_normal((1, kh, d)).astype(np.float32)
     v = rng.standard_normal((1, kh, d)).astype(np.float32)
@@ -213,7 +218,7 @@ def test_cache_bookkeeping():
     with pytest.raises(npu.NpuError):
         att.append(k, v, 1, 7)  # position mismatch
     att.reset()
-    assert att.info().length == 0
+    assert att.info().length == 0 and att.info().generation != gen1
     with pytest.raises(npu.NpuError):
         att.reserve(512)  # beyond the context
     with pytest.raises(npu.NpuError):
