@@ -202,3 +202,38 @@ def test_moe_blob_export_import_and_slot_swap():
     corrupt[0] ^= 0xFF
     with pytest.raises(npu.NpuError):
         other.import_(0, bytes(corrupt))
+
+
+def test_resident_moe_equals_paged_composition_on_gpu():
+    """The reference's paged path (src/model/experts/paged.rs:590-641, 494-507)
+    on the GPU: every nonzero-route assignment as its own row of a top=1 bank
+    with route 1.0, then the rank-ordered fma reduction on the host. The
+    resident top-8 run must give the same bits, including a repeated expert,
+    zero and negative routes."""
+    from tests.test_moe_oracle_pin import fma_vec
+    h, inter, experts, top, rows = 256, 96, 16, 8, 6
+    backend = npu.Backend(npu.ModelOptions(chunk=64))
+    gate, down = moe_bank(h, inter, experts, 8, "paged")
+    resident = backend.load_moe(gate, down, top)
+    single = backend.load_moe(gate, down, 1)
+    x = R.activations(4, "paged-x", rows, h)
+    ids, w = routed(rows, experts, top, "paged-r")
+    ids[1, 3] = ids[1, 0]  # repeated expert
+    w[2, 5] = 0.0
+    w[3, 1] = -0.25
+    out = np.zeros((rows, h), np.float32)
+    resident.run(x, ids, w, out, rows)
+    jobs = [(r, k) for r in range(rows) for k in range(top) if w[r, k] != 0.0]
+    xin = np.stack([x[r] for r, _ in jobs])
+    jid = np.array([[ids[r, k]] for r, k in jobs], np.int32)
+    contrib = np.zeros((len(jobs), h), np.float32)
+    single.run(xin, jid, np.ones((len(jobs), 1), np.float32), contrib, len(jobs))
+    by_job = {job: contrib[i] for i, job in enumerate(jobs)}
+    want = np.zeros((rows, h), np.float32)
+    for r in range(rows):
+        s = np.zeros(h, np.float32)
+        for k in range(top):
+            if w[r, k] > 0.0:
+                s = fma_vec(by_job[(r, k)], w[r, k], s)
+        want[r] = s
+    assert np.array_equal(out, want)
