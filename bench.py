@@ -628,6 +628,80 @@ def traffic_probe(torch, ctx, rows=1, reps=3):
         f"({lin_bytes(4, H, 2 * F, rows)} algorithmic B each)")
 
 
+def run_probes(torch, ctx, reps=20):
+    """Ceilings measured on this box with the library's roofline probes
+    (rk_npu_hip_mfma_probe, rk_npu_hip_stream_probe), beside the decode
+    projections' own per-launch times in the same setting: 36 launches on 36
+    distinct buffers / weight sets captured in a graph, HIP events on the
+    replay stream, so every read comes from HBM."""
+    import ctypes
+    from open_rknpu2_lm_infer_amd import _ffi as FFI
+    from open_rknpu2_lm_infer_amd import device as D
+    L = FFI.lib()
+    cur = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    res = {"mfma_int8": [], "hbm_read": [], "decode_kernels": []}
+    sink = torch.empty(4096 * 256, dtype=torch.int32, device="cuda")
+    for blocks in (256, 512, 1024, 2048):
+        iters = 512
+        def fn():
+            npu_check(L.rk_npu_hip_mfma_probe(blocks, iters, ctypes.c_void_p(sink.data_ptr()), cur()), "mfma probe")
+        ms, _ = graph_time(torch, fn, reps)
+        ops = blocks * 4 * iters * 8 * 65536
+        res["mfma_int8"].append({"blocks": blocks, "waves_per_simd": blocks // 256, "us": round(ms * 1e3, 2),
+                                 "tops": round(ops / (ms * 1e-3) / 1e12, 1)})
+        log(f"[probe] mfma blocks={blocks}: {res['mfma_int8'][-1]['tops']} TOPS")
+    gen = Gen(torch, 1)
+    t = DenseLayers(torch, ctx, gen, 1, (4, 4, 4, 4), tag="dec1")
+    # per projection: (name, K, N, GEMV grid, GEMV threads per block)
+    shapes = (("qkv", H, Q + 2 * KV, (Q + 2 * KV) // 8, 256), ("o", Q, H, H // 8, 256),
+              ("gate_up", H, 2 * F, 2 * F // 16, 320), ("down", F, H, 4 * H // 8, 256))
+    sinkb = torch.empty(1 << 20, dtype=torch.int32, device="cuda")
+    for name, k, n, grid, threads in shapes:
+        nbytes = lin_bytes(4, k, n, 1)
+        bufs = [torch.empty(k * n // 2 + 4 * n, dtype=torch.uint8, device="cuda") for _ in range(LAYERS)]
+        row = {"projection": name, "bytes": nbytes, "gemv_grid": [grid, threads]}
+        for label, blocks, thr, read in (("empty launch, GEMV grid", grid, threads, 0),
+                                         ("read, GEMV grid", grid, threads, 1),
+                                         ("read, 256x512", 256, 512, 1), ("read, 512x512", 512, 512, 1),
+                                         ("read, 1024x256", 1024, 256, 1), ("read, 2048x256", 2048, 256, 1)):
+            def fn():
+                for b in bufs:
+                    npu_check(L.rk_npu_hip_stream_probe(ctypes.c_void_p(b.data_ptr()), b.numel(), blocks, thr, read,
+                                                        ctypes.c_void_p(sinkb.data_ptr()), cur()), "stream probe")
+            ms, _ = graph_time(torch, fn, reps)
+            us = ms * 1e3 / LAYERS
+            row[label] = {"us": round(us, 3), "gbs": round(nbytes / (us * 1e-6) / 1e9, 1) if read else None}
+        del bufs
+        mats = [m[name] for m in t.w]
+        if name == "down":
+            def fn():
+                for m in t.w:
+                    D.ffn(ctx, m["gate_up"], m["down"], t.x_ffn, t.y_ffn, 1, gws=t.ws["gate_up"], dws=t.ws["down"])
+            ms_ffn, _ = graph_time(torch, fn, reps)
+            row["FFN call (gate_up launch + down launch)"] = {"us": round(ms_ffn * 1e3 / LAYERS, 3)}
+            with D.plan_switch("HM_FFN_FUSED", 1):
+                ms_one, _ = graph_time(torch, fn, reps)
+            row["FFN call as one launch (HM_FFN_FUSED=1)"] = {"us": round(ms_one * 1e3 / LAYERS, 3)}
+        else:
+            x = t.x_o if name == "o" else t.x_ffn
+            y = torch.empty(1, n // 2 if name == "gate_up" else n, dtype=torch.float16, device="cuda")
+            def fn():
+                for w in mats:
+                    D.linear(ctx, w, x, y, 1, swiglu=(name == "gate_up"), ws=t.ws[name])
+            ms, _ = graph_time(torch, fn, reps)
+            us = ms * 1e3 / LAYERS
+            row["library call"] = {"us": round(us, 3), "gbs": round(nbytes / (us * 1e-6) / 1e9, 1)}
+        res["hbm_read"].append(row)
+        log(f"[probe] {name}: {row}")
+    del t
+    return res
+
+
+def npu_check(rc, what):
+    if rc != 0:
+        raise RuntimeError(f"{what}: rc {rc}")
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -639,6 +713,8 @@ def main():
                     help="rows of the primary decode line (1 is the metric's configuration)")
     ap.add_argument("--only", choices=["prefill", "ffn512", "up128", "moe", "attention", "host"],
                     help="run one secondary workload alone and print its result (for profiling)")
+    ap.add_argument("--probes", action="store_true",
+                    help="only measure the ceilings (MFMA int8 rate, HBM read floors per decode projection)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only run the workload of the FETCH_SIZE / WRITE_SIZE counter runs")
     args = ap.parse_args()
@@ -651,6 +727,9 @@ def main():
     ctx = D.DeviceContext(0)
     if args.traffic_probe:
         traffic_probe(torch, ctx)
+        return
+    if args.probes:
+        print(json.dumps(run_probes(torch, ctx)), flush=True)
         return
     if args.only:
         steps = max(4, args.steps // 2)

@@ -65,6 +65,18 @@ int rk_npu_hip_ffn_run(void* gate_up_workspace, const void* gate_up, int gu_bits
                        void* down_workspace, const void* down, int dn_bits, const void* A,
                        int a_type, void* C, int c_type, int rows, void* stream);
 
+/* With the switch HM_FFN_FUSED set to 1, a one-row call of
+ * rk_npu_hip_ffn_run whose shapes allow it (W4 gate_up with K up to 3072,
+ * such as 2560 -> 2 x 9728) runs as ONE launch whose down pieces wait on the
+ * device, with a bounded spin, for the gate_up blocks of the same launch (the
+ * launch runs only when the GPU can hold all of its blocks at once). If that
+ * wait ever gives up (another workload holding the CUs for milliseconds), the
+ * output is not valid and the down workspace records it: rk_npu_hip_ffn_status
+ * synchronizes the device and returns RK_NPU_ERR_DEVICE once for such calls
+ * (clearing the record), else 0. The host-buffer rk_npu_w4a8_run_ffn_f32
+ * checks it itself. Off by default: slower than two launches here. */
+int rk_npu_hip_ffn_status(void* down_workspace, int dn_bits);
+
 /* Routed MoE on device buffers, semantics of rk_npu_moe_w8_run_f32. ids must
  * lie in [0, routed_experts): they are checked on the device and an
  * out-of-range id makes the call return RK_NPU_ERR_PARAM at the next
@@ -136,6 +148,11 @@ int rk_npu_hip_inject_alloc_failures(int count);
  *                    quantization wave in the GEMV blocks
  *   HM_GEMV_SPLITS   0 by shape; n > 0 forces n K pieces of the one-row GEMV
  *                    after a SwiGLU
+ *   HM_FFN_FUSED     0: a one-row FFN runs as two launches (gate_up, then
+ *                    down); 1: as one launch when its shapes allow
+ *   HM_FFN_SPIN      polls a one-launch FFN's down blocks make for their
+ *                    gate_up blocks before giving up (65536); negative: they
+ *                    give up at once (tests of the failure report)
  * Unknown names return RK_NPU_ERR_PARAM. */
 int rk_npu_hip_set_switch(const char* name, int value, int* previous);
 
@@ -160,6 +177,22 @@ typedef struct rk_npu_hip_kernel_stat {
 int rk_npu_hip_profile_begin(int max_launches);
 int rk_npu_hip_profile_end(void);
 int rk_npu_hip_profile_read(rk_npu_hip_kernel_stat* stats, int capacity, int* count);
+
+/* Roofline probes for measurement tools (no reference counterpart; nothing
+ * in the library uses them). Both only enqueue on `stream`.
+ * rk_npu_hip_stream_probe: one launch of `blocks` x `threads` (a multiple
+ * of 64 up to 512) threads that reads `bytes` (rounded down to 16) from the 16-byte aligned
+ * device buffer `src` once with 16-byte non-temporal loads, the loads the
+ * GEMV issues, or with read = 0 the same launch without loads (its fixed
+ * cost); one uint32 per block is stored to `sink` ([blocks]).
+ * rk_npu_hip_mfma_probe: `blocks` x 256 threads, each wave issuing `iters`
+ * rounds of 8 independent v_mfma_i32_32x32x32_i8 on register operands
+ * (65536 int8 ops each, no memory traffic): the dense int8 matrix-core rate
+ * of the part at its loaded clock; one int32 per thread is stored to
+ * `sink` ([blocks * 256]). */
+int rk_npu_hip_stream_probe(const void* src, uint64_t bytes, int blocks, int threads, int read, uint32_t* sink,
+                            void* stream);
+int rk_npu_hip_mfma_probe(int blocks, int iters, int32_t* sink, void* stream);
 
 /* Launch plan the library uses for a linear of this shape, for diagnostics:
  * kind 0 = GEMV (no MFMA), 1 = MFMA GEMM; tile sizes and K splits. */

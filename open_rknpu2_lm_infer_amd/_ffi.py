@@ -327,6 +327,9 @@ SIGNATURES = {
                                                         c_int]),
     "rk_npu_hip_workspace_codes": (c_int, [c_void_p, c_int, c_int, i8p, f32p, i32p]),
     "rk_npu_hip_inject_alloc_failures": (c_int, [c_int]),
+    "rk_npu_hip_ffn_status": (c_int, [c_void_p, c_int]),
+    "rk_npu_hip_stream_probe": (c_int, [c_void_p, c_uint64, c_int, c_int, c_int, c_void_p, c_void_p]),
+    "rk_npu_hip_mfma_probe": (c_int, [c_int, c_int, c_void_p, c_void_p]),
     "rk_npu_hip_set_switch": (c_int, [c_char_p, c_int, POINTER(c_int)]),
     "rk_npu_hip_linear_plan": (c_int, [c_int, c_int, c_int, c_int, P(rk_npu_hip_plan)]),
     "rk_npu_hip_profile_begin": (c_int, [c_int]),

@@ -9,7 +9,7 @@ PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG_DIR, "csrc")
 LIB_NAME = "libhip_matmul.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
-SOURCES = ["hip_matmul.hip", "moe.hip", "attention.hip", "unsupported_ops.hip"]
+SOURCES = ["hip_matmul.hip", "moe.hip", "attention.hip", "unsupported_ops.hip", "probes.hip"]
 
 # Bit-exactness of the quantization, dequantization and SwiGLU paths relies on
 # single IEEE operations: no contraction, correctly rounded division, IEEE

@@ -304,13 +304,15 @@ static const int kBN[] = {256, 128, 128, 128, 128};
 // Plan switches for tests and measurements. Each starts from its environment
 // variable, read once when the library first plans a launch; afterwards only
 // rk_npu_hip_set_switch changes it, so no launch reads the environment.
-enum SwitchId { SW_GEMM_VARIANT, SW_SPLITS, SW_FORCE_GEMM, SW_GEMV_QW, SW_GEMV_SPLITS, SW_COUNT };
+enum SwitchId { SW_GEMM_VARIANT, SW_SPLITS, SW_FORCE_GEMM, SW_GEMV_QW, SW_GEMV_SPLITS, SW_FFN_FUSED, SW_FFN_SPIN,
+                SW_COUNT };
 struct SwitchDef {
     const char* name;
     int fallback;
 };
 static const SwitchDef kSwitches[SW_COUNT] = {
-    {"HM_GEMM_VARIANT", -1}, {"HM_SPLITS", 0}, {"HM_FORCE_GEMM", 0}, {"HM_GEMV_QW", -1}, {"HM_GEMV_SPLITS", 0}};
+    {"HM_GEMM_VARIANT", -1}, {"HM_SPLITS", 0},         {"HM_FORCE_GEMM", 0}, {"HM_GEMV_QW", -1},
+    {"HM_GEMV_SPLITS", 0},   {"HM_FFN_FUSED", 0},      {"HM_FFN_SPIN", 1 << 16}};
 
 static std::atomic<int>* switch_table() {
     static std::atomic<int> table[SW_COUNT];
@@ -412,7 +414,7 @@ Plan plan_linear(int rows, const Geometry& g) {
 // --- workspaces -------------------------------------------------------------
 
 struct WsLayout {
-    size_t a, codes, rows, c, part, split_part, kacc, total;
+    size_t a, codes, rows, c, part, split_part, kacc, sync, total;
     size_t split_part_ints;
 };
 
@@ -435,7 +437,8 @@ static WsLayout ws_layout(const Geometry& g, int M) {
     L.split_part_ints = split_need(g, M);
     L.split_part = round_up_z(L.split_part_ints * 4, 256);
     L.kacc = round_up_z(((size_t)g.N_pad + 8) * 8, 256);
-    L.total = L.a + L.codes + 3 * L.rows + L.c + L.part + L.split_part + L.kacc;
+    L.sync = round_up_z((size_t)FFN_SYNC_WORDS * 4, 256);
+    L.total = L.a + L.codes + 3 * L.rows + L.c + L.part + L.split_part + L.kacc + L.sync;
     return L;
 }
 
@@ -482,6 +485,8 @@ Workspace* workspace_create(Domain* d, int bits, int M, int K, int N) {
     ws->split_part_ints = L.split_part_ints;
     off += L.split_part;
     ws->kacc = reinterpret_cast<unsigned long long*>(base + off);
+    off += L.kacc;
+    ws->sync = reinterpret_cast<unsigned*>(base + off);
     // Zero everything once (padding rows of the code planes stay zero).
     bool ok = hipMemset(base, 0, L.total) == hipSuccess &&
               hipStreamCreateWithFlags(&ws->stream, hipStreamNonBlocking) == hipSuccess &&
@@ -908,8 +913,171 @@ int enqueue_linear(Workspace* ws, const Weights* w, const void* x, int x_type, l
     return hipGetLastError() == hipSuccess ? RK_NPU_OK : RK_NPU_ERR_DEVICE;
 }
 
+// --- the FFN of one row in one launch (ffn_m1_kernel, opt-in: HM_FFN_FUSED=1) ------
+// Eligible: one row, a W4 SwiGLU gate_up whose tile pairs take 5 to 8 rounds of
+// the block's 192 weight threads (K in 1600..3072; 2560x19456: 7) with a
+// quantization wave, 16-byte aligned activations, and a down projection split
+// into K pieces of at most 48 (W4) / 40 (W8) units of 64 (3 / 5 rounds of 256
+// threads). Measured on the Qwen3-4B decode FFN (2560 -> 2x9728 -> 2560, W4,
+// 36 distinct layers in a graph, one MI355X): 16.5 us per call against 14.3 us
+// for the gate_up and split-K down launches, so it is not the default. Block
+// timestamps of one call: every block starts within 1.1 us; the gate/up work
+// publishes at 6.2 us (p50) but the last producer only at 8.5 us (the early
+// finishers' down-weight loads compete with it); the arrival chain and the
+// flag reach the down pieces at 11.0 us (p50); quantizing the middle slice
+// (its loads, the barriers) ends at 13.2 us, the dots at 13.8, the split-K
+// sums at 14.3 us: each step is a memory round trip of ~0.5 us under the
+// full weight stream, and together they cost more than the second launch.
+struct FfnFusedPlan {
+    int rwg, rwd, ksplit, piece_units, producers, consumers;
+};
+
+static bool plan_ffn_fused(const Weights* gw, const Weights* dw, const void* A, int a_type, int rows,
+                           FfnFusedPlan& fp) {
+    if (rows != 1 || switch_value(SW_FFN_FUSED) == 0) return false;
+    const Geometry& G = gw->g;
+    const Geometry& Dg = dw->g;
+    if (G.bits != 4 || !G.half || (a_type != DT_F32 && a_type != DT_F16)) return false;
+    if (plan_linear(1, G).kind != 0 || plan_linear(1, Dg).kind != 0) return false;
+    const size_t esz = a_type == DT_F32 ? 4 : 2;
+    if (G.K % 16 != 0 || ((size_t)G.K * esz) % 16 != 0 || (reinterpret_cast<uintptr_t>(A) & 15) != 0) return false;
+    // rounds of the block's weight threads over a gate/up tile pair
+    const int w_rounds = ((G.K_pad / 32) * 8 * 2 + FFN_WEIGHT_THREADS - 1) / FFN_WEIGHT_THREADS;
+    const int qb = a_type == DT_F32 ? gemv_qb<float>() : gemv_qb<__half>();
+    if (w_rounds < 5 || w_rounds > 8 || G.K_pad / 16 > 64 * qb) return false;
+    fp.rwg = w_rounds <= 6 ? 6 : (w_rounds <= 7 ? 7 : 8);
+    // down: pieces of whole 64-k units, about 1280 blocks as the split-K GEMV
+    const int units = Dg.K_pad / 64;
+    const int max_units = Dg.bits == 4 ? 48 : 40;  // 3 / 5 rounds of 256 threads per piece
+    const int groups = Dg.N_pad / 8;
+    int ksplit = std::max(1, std::min((1280 + groups / 2) / groups, 8));
+    const int forced = switch_value(SW_GEMV_SPLITS);
+    if (forced > 0) ksplit = forced;
+    ksplit = std::max(ksplit, (units + max_units - 1) / max_units);
+    ksplit = std::min(ksplit, units);
+    fp.piece_units = (units + ksplit - 1) / ksplit;
+    if (fp.piece_units > max_units) return false;
+    fp.ksplit = ksplit;
+    fp.rwd = Dg.bits == 4 ? 3 : 5;
+    fp.producers = G.N_pad / 16;
+    fp.consumers = groups * ksplit;
+    return true;
+}
+
+// Blocks of the one-launch FFN kernel `fn` that fit the GPU at once with
+// `lds` bytes of dynamic shared memory (0 if unknown), cached per kernel.
+static long ffn_capacity(const void* fn, size_t lds) {
+    static std::mutex mu;
+    static std::map<std::pair<const void*, size_t>, long> cache;
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = cache.find({fn, lds});
+    if (it != cache.end()) return it->second;
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, FFN_THREADS, lds) != hipSuccess) {
+        (void)hipGetLastError();
+        per_cu = 0;
+    }
+    const long cap = (long)per_cu * device_cus();
+    cache[{fn, lds}] = cap;
+    return cap;
+}
+
+template <typename TX, int RWG, int BD>
+static bool launch_ffn_fused(const GemvParams& Pg, const GemvParams& Pd, int grid, size_t lds, hipStream_t s) {
+    constexpr int RWD = BD == 4 ? 3 : 5;
+    const void* fn = reinterpret_cast<const void*>(&ffn_m1_kernel<TX, 4, RWG, BD, RWD>);
+    if (ffn_capacity(fn, lds) < grid) return false;  // must be resident as a whole
+    hipLaunchKernelGGL((ffn_m1_kernel<TX, 4, RWG, BD, RWD>), dim3(grid), dim3(FFN_THREADS), lds, s, Pg, Pd);
+    return true;
+}
+
+template <typename TX, int BD>
+static bool launch_ffn_fused_rw(int rwg, const GemvParams& Pg, const GemvParams& Pd, int grid, size_t lds,
+                                hipStream_t s) {
+    if (rwg == 6) return launch_ffn_fused<TX, 6, BD>(Pg, Pd, grid, lds, s);
+    if (rwg == 7) return launch_ffn_fused<TX, 7, BD>(Pg, Pd, grid, lds, s);
+    return launch_ffn_fused<TX, 8, BD>(Pg, Pd, grid, lds, s);
+}
+
+static GemvParams gemv_params(Workspace* ws, const Weights* w, const void* x, long lda, int rows, int rule, void* c,
+                              int c_type, long ldc) {
+    const Geometry& g = w->g;
+    GemvParams V{};
+    V.x = x;
+    V.lda = lda;
+    V.rule = rule;
+    V.vec = 1;
+    V.b = w->packed;
+    V.colscale = w->colscale;
+    V.c = c;
+    V.ldc = ldc;
+    V.c_type = c_type;
+    V.M = rows;
+    V.K = g.K;
+    V.N = g.N;
+    V.K_pad = g.K_pad;
+    V.N_pad = g.N_pad;
+    V.half = g.half;
+    V.part_out = ws->partmax;
+    V.diag_codes = ws->codes;
+    V.diag_scale = ws->rowscale;
+    V.diag_rowsum = ws->rowsum;
+    V.M_alloc = ws->M_alloc;
+    V.ksplit = 1;
+    V.kacc = ws->kacc;
+    return V;
+}
+
+// Enqueues the one-launch FFN; false (nothing enqueued) when the launch could
+// not be resident as a whole on this GPU.
+static bool enqueue_ffn_fused(Workspace* gws, const Weights* gw, Workspace* dws, const Weights* dw, const void* A,
+                              int a_type, void* C, int c_type, int rule, const FfnFusedPlan& fp, hipStream_t s) {
+    const int F = gw->g.N / 2;
+    GemvParams Pg = gemv_params(gws, gw, A, gw->g.K, 1, rule, gws->c_f32, DT_F32, F);
+    GemvParams Pd = gemv_params(dws, dw, gws->c_f32, F, 1, rule, C, c_type, dw->g.N);
+    Pd.ksplit = fp.ksplit;
+    for (GemvParams* P : {&Pg, &Pd}) {
+        P->sync = dws->sync;
+        P->producers = fp.producers;
+        P->consumers = fp.consumers;
+        P->spin_limit = switch_value(SW_FFN_SPIN);
+    }
+    const int grid = std::max(fp.producers, fp.consumers);
+    const size_t lds = (size_t)gw->g.K_pad + (size_t)64 * fp.piece_units;
+    char name[64];
+    std::snprintf(name, sizeof(name), "ffn_m1<w4,w%d,k/%d>", dw->g.bits, fp.ksplit);
+    const int slot = prof_begin(s, 0, dw->g.bits, EPI_SWIGLU_MAX, 1, gw->g.K, dw->g.N, name);
+    bool launched;
+    if (a_type == DT_F32)
+        launched = dw->g.bits == 4 ? launch_ffn_fused_rw<float, 4>(fp.rwg, Pg, Pd, grid, lds, s)
+                                   : launch_ffn_fused_rw<float, 8>(fp.rwg, Pg, Pd, grid, lds, s);
+    else
+        launched = dw->g.bits == 4 ? launch_ffn_fused_rw<__half, 4>(fp.rwg, Pg, Pd, grid, lds, s)
+                                   : launch_ffn_fused_rw<__half, 8>(fp.rwg, Pg, Pd, grid, lds, s);
+    prof_end(slot, s);
+    return launched;
+}
+
+// The down workspace's one-launch FFN error word: nonzero when a consumer of
+// an earlier call gave up waiting for its producers (its output is then not
+// valid). Reading clears it. The caller has synchronized the stream.
+int ffn_take_error(Workspace* dws) {
+    if (!dws->sync) return RK_NPU_OK;
+    unsigned err = 0;
+    unsigned* word = dws->sync + (4 * FFN_SLOTS + 2) * FFN_LINE;
+    if (hipMemcpy(&err, word, 4, hipMemcpyDeviceToHost) != hipSuccess) return RK_NPU_ERR_DEVICE;
+    if (!err) return RK_NPU_OK;
+    const unsigned zero = 0;
+    (void)hipMemcpy(word, &zero, 4, hipMemcpyHostToDevice);
+    return RK_NPU_ERR_DEVICE;
+}
+
 int enqueue_ffn(Workspace* gws, const Weights* gw, Workspace* dws, const Weights* dw, const void* A, int a_type,
                 void* C, int c_type, int rows, int rule, hipStream_t s) {
+    FfnFusedPlan fp;
+    if (plan_ffn_fused(gw, dw, A, a_type, rows, fp) &&
+        enqueue_ffn_fused(gws, gw, dws, dw, A, a_type, C, c_type, rule, fp, s))
+        return hipGetLastError() == hipSuccess ? RK_NPU_OK : RK_NPU_ERR_DEVICE;
     const int F = gw->g.N / 2;
     RowMax mid_max{nullptr, 0};
     int rc = enqueue_linear(gws, gw, A, a_type, gw->g.K, rows, rule, RowMax{nullptr, 0}, gws->c_f32, DT_F32, F,
@@ -997,6 +1165,7 @@ static bool scratch_workspace(uint8_t* base, const Weights* w, int rows, Workspa
     ws.rowmax = reinterpret_cast<unsigned*>(take((size_t)ws.M_alloc * 4));
     ws.partmax = reinterpret_cast<float*>(take((size_t)g.N_pad * 4));
     ws.kacc = reinterpret_cast<unsigned long long*>(take(((size_t)g.N_pad + 8) * 8));
+    ws.sync = nullptr;  // (a linear call has no one-launch FFN)
     if (off > STATIC_SCRATCH_BYTES) return false;
     // the rest holds split-K partials; plans whose partials do not fit run unsplit
     ws.split_part = reinterpret_cast<int*>(base + off);
@@ -1412,6 +1581,8 @@ int rk_npu_w4a8_run_ffn_f32(rk_npu_w4a8_workspace* gate_up_workspace, const rk_n
     if (timings && hipStreamSynchronize(s) != hipSuccess) return RK_NPU_ERR_DEVICE;
     const double t2 = now_us();
     if (!download_host(st_out, C, dws->c_f32, (size_t)M * H * 4, s)) return RK_NPU_ERR_DEVICE;
+    rc = ffn_take_error(dws);
+    if (rc != RK_NPU_OK) return rc;
     if (timings) {
         const double t3 = now_us();
         timings->upload_us = t1 - t0;
@@ -1548,6 +1719,14 @@ int rk_npu_hip_ffn_run(void* gate_up_workspace, const void* gate_up, int gu_bits
     if (hipSetDevice(device_of(gws->domain)) != hipSuccess) return RK_NPU_ERR_DEVICE;
     hipStream_t s = static_cast<hipStream_t>(stream);
     return enqueue_ffn(gws, gw, dws, dw, A, a_type, C, c_type, rows, QUANT_DENSE, s);
+}
+
+int rk_npu_hip_ffn_status(void* down_workspace, int dn_bits) {
+    Workspace* dws = as_ws(down_workspace, dn_bits);
+    if (!dws) return RK_NPU_ERR_PARAM;
+    if (hipSetDevice(device_of(dws->domain)) != hipSuccess || hipDeviceSynchronize() != hipSuccess)
+        return RK_NPU_ERR_DEVICE;
+    return ffn_take_error(dws);
 }
 
 rk_npu_f32i8f32_weights* rk_npu_hip_f32i8f32_weights_create_device(rk_npu_iommu_domain* domain,

@@ -1195,7 +1195,115 @@ struct GemvParams {
     // way.
     int ksplit;
     unsigned long long* kacc;
+    // One-launch FFN (ffn_m1_kernel): the gate_up blocks (producers) publish
+    // the middle row and its maxima to the down blocks (consumers) of the same
+    // launch through `sync` (FfnSync layout); fuse_block / fuse_blocks are the
+    // block's index in the whole launch and the launch's block count.
+    unsigned* sync;
+    int producers, consumers;
+    int spin_limit;
+    int fuse_block, fuse_blocks;
 };
+
+// Synchronisation words of a one-launch FFN, kept zero between launches (the
+// launch's last block clears them). Arrivals are spread over SLOTS counters
+// so that no address takes more than a few dozen atomics, and every word has
+// its own 64-byte line:
+//   cnt[s]   producers with index % SLOTS == s that published their middle
+//            values and block max (counted after those stores completed)
+//   mx[s]    max |middle| over those producers (float bits, atomic max)
+//   ready    producer slots that are complete; the producer completing the
+//            last one sets the flags
+//   flag[r]  SLOTS replicas of the all-published flag (64-bit), so the down
+//            blocks each poll one line of their own residue class
+//   done[s]  blocks with launch index % SLOTS == s that finished
+//   top      done slots that completed; the block completing the last clears all
+//   err      bit 0: a down block gave up waiting (its spin limit ran out)
+constexpr int FFN_SLOTS = 32;
+constexpr int FFN_LINE = 16;  // words per line (64 bytes)
+constexpr int FFN_SYNC_WORDS = (4 * FFN_SLOTS + 3) * FFN_LINE;
+struct FfnSync {
+    unsigned* base;
+    __device__ unsigned* cnt(int s) const { return base + s * FFN_LINE; }
+    __device__ unsigned* mx(int s) const { return base + (FFN_SLOTS + s) * FFN_LINE; }
+    __device__ unsigned* done(int s) const { return base + (2 * FFN_SLOTS + s) * FFN_LINE; }
+    __device__ unsigned long long* flag(int r) const {
+        return reinterpret_cast<unsigned long long*>(base + (3 * FFN_SLOTS + r) * FFN_LINE);
+    }
+    __device__ unsigned* top() const { return base + 4 * FFN_SLOTS * FFN_LINE; }
+    __device__ unsigned* ready() const { return base + (4 * FFN_SLOTS + 1) * FFN_LINE; }
+    __device__ unsigned* err() const { return base + (4 * FFN_SLOTS + 2) * FFN_LINE; }
+};
+// Blocks i < n with i % FFN_SLOTS == s.
+__device__ __forceinline__ unsigned ffn_slot_count(int n, int s) {
+    return (unsigned)(n / FFN_SLOTS + (s < n % FFN_SLOTS ? 1 : 0));
+}
+
+enum { FUSE_NONE = 0, FUSE_PRODUCER = 1, FUSE_CONSUMER = 2 };
+
+__device__ __forceinline__ unsigned ld_agent(const unsigned* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent(unsigned* p, unsigned v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// A block of a one-launch FFN has finished everything that touches the
+// synchronisation words or the middle row (called by one lane, after its
+// wave's memory operations completed): count it, and let the last block of
+// the launch clear the words for the next launch.
+__device__ __forceinline__ void ffn_block_done(const GemvParams& P) {
+    const FfnSync S{P.sync};
+    const int s = P.fuse_block % FFN_SLOTS;
+    const unsigned was = __hip_atomic_fetch_add(S.done(s), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (was + 1 != ffn_slot_count(P.fuse_blocks, s)) return;
+    const unsigned t = __hip_atomic_fetch_add(S.top(), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if ((int)t + 1 != min(P.fuse_blocks, FFN_SLOTS)) return;
+    for (int i = 0; i < FFN_SLOTS; ++i) {
+        st_agent(S.cnt(i), 0u);
+        st_agent(S.mx(i), 0u);
+        st_agent(S.done(i), 0u);
+        __hip_atomic_store(S.flag(i), 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    st_agent(S.ready(), 0u);
+    st_agent(S.top(), 0u);
+}
+
+// A producer has published (its stores and max completed): count it; the
+// producer that completes the last slot publishes the row max to the flags.
+__device__ __forceinline__ void ffn_producer_arrive(const GemvParams& P, int producer) {
+    const FfnSync S{P.sync};
+    const int s = producer % FFN_SLOTS;
+    const unsigned was = __hip_atomic_fetch_add(S.cnt(s), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (was + 1 != ffn_slot_count(P.producers, s)) return;
+    const unsigned r = __hip_atomic_fetch_add(S.ready(), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if ((int)r + 1 != min(P.producers, FFN_SLOTS)) return;
+    for (int i = 0; i < FFN_SLOTS; ++i)
+        __hip_atomic_store(S.flag(i), 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// A consumer wave waits (one lane polls its flag replica, bounded: past
+// P.spin_limit polls, or at once when it is negative, it flags the error word
+// and goes on) until every producer has published, then returns the row max,
+// the max of the slot maxima (each producer's max completed before its slot
+// did, and every slot before the flag was set).
+__device__ __forceinline__ float ffn_wait_row_max(const GemvParams& P, int lane) {
+    const FfnSync S{P.sync};
+    if (lane == 0) {
+        const unsigned long long* f = S.flag(P.fuse_block % FFN_SLOTS);
+        for (int it = 0;; ++it) {
+            if (P.spin_limit >= 0 && __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0ull) break;
+            if (it >= P.spin_limit) {
+                __hip_atomic_fetch_or(S.err(), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+    }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    const unsigned m = lane < FFN_SLOTS ? ld_agent(S.mx(lane)) : 0u;
+    return wave_max(__uint_as_float(m));
+}
 
 
 // Activation chunks per lane of the quantization wave (QWN = 1 blocks): rows
@@ -1215,7 +1323,7 @@ constexpr int gemv_qb() { return sizeof(T) == 2 ? 4 : 3; }
 // partial-maxima batches of each wave running in series.)
 template <typename T, int MR, int QWN>
 __device__ __forceinline__ void gemv_quant_waves(const GemvParams& P, int8_t* sa, float* s_scale,
-                                                 int (*s_sum)[MR], int qt) {
+                                                 int (*s_sum)[MR], int qt, bool diag) {
     constexpr int QB = gemv_qb<T>();
     constexpr int QT = 64 * QWN;
     constexpr int PB = 8;  // precomputed partial maxima per lane per batch
@@ -1225,12 +1333,14 @@ __device__ __forceinline__ void gemv_quant_waves(const GemvParams& P, int8_t* sa
     // a masked lane reads its own chunk of row 0 (never one shared address)
     const T* spare = x + (size_t)min(qt, (P.K >> 4) - 1) * 16;
     v4u xr[QB][4];
+    {
 #pragma unroll
-    for (int j = 0; j < QB; ++j) {
-        if (QT * j >= chunks) break;
-        const int c = qt + QT * j, kg = c / MR, m = c % MR;
-        const bool ok = c < chunks && m < P.M && kg * 16 < P.K;
-        load16_raw(ok ? x + (size_t)m * P.lda + kg * 16 : spare, xr[j]);
+        for (int j = 0; j < QB; ++j) {
+            if (QT * j >= chunks) break;
+            const int c = qt + QT * j, kg = c / MR, m = c % MR;
+            const bool ok = c < chunks && m < P.M && kg * 16 < P.K;
+            load16_raw(ok ? x + (size_t)m * P.lda + kg * 16 : spare, xr[j]);
+        }
     }
     // words of a chunk the lane does not own (it read its spare chunk) are
     // zeroed once, before both passes
@@ -1288,7 +1398,7 @@ __device__ __forceinline__ void gemv_quant_waves(const GemvParams& P, int8_t* sa
             scale[m] = (v == 0.0f) ? 1.0f : v / 127.0f;
         inv[m] = 1.0f / scale[m];
     }
-    const bool diag = blockIdx.x == 0 && P.diag_codes;
+    diag = diag && P.diag_codes;
     int psum[MR];
 #pragma unroll
     for (int m = 0; m < MR; ++m) psum[m] = 0;
@@ -1321,19 +1431,25 @@ __device__ __forceinline__ void gemv_quant_waves(const GemvParams& P, int8_t* sa
 // QWN = 1: the block has a quantization wave (gemv_quant_waves) before its
 // NTHR weight threads; the rows must fit it (at most 64 * gemv_qb<T>() chunks).
 // SPLITK: the block is one K piece of a group (GemvParams::ksplit).
+// One block of the GEMV: block `bid` of `nblk` along x. FUSE_PRODUCER /
+// FUSE_CONSUMER are the gate_up and down roles in a one-launch FFN
+// (ffn_m1_kernel); FUSE_NONE is the standalone GEMV (gemv_kernel).
 template <typename T, int MR, int BITS, int EPI, int RW, int NW, bool PREQ, int GPB = 1, int NTHR = 256,
-          bool GROUPED = false, int QWN = 0, bool SPLITK = false>
-__global__ __launch_bounds__(NTHR + 64 * QWN) void gemv_kernel(GemvParams P) {
-    extern __shared__ __attribute__((aligned(16))) int8_t sa[];  // [K_pad/16][MR][16] (the piece's K)
+          bool GROUPED = false, int QWN = 0, bool SPLITK = false, int FUSE = FUSE_NONE>
+__device__ __forceinline__ void gemv_block(GemvParams P, const int bid, const int nblk, int8_t* sa) {
+    // sa: [K_pad/16][MR][16] codes (the piece's K) in dynamic shared memory
     // Split K: this block's piece of the 64-k units, the row slice, and where
     // its planes start in the tile.
-    int plane_off = 0, grp = blockIdx.x;
+    int plane_off = 0, grp = bid;
     const int K_pad_full = P.K_pad;
+    static_assert(FUSE == FUSE_NONE || (MR == 1 && GPB == 1 && !PREQ && !GROUPED), "the one-launch FFN runs one row");
+    static_assert(FUSE != FUSE_PRODUCER || (EPI == EPI_SWIGLU_MAX && QWN == 1), "producers: the SwiGLU GEMV, quantization wave");
+    static_assert(FUSE != FUSE_CONSUMER || (SPLITK && QWN == 0), "consumers: split-K pieces quantized by the whole block");
     if constexpr (SPLITK) {
         static_assert(MR == 1 && GPB == 1 && EPI == EPI_PLAIN && !PREQ && !GROUPED && QWN == 0,
                       "split K: one row, plain epilogue, in-block quantization");
-        const int piece = blockIdx.x % P.ksplit;
-        grp = blockIdx.x / P.ksplit;
+        const int piece = bid % P.ksplit;
+        grp = bid / P.ksplit;
         const int U = P.K_pad >> 6;
         const int u0 = U * piece / P.ksplit, u1 = U * (piece + 1) / P.ksplit;
         plane_off = u0 * (BITS == 8 ? 4 : 2);
@@ -1387,7 +1503,7 @@ __global__ __launch_bounds__(NTHR + 64 * QWN) void gemv_kernel(GemvParams P) {
             // instead of queuing behind it (gate/up 2560x19456 W4 M=1: 8.7 us
             // with the wave last at normal priority, 6.5 us first at priority 3).
             __builtin_amdgcn_s_setprio(3);
-            gemv_quant_waves<T, MR, QWN>(P, sa, s_red[0], s_isum, threadIdx.x);
+            gemv_quant_waves<T, MR, QWN>(P, sa, s_red[0], s_isum, threadIdx.x, grp == 0);
             wait_lgkmcnt0();
             __builtin_amdgcn_s_barrier();  // codes, scales and code sums are in LDS
             __builtin_amdgcn_s_barrier();  // (the weight waves' partial sums)
@@ -1402,7 +1518,7 @@ __global__ __launch_bounds__(NTHR + 64 * QWN) void gemv_kernel(GemvParams P) {
     const int NWIN = (CPG + NTHR * RW - 1) / (NTHR * RW);
     const int chunks = KG16 * MR;            // activation chunks (<= NTHR * XMAX unless PREQ)
     const int g0 = grp * GPB;  // first group of the block
-    const int groups = SPLITK ? gridDim.x / P.ksplit : gridDim.x * GPB;
+    const int groups = SPLITK ? nblk / P.ksplit : nblk * GPB;
     // (a tile's planes span the whole K even when the block takes a piece)
     const int CPT_full = (BITS == 8 ? K_pad_full >> 4 : K_pad_full >> 5) * 8;
 
@@ -1453,7 +1569,9 @@ __global__ __launch_bounds__(NTHR + 64 * QWN) void gemv_kernel(GemvParams P) {
     const T* x = static_cast<const T*>(P.x);
 #pragma unroll
     for (int j = 0; j < XMAX; ++j) {
-        if (QW || NTHR * j >= chunks) break;  // (QW: the quantization wave loads the rows)
+        // (QW: the quantization wave loads the rows; a one-launch FFN's down
+        // block loads its middle slice after the producers have published)
+        if (QW || FUSE == FUSE_CONSUMER || NTHR * j >= chunks) break;
         const int c = tid + NTHR * j, kg = c / MR, m = c % MR;
         if (PREQ) {
             const bool ok = c < chunks && m < P.M;
@@ -1504,6 +1622,7 @@ __global__ __launch_bounds__(NTHR + 64 * QWN) void gemv_kernel(GemvParams P) {
 
     float scale[MR];
     int corr[MR];
+    int row_isum[MR];  // the block's code sum of each row (its K piece when split)
     if (PREQ) {
         // 2-3. Rows quantized beforehand: codes to LDS, scales and sums from HBM.
 #pragma unroll
@@ -1522,6 +1641,8 @@ __global__ __launch_bounds__(NTHR + 64 * QWN) void gemv_kernel(GemvParams P) {
             scale[m] = m < P.M ? P.diag_scale[m] : 1.0f;
             corr[m] = (BITS == 4 && m < P.M) ? 8 * P.diag_rowsum[m] : 0;
         }
+#pragma unroll
+        for (int m = 0; m < MR; ++m) row_isum[m] = 0;
         wait_lgkmcnt0();
         __builtin_amdgcn_s_barrier();
     } else if (QW) {
@@ -1534,9 +1655,10 @@ __global__ __launch_bounds__(NTHR + 64 * QWN) void gemv_kernel(GemvParams P) {
 #pragma unroll
             for (int w = 0; w < QWN; ++w) isum += s_isum[w][m];
             corr[m] = BITS == 4 ? 8 * isum : 0;
-            if (blockIdx.x == 0 && P.diag_codes && tid == m && m < P.M) {
+            row_isum[m] = isum;
+            if (grp == 0 && P.diag_codes && tid == m && m < P.M) {
                 P.diag_scale[m] = scale[m];
-                P.diag_rowsum[m] = isum;
+                if (!SPLITK) P.diag_rowsum[m] = isum;  // (split: summed over pieces below)
             }
         }
     } else {
@@ -1545,6 +1667,24 @@ __global__ __launch_bounds__(NTHR + 64 * QWN) void gemv_kernel(GemvParams P) {
         float mx[MR];
 #pragma unroll
         for (int m = 0; m < MR; ++m) mx[m] = 0.0f;
+        if constexpr (FUSE == FUSE_CONSUMER) {
+            // every wave waits for the producers and takes the row max from
+            // their slot maxima; then its threads load their middle chunks
+            // with ordinary loads: no cache can hold a stale copy of the row
+            // (no block of this launch reads it before the flag, the producers
+            // stored it at agent scope before counting themselves, and a
+            // launch never starts with another launch's stale lines, by the
+            // runtime's kernel-boundary ordering), and each XCD's L2 fetches it
+            // once for all the pieces it runs.
+            mx[0] = ffn_wait_row_max(P, lane);
+#pragma unroll
+            for (int j = 0; j < XMAX; ++j) {
+                if (NTHR * j >= chunks) break;
+                const int c = tid + NTHR * j;
+                const bool ok = c < chunks && c * 16 < P.K;
+                load16_raw(ok ? x + (size_t)c * 16 : reinterpret_cast<const T*>(own), xraw[j]);
+            }
+        }
         // words of a chunk the thread does not own (it read its own weight
         // bytes) are zeroed once, before both passes
 #pragma unroll
@@ -1556,7 +1696,9 @@ __global__ __launch_bounds__(NTHR + 64 * QWN) void gemv_kernel(GemvParams P) {
             for (int q = 0; q < (int)sizeof(T); ++q)  // (sizeof(T) 16-byte words per chunk)
                 xraw[j][q] = ok ? xraw[j][q] : v4u{0u, 0u, 0u, 0u};
         }
-        if (P.part_in) {
+        if (FUSE == FUSE_CONSUMER) {
+            // (the row max is already known)
+        } else if (P.part_in) {
 #pragma unroll
             for (int m = 0; m < MR; ++m) {
 #pragma unroll
@@ -1628,8 +1770,10 @@ __global__ __launch_bounds__(NTHR + 64 * QWN) void gemv_kernel(GemvParams P) {
         wait_lgkmcnt0();
         __builtin_amdgcn_s_barrier();
 #pragma unroll
-        for (int m = 0; m < MR; ++m)
-            corr[m] = (BITS == 4) ? 8 * block_isum(m) : 0;
+        for (int m = 0; m < MR; ++m) {
+            row_isum[m] = block_isum(m);
+            corr[m] = (BITS == 4) ? 8 * row_isum[m] : 0;
+        }
         if (grp == 0 && P.diag_codes) {
             for (int c = tid; c < chunks; c += NTHR)
                 *reinterpret_cast<v4u*>(P.diag_codes + ((size_t)(c / MR) * P.M_alloc + c % MR) * 16) =
@@ -1739,21 +1883,23 @@ __global__ __launch_bounds__(NTHR + 64 * QWN) void gemv_kernel(GemvParams P) {
                 const unsigned long long was = __hip_atomic_fetch_add(slot, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 if ((was >> 40) == last) {
                     const long long total = (long long)((was + mine) & LOW) - (long long)(P.ksplit * BIAS);
-                    __hip_atomic_exchange(slot, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    // every piece has added: clear the slot for the next call
+                    __hip_atomic_store(slot, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     const float y = ((float)(int)total * scale[0]) * cs[0];
                     const int p = 8 * tile[0] + c8;
                     if (P.M > 0 && p < P.N) store_out(P.c, P.c_type, orig_col(p, P.half), y);
                 }
             }
             if (lane == 0 && grp == 0 && P.diag_codes) {
-                const unsigned long long sm = ONE + (unsigned long long)((long long)block_isum(0) + (long long)BIAS);
+                const unsigned long long sm = ONE + (unsigned long long)((long long)row_isum[0] + (long long)BIAS);
                 unsigned long long* row_slot = P.kacc + P.N_pad;
                 const unsigned long long was = __hip_atomic_fetch_add(row_slot, sm, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 if ((was >> 40) == last) {
                     P.diag_rowsum[0] = (int)((long long)((was + sm) & LOW) - (long long)(P.ksplit * BIAS));
-                    __hip_atomic_exchange(row_slot, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_store(row_slot, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 }
             }
+
         }
         return;
     }
@@ -1779,17 +1925,80 @@ __global__ __launch_bounds__(NTHR + 64 * QWN) void gemv_kernel(GemvParams P) {
                         store_out(P.c, P.c_type, (size_t)m * P.ldc + orig_col(p, P.half), y[0]);
                 } else {
                     const float o = hm_swiglu(y[0], y[TPG - 1]);
-                    if (lane < 8 && row_ok && p < P.N)
-                        store_out(P.c, P.c_type, (size_t)m * P.ldc + ((p >> 6) << 5) + (p & 31), o);
+                    const size_t oi = (size_t)m * P.ldc + ((p >> 6) << 5) + (p & 31);
+                    if constexpr (FUSE == FUSE_PRODUCER) {
+                        // f32 middle, stored at agent scope for the consumers
+                        if (lane < 8 && row_ok && p < P.N)
+                            __hip_atomic_store(static_cast<float*>(P.c) + oi, o, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+                    } else {
+                        if (lane < 8 && row_ok && p < P.N) store_out(P.c, P.c_type, oi, o);
+                    }
                     if (EPI == EPI_SWIGLU_MAX) {
                         float mxo = (lane < 8 && p < P.N) ? fabsf(o) : 0.0f;
                         mxo = max8(mxo);
-                        if (lane == 0) P.part_out[(size_t)m * groups + g] = row_ok ? mxo : 0.0f;
+                        if constexpr (FUSE == FUSE_PRODUCER) {
+                            if (lane == 0 && row_ok)
+                                __hip_atomic_fetch_max(FfnSync{P.sync}.mx(bid % FFN_SLOTS), __float_as_uint(mxo),
+                                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        } else {
+                            if (lane == 0) P.part_out[(size_t)m * groups + g] = row_ok ? mxo : 0.0f;
+                        }
                     }
                 }
             }
         }
+        if constexpr (FUSE == FUSE_PRODUCER) {
+            // Publish: the middle values and the max have completed at agent
+            // scope before the arrival is counted.
+            wait_vmcnt<0>();
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            if (lane == 0) ffn_producer_arrive(P, bid);
+        }
     }
+}
+
+template <typename T, int MR, int BITS, int EPI, int RW, int NW, bool PREQ, int GPB = 1, int NTHR = 256,
+          bool GROUPED = false, int QWN = 0, bool SPLITK = false>
+__global__ __launch_bounds__(NTHR + 64 * QWN) void gemv_kernel(GemvParams P) {
+    extern __shared__ __attribute__((aligned(16))) int8_t sa[];
+    gemv_block<T, MR, BITS, EPI, RW, NW, PREQ, GPB, NTHR, GROUPED, QWN, SPLITK>(P, blockIdx.x, gridDim.x, sa);
+}
+
+// The FFN of one row in one launch. Block b first computes gate/up tile pair
+// b (b < G.producers: a quantization wave and 192 weight threads, `RWG`
+// rounds of weights, the SwiGLU middle values published at agent scope),
+// then K piece b of the down projection (b < Dn.consumers: 256 threads,
+// `RWD` rounds): it requests that piece's weights at once, waits (bounded)
+// until every producer has published, quantizes its slice of the middle with
+// the row's max and adds its split-K sums. Every block's down weights stream
+// right after its own gate/up work, and no block holds a CU slot idle. The
+// launch must be resident as a whole (the plan checks the occupancy), since a
+// block waits for producers that may run later in launch order; if it is not
+// (another workload holding CUs), the wait runs out and the error word says
+// so. Results are bit-identical to the two-launch FFN: the same quantization,
+// products and epilogues, with the middle's max taken over the producers'
+// block maxima.
+// Blocks of 256 threads, one wave per SIMD (five-wave blocks fit four, not
+// five, to a CU here).
+constexpr int FFN_WEIGHT_THREADS = 192;
+constexpr int FFN_THREADS = FFN_WEIGHT_THREADS + 64;
+template <typename TX, int BG, int RWG, int BD, int RWD>
+__global__ __launch_bounds__(FFN_THREADS) void ffn_m1_kernel(GemvParams G, GemvParams Dn) {
+    extern __shared__ __attribute__((aligned(16))) int8_t sa[];
+    const int b = blockIdx.x;
+    G.fuse_block = Dn.fuse_block = b;
+    G.fuse_blocks = Dn.fuse_blocks = gridDim.x;
+    if (b < G.producers)
+        gemv_block<TX, 1, BG, EPI_SWIGLU_MAX, RWG, 1, false, 1, FFN_WEIGHT_THREADS, false, 1, false, FUSE_PRODUCER>(
+            G, b, G.producers, sa);
+    // (the producers' codes stay in the first K_pad bytes: some of its waves
+    // may still read them while others start on the piece)
+    if (b < Dn.consumers)
+        gemv_block<float, 1, BD, EPI_PLAIN, RWD, 1, false, 1, FFN_THREADS, false, 0, true, FUSE_CONSUMER>(
+            Dn, b, Dn.consumers, sa + G.K_pad);
+    __syncthreads();
+    if (threadIdx.x == 0) ffn_block_done(G);
 }
 
 }  // namespace hm

@@ -1,0 +1,100 @@
+// Roofline probes (rk_npu_hip_stream_probe, rk_npu_hip_mfma_probe): kernels
+// that measure the two ceilings the hot path is judged against on the box
+// it runs on, so the floors quoted for each projection come from committed
+// code. They compute nothing the library uses.
+//   stream: read `bytes` of device memory once with 16-byte non-temporal
+//     loads (the GEMV's load instruction) in one launch of a chosen grid, or
+//     launch the same grid with no loads (the launch's fixed cost);
+//   mfma: back-to-back independent v_mfma_i32_32x32x32_i8 from registers
+//     (no memory traffic): the dense int8 matrix-core rate the clock allows.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "../../include/rk_npu_hip.h"
+
+namespace hm {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+// Thread t of the grid reads chunks t, t + T, t + 2T, ... (T = all threads):
+// every wave load is one contiguous KB. The xor of the words is reduced per
+// block and stored, so the loads cannot be removed.
+__global__ __launch_bounds__(512) void stream_probe_kernel(const v4u* __restrict__ src, size_t chunks, int read,
+                                                           unsigned* __restrict__ sink) {
+    __shared__ unsigned s_x[8];
+    const size_t T = (size_t)gridDim.x * blockDim.x;
+    unsigned x = 0;
+    if (read) {
+        size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+        // four loads in flight per thread before the first use
+        for (; i + 3 * T < chunks; i += 4 * T) {
+            const v4u a = __builtin_nontemporal_load(src + i);
+            const v4u b = __builtin_nontemporal_load(src + i + T);
+            const v4u c = __builtin_nontemporal_load(src + i + 2 * T);
+            const v4u d = __builtin_nontemporal_load(src + i + 3 * T);
+            x ^= a.x ^ a.y ^ a.z ^ a.w ^ b.x ^ b.y ^ b.z ^ b.w ^ c.x ^ c.y ^ c.z ^ c.w ^ d.x ^ d.y ^ d.z ^ d.w;
+        }
+        for (; i < chunks; i += T) {
+            const v4u a = __builtin_nontemporal_load(src + i);
+            x ^= a.x ^ a.y ^ a.z ^ a.w;
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) x ^= __shfl_xor(x, off);
+    if ((threadIdx.x & 63) == 0) s_x[threadIdx.x >> 6] = x;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned v = 0;
+        for (int w = 0; w < (int)(blockDim.x >> 6); ++w) v ^= s_x[w];
+        sink[blockIdx.x] = v;
+    }
+}
+
+// Each wave keeps 8 independent 32x32 int32 accumulators and issues
+// `iters` rounds of 8 MFMAs on operands held in registers.
+__global__ __launch_bounds__(256) void mfma_probe_kernel(int iters, int* __restrict__ sink) {
+    v16i acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[j][r] = 0;
+    const int t = threadIdx.x;
+    v4i a = {t, t + 1, t + 2, t + 3}, b = {t ^ 5, t ^ 6, t ^ 7, t ^ 9};
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, acc[j], 0, 0, 0);
+    }
+    int s = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s += acc[j][r];
+    sink[(size_t)blockIdx.x * blockDim.x + t] = s;
+}
+
+}  // namespace hm
+
+using namespace hm;
+
+extern "C" {
+
+int rk_npu_hip_stream_probe(const void* src, uint64_t bytes, int blocks, int threads, int read, uint32_t* sink,
+                            void* stream) {
+    if (blocks < 1 || blocks > (1 << 20) || threads < 64 || threads > 512 || threads % 64 != 0 ||
+        !sink || (read && (!src || (reinterpret_cast<uintptr_t>(src) & 15) != 0)))
+        return RK_NPU_ERR_PARAM;
+    hipLaunchKernelGGL(stream_probe_kernel, dim3(blocks), dim3(threads), 0, static_cast<hipStream_t>(stream),
+                       static_cast<const v4u*>(src), (size_t)(read ? bytes / 16 : 0), read, sink);
+    return hipGetLastError() == hipSuccess ? RK_NPU_OK : RK_NPU_ERR_DEVICE;
+}
+
+int rk_npu_hip_mfma_probe(int blocks, int iters, int32_t* sink, void* stream) {
+    if (blocks < 1 || blocks > (1 << 20) || iters < 1 || !sink) return RK_NPU_ERR_PARAM;
+    hipLaunchKernelGGL(mfma_probe_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream), iters, sink);
+    return hipGetLastError() == hipSuccess ? RK_NPU_OK : RK_NPU_ERR_DEVICE;
+}
+
+}  // extern "C"

@@ -86,6 +86,7 @@ struct Workspace {
     int* split_part;        // split-K int32 partials [pieces][tiles][tile ints]
     size_t split_part_ints; // partial ints available
     unsigned long long* kacc;  // split-K GEMV column slots [N_pad] + row code-sum slot, kept zero between calls
+    unsigned* sync;            // one-launch FFN synchronisation words (FfnSync), kept zero between calls
     // pinned host staging of the host-buffer calls (allocated on first use)
     void* host_stage;
     size_t host_stage_bytes;
@@ -132,6 +133,10 @@ int enqueue_linear(Workspace* ws, const Weights* w, const void* x, int x_type, l
 // gate_up (SwiGLU + row max) -> requant of the middle (same rule) -> down.
 int enqueue_ffn(Workspace* gws, const Weights* gw, Workspace* dws, const Weights* dw, const void* A, int a_type,
                 void* C, int c_type, int rows, int rule, hipStream_t s);
+
+// RK_NPU_ERR_DEVICE (and cleared) when a one-launch FFN on this down
+// workspace gave up waiting for its gate_up blocks since the last check.
+int ffn_take_error(Workspace* dws);
 
 int device_of(Domain* d);
 struct BusyGuard {
