@@ -18,16 +18,24 @@ runs) between two HIP events; the faster valid one is used, both are reported.
 roofline: the dominant kernel's algorithmic bytes (or ops) per launch over its
 average launch time: 36 back-to-back launches of that kernel alone (distinct
 layers' weights) captured in a graph and timed with HIP events on the replay
-stream.
+stream. `--roofline-only` runs only these passes (every line's, and the
+per-projection passes of the decode and prefill sets), so a kernel-trace
+profile of that command holds the same launches; `--summarize-trace CSV`
+turns such a trace into per-kernel averages.
 cpu_baseline: the C oracle (OpenMP) on a bounded sample of the same workload
-on this host's cores.
+on this host's cores: one warm-up, then the median of at least 5 timed
+repetitions, with the CPU model, the cores visible to the process and the
+OpenMP thread count.
 """
 from __future__ import annotations
 
 import argparse
+import csv
+import functools
 import json
 import math
 import os
+import statistics
 import sys
 import time
 
@@ -38,6 +46,7 @@ if ROOT not in sys.path:
 METRIC = "int8 TOPS (% MFMA peak) at M=512/4096 prefill; HBM GB/s at M=1 decode"
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0
+F16_PEAK_TFLOPS = 2500.0
 
 # Qwen3-4B layer shapes
 H, Q, KV, F, LAYERS, VOCAB = 2560, 4096, 1024, 9728, 36, 151936
@@ -157,17 +166,73 @@ def graph_time(torch, fn, reps, check=None):
 # what the same counter reads for a 268,435,456-byte device copy in the same
 # run: FETCH_SIZE 131,090.2 KiB (factor 2.0), WRITE_SIZE 262,144 KiB (factor 1.0).
 # Summary and commands: profiles/traffic_gemv_gate_up_m1.txt.
-TRAFFIC_GEMV_GATE_UP_M1 = int(round((12431.0 * 2.0 + 81.0625 * 1.0) * 1024))
+TRAFFIC_GEMV_GATE_UP = {1: int(round((12431.0 * 2.0 + 81.0625 * 1.0) * 1024))}
 
 
-def roofline(achieved, bound, kernel, avg_us, work, launches, method, traffic=None):
+ROOF_METHOD = "graph of 36 back-to-back launches (distinct weights), HIP events on the replay stream"
+
+
+def roofline(achieved, bound, kernel, avg_us, work, launches, method=ROOF_METHOD, traffic=None, peak=None):
     if bound == "hbm":
-        peak, unit = HBM_PEAK_GBS, "GB/s"
+        peak, unit = peak or HBM_PEAK_GBS, "GB/s"
     else:
-        peak, unit = INT8_PEAK_TOPS, "TFLOP/s"
+        peak, unit = peak or INT8_PEAK_TOPS, "TFLOP/s"
     return {"bound": bound, "kernel": kernel, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
             "frac": round(achieved / peak, 4), "traffic": traffic, "avg_us": round(avg_us, 3),
             "work_per_launch": work, "launches": launches, "method": method}
+
+
+def roof_of(bound, kernel, work, us, launches, method=ROOF_METHOD, traffic=None, peak=None):
+    """roofline() from algorithmic work per launch (bytes for "hbm", ops for
+    "mfma") and the average launch time in microseconds."""
+    scale = 1e9 if bound == "hbm" else 1e12
+    return roofline(work / (us * 1e-6) / scale, bound, kernel, us, work, launches, method, traffic, peak)
+
+
+def per_launch_us(torch, fns, reps):
+    """Average time per launch of the calls fns[i]() (each one library call,
+    normally on its own weights), captured back to back in one HIP graph and
+    replayed `reps` times between two HIP events on the replay stream."""
+    def run():
+        for f in fns:
+            f()
+    ms, _ = graph_time(torch, run, reps)
+    return ms * 1e3 / len(fns)
+
+
+def cpu_info():
+    """The host facts every CPU baseline carries: CPU model name, cores
+    visible to this process (and in the machine), the oracle's OpenMP threads."""
+    from oracle import oracle
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"model": model, "nproc": len(os.sched_getaffinity(0)), "cpu_count": os.cpu_count(),
+            "omp_threads": oracle.threads(), "OMP_NUM_THREADS": os.environ.get("OMP_NUM_THREADS")}
+
+
+def cpu_median(fn, budget_s, min_reps=5):
+    """One warm-up call, then timed calls until both `min_reps` calls and
+    `budget_s` seconds are done: (median seconds per call, calls timed)."""
+    fn()
+    times, t_start = [], time.perf_counter()
+    while len(times) < min_reps or time.perf_counter() - t_start < budget_s:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
+
+
+def cpu_baseline(value, unit, sec, reps, sample, **extra):
+    info = cpu_info()
+    return {"value": round(value, 3), "unit": unit, "cores": info["omp_threads"], "kind": "port",
+            "sample": sample, "ms": round(sec * 1e3, 3), "reps": reps, **extra, **info}
 
 
 # ---------------------------------------------------------------------------------
@@ -224,7 +289,7 @@ class DenseLayers:
 
 
 def cpu_decode_baseline(layer0, rows, budget_s=10.0):
-    """Oracle (C, OpenMP) on layer 0's decode set, repeated for ~budget_s."""
+    """Oracle (C, OpenMP) on layer 0's decode set, timed as cpu_median()."""
     import numpy as np
     from oracle import oracle
     g = np.random.default_rng(1)
@@ -232,101 +297,178 @@ def cpu_decode_baseline(layer0, rows, budget_s=10.0):
     xo = g.standard_normal((rows, Q)).astype(np.float16).astype(np.float32)
     qkv, o, gu, dn = (layer0[n] for n in ("qkv", "o", "gate_up", "down"))
     bytes_layer = sum(lin_bytes(b, c.shape[0], c.shape[1], rows) for b, c, _ in (qkv, o, gu, dn))
-    reps, t0 = 0, time.perf_counter()
-    while True:
+
+    def one():
         oracle.linear(qkv[1], qkv[2], x)
         oracle.linear(o[1], o[2], xo)
         oracle.ffn(gu[1], gu[2], dn[1], dn[2], x)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s:
-            break
-    return {"value": round(bytes_layer * reps / el / 1e9, 3), "unit": "GB/s", "cores": oracle.threads(),
-            "kind": "port",
-            "sample": f"layer 0 of 36, M={rows} decode set (qkv, o, gate_up+SwiGLU->requant->down), "
-                      f"{reps} repetitions in {el:.1f} s; same algorithmic-byte count as the GPU line"}
+
+    sec, reps = cpu_median(one, budget_s)
+    return cpu_baseline(bytes_layer / sec / 1e9, "GB/s", sec, reps,
+                        f"layer 0 of 36, M={rows} decode set (qkv, o, gate_up+SwiGLU->requant->down); "
+                        f"same algorithmic-byte count as the GPU line; ms is per layer",
+                        ms_step_x36=round(sec * 1e3 * LAYERS, 2))
 
 
-def run_decode(torch, ctx, rows, steps, warmup, want_cpu, want_roofline=True):
-    from open_rknpu2_lm_infer_amd import device as D
+def decode_passes(torch, ctx, t, reps):
+    """Per-projection launch times of a decode set (36 launches each, one per
+    layer, in a graph): qkv, o, gate_up (+SwiGLU, fp16 out) and the FFN call
+    (gate_up + SwiGLU + row max, then the down launch that requantizes the
+    middle); the down launch's time is the FFN call's minus gate_up's."""
+    D, r = t.D, t.rows
+    mid = torch.empty(r, F, dtype=torch.float16, device="cuda")
+    specs = (
+        ("qkv", lambda m: D.linear(ctx, m["qkv"], t.x_qkv, t.y_qkv, r, ws=t.ws["qkv"]),
+         lin_bytes(4, H, Q + 2 * KV, r)),
+        ("o", lambda m: D.linear(ctx, m["o"], t.x_o, t.y_o, r, ws=t.ws["o"]), lin_bytes(4, Q, H, r)),
+        ("gate_up", lambda m: D.linear(ctx, m["gate_up"], t.x_ffn, mid, r, swiglu=True, ws=t.ws["gate_up"]),
+         lin_bytes(4, H, 2 * F, r)),
+        ("ffn call", lambda m: D.ffn(ctx, m["gate_up"], m["down"], t.x_ffn, t.y_ffn, r, gws=t.ws["gate_up"],
+                                     dws=t.ws["down"]), lin_bytes(4, H, 2 * F, r) + lin_bytes(4, F, H, r)),
+    )
+    out = {}
+    for name, fn, work in specs:
+        us = per_launch_us(torch, [functools.partial(fn, m) for m in t.w], reps)
+        out[name] = {"us": round(us, 3), "bytes": work, "gbs": round(work / us / 1e3, 1),
+                     "frac_hbm": round(work / us / 1e3 / HBM_PEAK_GBS, 4)}
+    us_dn = out["ffn call"]["us"] - out["gate_up"]["us"]
+    dn = lin_bytes(4, F, H, r)
+    out["down (ffn call - gate_up)"] = {"us": round(us_dn, 3), "bytes": dn, "gbs": round(dn / us_dn / 1e3, 1),
+                                        "frac_hbm": round(dn / us_dn / 1e3 / HBM_PEAK_GBS, 4)}
+    return out
+
+
+def run_decode(torch, ctx, rows, steps, warmup, want_cpu, want_roofline=True, timed=True, reps=None):
     gen = Gen(torch, 1)
     log(f"[bench] decode M={rows}: creating 36 layers of W4 weights")
     t = DenseLayers(torch, ctx, gen, rows, (4, 4, 4, 4), tag=f"dec{rows}")
     nbytes = t.bytes_per_layer() * LAYERS
-    ms_eager = time_steps(torch, t.step, steps, warmup)
-    check = lambda: [t.y_qkv.clone(), t.y_o.clone(), t.y_ffn.clone()]
-    ms_graph, ok = graph_time(torch, t.step, steps, check)
-    ms = min(ms_graph, ms_eager) if ok else ms_eager
-    out = {"ms_per_step": ms, "value": nbytes / (ms * 1e-3) / 1e9, "bytes_per_step": nbytes,
-           "ms_eager": ms_eager, "ms_graph": ms_graph, "graph_matches_eager": ok}
-    log(f"[bench] decode M={rows}: eager {ms_eager:.3f} ms/step, graph {ms_graph:.3f} ms/step "
-        f"(replay bit-exact: {ok}) -> {out['value']:.1f} GB/s")
+    out = {"bytes_per_step": nbytes}
+    if timed:
+        ms_eager = time_steps(torch, t.step, steps, warmup)
+        check = lambda: [t.y_qkv.clone(), t.y_o.clone(), t.y_ffn.clone()]
+        ms_graph, ok = graph_time(torch, t.step, steps, check)
+        ms = min(ms_graph, ms_eager) if ok else ms_eager
+        out.update({"ms_per_step": ms, "value": nbytes / (ms * 1e-3) / 1e9, "ms_eager": ms_eager,
+                    "ms_graph": ms_graph, "graph_matches_eager": ok})
+        log(f"[bench] decode M={rows}: eager {ms_eager:.3f} ms/step, graph {ms_graph:.3f} ms/step "
+            f"(replay bit-exact: {ok}) -> {out['value']:.1f} GB/s")
     if want_roofline:
-        # Dominant kernel: the gate_up GEMV (25 MB of W4 weights per launch),
-        # the same kernel the fused FFN launches. 36 launches on distinct
-        # layers' weights, graph-captured, between two events.
-        gu = [mats["gate_up"] for mats in t.w]
-        mid = torch.empty(rows, F, dtype=torch.float16, device="cuda")
-        ws = t.ws["gate_up"]
-        def gu_run():
-            for w in gu:
-                D.linear(ctx, w, t.x_ffn, mid, rows, swiglu=True, ws=ws)
-        ms_gu, _ = graph_time(torch, gu_run, steps)
-        per_launch_us = ms_gu * 1e3 / len(gu)
-        work = lin_bytes(4, H, 2 * F, rows)
-        out["roofline"] = roofline(work / (per_launch_us * 1e-6) / 1e9, "hbm",
-                                   f"gemv_kernel<__half,{rows if rows in (1, 2, 4) else 8},4,SwiGLU> "
-                                   f"gate_up 2560x19456 W4, M={rows}", per_launch_us, work, len(gu) * steps,
-                                   "graph of 36 back-to-back launches (distinct weights), HIP events on the replay stream",
-                                   TRAFFIC_GEMV_GATE_UP_M1 if rows == 1 else None)
+        # Dominant kernel: the gate_up GEMV (25 MB of W4 weights per launch).
+        passes = decode_passes(torch, ctx, t, reps or steps)
+        gu = passes["gate_up"]
+        out["projections"] = passes
+        out["roofline"] = roof_of("hbm", f"gemv_kernel (W4, SwiGLU epilogue) gate_up 2560x19456, M={rows}",
+                                  gu["bytes"], gu["us"], LAYERS * (reps or steps),
+                                  traffic=TRAFFIC_GEMV_GATE_UP.get(rows))
+        log(f"[bench] decode M={rows} projections: {passes}")
         log(f"[bench] decode roofline: {out['roofline']}")
     if want_cpu:
-        log("[bench] cpu baseline (oracle) on layer 0 ...")
-        out["cpu_baseline"] = cpu_decode_baseline(t.host0, rows)
+        log(f"[bench] cpu baseline (oracle) on layer 0, M={rows} ...")
+        out["cpu_baseline"] = cpu_decode_baseline(t.host0, rows, 10.0 if rows == 1 else 4.0)
         log(f"[bench] cpu baseline: {out['cpu_baseline']}")
     del t
     return out
 
 
-def run_prefill(torch, ctx, rows, steps, warmup):
+def prefill_passes(torch, ctx, t, head, y_head, ws_head, reps):
+    """Per-projection launch times of the M=4096 set: each entry is 36
+    back-to-back library calls (quantization launch + GEMM launch) on the 36
+    layers' weights (the lm_head: 4 calls on its one weight set, 389 MB, more
+    than the last-level cache holds), in a graph."""
+    D, r = t.D, t.rows
+    mid = torch.empty(r, F, dtype=torch.float16, device="cuda")
+    specs = (
+        ("qkv W8", lambda m: D.linear(ctx, m["qkv"], t.x_qkv, t.y_qkv, r, ws=t.ws["qkv"]), 2.0 * r * H * (Q + 2 * KV)),
+        ("o W8", lambda m: D.linear(ctx, m["o"], t.x_o, t.y_o, r, ws=t.ws["o"]), 2.0 * r * Q * H),
+        ("gate_up W4 +SwiGLU", lambda m: D.linear(ctx, m["gate_up"], t.x_ffn, mid, r, swiglu=True,
+                                                  ws=t.ws["gate_up"]), 2.0 * r * H * 2 * F),
+        ("ffn call (gate_up W4 + down W8)", lambda m: D.ffn(ctx, m["gate_up"], m["down"], t.x_ffn, t.y_ffn, r,
+                                                            gws=t.ws["gate_up"], dws=t.ws["down"]),
+         2.0 * r * (H * 2 * F + F * H)),
+    )
+    out = {}
+    for name, fn, work in specs:
+        us = per_launch_us(torch, [functools.partial(fn, m) for m in t.w], reps)
+        out[name] = {"us": round(us, 2), "ops": work, "tops": round(work / us / 1e6, 1),
+                     "frac_int8": round(work / us / 1e6 / INT8_PEAK_TOPS, 4)}
+    us = per_launch_us(torch, [lambda: D.linear(ctx, head, t.x_qkv, y_head, r, ws=ws_head)] * 4, reps)
+    work = 2.0 * r * H * VOCAB
+    out["lm_head W8"] = {"us": round(us, 2), "ops": work, "tops": round(work / us / 1e6, 1),
+                         "frac_int8": round(work / us / 1e6 / INT8_PEAK_TOPS, 4)}
+    gu, fc = out["gate_up W4 +SwiGLU"], out["ffn call (gate_up W4 + down W8)"]
+    us_dn, work = fc["us"] - gu["us"], 2.0 * r * F * H
+    out["down W8 (ffn call - gate_up)"] = {"us": round(us_dn, 2), "ops": work, "tops": round(work / us_dn / 1e6, 1),
+                                           "frac_int8": round(work / us_dn / 1e6 / INT8_PEAK_TOPS, 4)}
+    return out
+
+
+def cpu_prefill_baseline(t, head_host, x_rows, budget_s=8.0):
+    """Oracle on a 64-row sample of layer 0 (qkv, o, FFN) and of the lm_head;
+    ms_step_extrapolated = (36 x layer + lm_head) x 4096 / 64."""
+    from oracle import oracle
+    x, xo = x_rows
+    (qb, qc, qs), (ob, oc, os_), (gb, gc, gs), (db, dc, ds) = (t.host0[n] for n in ("qkv", "o", "gate_up", "down"))
+
+    def layer():
+        oracle.linear(qc, qs, x)
+        oracle.linear(oc, os_, xo)
+        oracle.ffn(gc, gs, dc, ds, x)
+
+    sec_l, reps_l = cpu_median(layer, budget_s / 2)
+    sec_h, reps_h = cpu_median(lambda: oracle.linear(head_host[0], head_host[1], x), budget_s / 2)
+    rows = x.shape[0]
+    ops = 2.0 * rows * (H * (Q + 2 * KV) + Q * H + H * 2 * F + F * H) + 2.0 * rows * H * VOCAB
+    sec = sec_l + sec_h
+    return cpu_baseline(ops / sec / 1e12, "TOPS", sec, min(reps_l, reps_h),
+                        f"{rows} of 4096 rows: layer 0 (qkv, o, gate_up+SwiGLU->requant->down) and the lm_head, "
+                        f"medians {sec_l * 1e3:.1f} + {sec_h * 1e3:.1f} ms",
+                        ms_step_extrapolated=round((LAYERS * sec_l + sec_h) * 1e3 * 4096 / rows, 1))
+
+
+def run_prefill(torch, ctx, rows, steps, warmup, want_cpu=True, timed=True, reps=None):
     """Config 3: M=4096, qkv/o/down W8A8, gate_up W4A8, 36 layers + lm_head W8."""
     from open_rknpu2_lm_infer_amd import device as D
     gen = Gen(torch, 3)
     log(f"[bench] prefill M={rows}: creating 36 layers + lm_head")
     t = DenseLayers(torch, ctx, gen, rows, (8, 8, 4, 8), outliers=True, tag="pf")
-    head = ctx.weights(8, gen.codes("pf/lm_head", 8, H, VOCAB), gen.scales("pf/lm_head", VOCAB))
+    head_codes = gen.codes("pf/lm_head", 8, H, VOCAB)
+    head_scales = gen.scales("pf/lm_head", VOCAB)
+    head = ctx.weights(8, head_codes, head_scales)
+    head_host = (head_codes.cpu().numpy(), head_scales.cpu().numpy()) if want_cpu else None
+    del head_codes, head_scales
     y_head = torch.empty(rows, VOCAB, dtype=torch.float16, device="cuda")
     ws_head = ctx.workspace(8, rows, H, VOCAB)
-
-    def step():
-        t.step()
-        D.linear(ctx, head, t.x_qkv, y_head, rows, ws=ws_head)
-
-    ms, ms_eager, ms_graph, ok = best_time(torch, step, steps, warmup,
-                                           lambda: [t.y_qkv.clone(), t.y_ffn.clone(), y_head.clone()])
     ops = t.ops_per_layer() * LAYERS + 2.0 * rows * H * VOCAB
-    # dominant kernel: the W4 gate_up GEMM with fused SwiGLU, 36 launches on
-    # the 36 layers' weights in a graph; each linear also launches its
-    # activation quantization (about 5% of the pair), which the time includes.
-    gu = [mats["gate_up"] for mats in t.w]
-    mid = torch.empty(rows, F, dtype=torch.float16, device="cuda")
-    def gu_run():
-        for w in gu:
-            D.linear(ctx, w, t.x_ffn, mid, rows, swiglu=True, ws=t.ws["gate_up"])
-    ms_gu, _ = graph_time(torch, gu_run, max(2, steps // 2))
-    per_us = ms_gu * 1e3 / len(gu)
-    launches = len(gu)
-    work = 2.0 * rows * H * 2 * F
-    res = {"workload": f"prefill M={rows}: Qwen3-4B qkv/o/down W8A8 + gate_up W4A8 (+SwiGLU) x36 + lm_head W8A8",
-           "value": round(ops / (ms * 1e-3) / 1e12, 2), "unit": "TOPS", "ms_per_step": round(ms, 3),
-           "frac_of_int8_peak": round(ops / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4),
-           "ms_eager": round(ms_eager, 3), "ms_graph": round(ms_graph, 3), "graph_matches_eager": ok,
-           "roofline": roofline(work / (per_us * 1e-6) / 1e12, "mfma",
-                                f"gemm_kernel<128,128,2,2,W4,SwiGLU> gate_up 2560x19456, M={rows}", per_us, work,
-                                launches, "graph of 36 back-to-back quantization + GEMM launch pairs, HIP events "
-                                "on the replay stream"),
-           "vendor_ref": vendor_int8_gemm(torch, rows, H, 2 * F)}
-    log(f"[bench] prefill: {res['value']} TOPS ({ms:.2f} ms/step); vendor int8 GEMM {res['vendor_ref']}")
+    res = {"workload": f"prefill M={rows}: Qwen3-4B qkv/o/down W8A8 + gate_up W4A8 (+SwiGLU) x36 + lm_head W8A8"}
+    if timed:
+        def step():
+            t.step()
+            D.linear(ctx, head, t.x_qkv, y_head, rows, ws=ws_head)
+
+        ms, ms_eager, ms_graph, ok = best_time(torch, step, steps, warmup,
+                                               lambda: [t.y_qkv.clone(), t.y_ffn.clone(), y_head.clone()])
+        res.update({"value": round(ops / (ms * 1e-3) / 1e12, 2), "unit": "TOPS", "ms_per_step": round(ms, 3),
+                    "frac_of_int8_peak": round(ops / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4),
+                    "ms_eager": round(ms_eager, 3), "ms_graph": round(ms_graph, 3), "graph_matches_eager": ok})
+    # dominant kernel: the W4 gate_up GEMM with fused SwiGLU; each library
+    # call also launches its activation quantization, which the time includes.
+    passes = prefill_passes(torch, ctx, t, head, y_head, ws_head, reps or max(2, steps // 2))
+    gu = passes["gate_up W4 +SwiGLU"]
+    res["projections"] = passes
+    res["roofline"] = roof_of("mfma", f"gemm_kernel (W4, SwiGLU epilogue) gate_up 2560x19456, M={rows}, "
+                                      "with its quantization launch", gu["ops"], gu["us"],
+                              LAYERS * (reps or max(2, steps // 2)),
+                              method="graph of 36 back-to-back quantization + GEMM launch pairs (distinct weights), "
+                                     "HIP events on the replay stream")
+    if timed:
+        res["vendor_ref"] = vendor_int8_gemm(torch, rows, H, 2 * F)
+        log(f"[bench] prefill: {res['value']} TOPS ({ms:.2f} ms/step); vendor int8 GEMM {res['vendor_ref']}")
+    log(f"[bench] prefill projections: {passes}")
+    if want_cpu:
+        xs = t.x_qkv[:64].float().cpu().numpy(), t.x_o[:64].float().cpu().numpy()
+        res["cpu_baseline"] = cpu_prefill_baseline(t, head_host, xs)
+        log(f"[bench] prefill cpu baseline: {res['cpu_baseline']}")
     del t, head
     return res
 
@@ -353,48 +495,91 @@ def vendor_int8_gemm(torch, m, k, n, reps=20):
         return {"op": "torch._int_mm", "error": str(ex)[:120]}
 
 
-def run_ffn512(torch, ctx, steps, warmup, rows=512):
+def run_ffn512(torch, ctx, steps, warmup, rows=512, want_cpu=True, timed=True, reps=None):
     """Config 2: M=512 W4A8 gate_up -> SwiGLU -> requant -> W8A8 down, 36 layers."""
     from open_rknpu2_lm_infer_amd import device as D
+    from oracle import oracle
     gen = Gen(torch, 2)
-    layers = []
+    layers, host0 = [], None
     for l in range(LAYERS):
-        layers.append((ctx.weights(4, gen.codes(f"ffn/l{l}/gu", 4, H, 2 * F), gen.scales(f"ffn/l{l}/gu", 2 * F)),
-                       ctx.weights(8, gen.codes(f"ffn/l{l}/dn", 8, F, H), gen.scales(f"ffn/l{l}/dn", H))))
+        gc, gs = gen.codes(f"ffn/l{l}/gu", 4, H, 2 * F), gen.scales(f"ffn/l{l}/gu", 2 * F)
+        dc, ds = gen.codes(f"ffn/l{l}/dn", 8, F, H), gen.scales(f"ffn/l{l}/dn", H)
+        if l == 0 and want_cpu:
+            host0 = [v.cpu().numpy() for v in (gc, gs, dc, ds)]
+        layers.append((ctx.weights(4, gc, gs), ctx.weights(8, dc, ds)))
+        del gc, gs, dc, ds
     x = gen.acts("ffn/x", rows, H, True)
     y = torch.empty(rows, H, dtype=torch.float16, device="cuda")
     gws = ctx.workspace(4, rows, H, 2 * F)
     dws = ctx.workspace(8, rows, F, H)
+    ops_layer = 2.0 * rows * (H * 2 * F + F * H)
+    res = {"workload": "FFN block M=512: W4A8 gate_up 2560->2x9728 + SwiGLU + requant + W8A8 down, 36 layers"}
+    calls = [functools.partial(D.ffn, ctx, gu, dn, x, y, rows, gws=gws, dws=dws) for gu, dn in layers]
+    if timed:
+        def step():
+            for c in calls:
+                c()
 
-    def step():
-        for gu, dn in layers:
-            D.ffn(ctx, gu, dn, x, y, rows, gws=gws, dws=dws)
-
-    ms, ms_eager, ms_graph, ok = best_time(torch, step, steps, warmup, lambda: [y.clone()])
-    ops = LAYERS * 2.0 * rows * (H * 2 * F + F * H)
-    res = {"workload": "FFN block M=512: W4A8 gate_up 2560->2x9728 + SwiGLU + requant + W8A8 down, 36 layers",
-           "value": round(ops / (ms * 1e-3) / 1e12, 2), "unit": "TOPS", "ms_per_step": round(ms, 3),
-           "frac_of_int8_peak": round(ops / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4),
-           "ms_eager": round(ms_eager, 3), "ms_graph": round(ms_graph, 3), "graph_matches_eager": ok}
-    log(f"[bench] ffn512: {res['value']} TOPS")
-    del layers
+        ms, ms_eager, ms_graph, ok = best_time(torch, step, steps, warmup, lambda: [y.clone()])
+        ops = LAYERS * ops_layer
+        res.update({"value": round(ops / (ms * 1e-3) / 1e12, 2), "unit": "TOPS", "ms_per_step": round(ms, 3),
+                    "frac_of_int8_peak": round(ops / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4),
+                    "ms_eager": round(ms_eager, 3), "ms_graph": round(ms_graph, 3), "graph_matches_eager": ok})
+        log(f"[bench] ffn512: {res['value']} TOPS")
+    n = reps or max(2, steps // 2)
+    us = per_launch_us(torch, calls, n)
+    res["roofline"] = roof_of("mfma", "FFN call M=512 (quantization + gate_up W4 GEMM + SwiGLU + requant + down W8 GEMM)",
+                              ops_layer, us, LAYERS * n,
+                              method="graph of 36 back-to-back FFN calls (distinct weights), HIP events on the "
+                                     "replay stream")
+    if want_cpu:
+        xs = x[:64].float().cpu().numpy()
+        sec, reps_c = cpu_median(lambda: oracle.ffn(host0[0], host0[1], host0[2], host0[3], xs), 4.0)
+        res["cpu_baseline"] = cpu_baseline(2.0 * 64 * (H * 2 * F + F * H) / sec / 1e12, "TOPS", sec, reps_c,
+                                           "64 of 512 rows of layer 0's FFN (gate_up+SwiGLU->requant->down)",
+                                           ms_step_extrapolated=round(sec * 1e3 * LAYERS * rows / 64, 1))
+        log(f"[bench] ffn512 cpu baseline: {res['cpu_baseline']}")
+    del layers, calls
     return res
 
 
-def run_up128(torch, ctx, steps, warmup, rows=128):
-    """Config 0: single W8A8 linear M=128 K=2560 N=9728, outlier channels."""
+def run_up128(torch, ctx, steps, warmup, rows=128, want_cpu=True, timed=True, reps=None):
+    """Config 0: single W8A8 linear M=128 K=2560 N=9728, outlier channels.
+    Timed on 36 distinct weight copies launched back to back (900 MB, more
+    than the last-level cache holds: every call reads its weights from HBM);
+    the same call replayed on one weight set (25 MB, cache-resident) is
+    reported beside it."""
     from open_rknpu2_lm_infer_amd import device as D
+    from oracle import oracle
     gen = Gen(torch, 0)
-    w = ctx.weights(8, gen.codes("up/w", 8, H, F), gen.scales("up/w", F))
+    codes, scales = gen.codes("up/w", 8, H, F), gen.scales("up/w", F)
+    ws_ = [ctx.weights(8, codes, scales) for _ in range(LAYERS)]
+    host = (codes.cpu().numpy(), scales.cpu().numpy()) if want_cpu else None
+    del codes, scales
     x = gen.acts("up/x", rows, H, True)
     y = torch.empty(rows, F, dtype=torch.float16, device="cuda")
     ws = ctx.workspace(8, rows, H, F)
-    step = lambda: D.linear(ctx, w, x, y, rows, ws=ws)
-    ms, _, _, _ = best_time(torch, step, steps * 10, warmup, lambda: [y.clone()])
-    ops = 2.0 * rows * H * F
-    return {"workload": "W8A8 linear M=128 K=2560 N=9728 (Qwen3-4B FFN up)", "value": round(ops / (ms * 1e-3) / 1e12, 2),
-            "unit": "TOPS", "ms_per_step": round(ms, 4),
-            "gbs": round(lin_bytes(8, H, F, rows) / (ms * 1e-3) / 1e9, 1)}
+    ops, nbytes = 2.0 * rows * H * F, lin_bytes(8, H, F, rows)
+    n = reps or steps
+    us = per_launch_us(torch, [functools.partial(D.linear, ctx, w, x, y, rows, ws=ws) for w in ws_], n)
+    res = {"workload": "W8A8 linear M=128 K=2560 N=9728 (Qwen3-4B FFN up)",
+           "value": round(ops / (us * 1e-6) / 1e12, 2), "unit": "TOPS", "ms_per_step": round(us * 1e-3, 4),
+           "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+           "timing": "per call over 36 distinct weight copies in a graph (weights read from HBM)",
+           "roofline": roof_of("hbm", "W8A8 linear M=128 (quantization + gemm_kernel), 2560x9728", nbytes, us,
+                               LAYERS * n, method="graph of 36 back-to-back calls on distinct weight copies, HIP "
+                                                  "events on the replay stream")}
+    if timed:
+        step = lambda: D.linear(ctx, ws_[0], x, y, rows, ws=ws)
+        ms, _, _, _ = best_time(torch, step, steps * 10, warmup, lambda: [y.clone()])
+        res["cache_resident_us"] = round(ms * 1e3, 2)
+    if want_cpu:
+        xh = x.float().cpu().numpy()
+        sec, reps_c = cpu_median(lambda: oracle.linear(host[0], host[1], xh), 4.0)
+        res["cpu_baseline"] = cpu_baseline(ops / sec / 1e12, "TOPS", sec, reps_c, "the whole call (128 rows)")
+    log(f"[bench] up128: {res['value']} TOPS, {res['gbs']} GB/s per call from HBM")
+    del ws_
+    return res
 
 
 def run_host_abi(layers=4, reps=20):
@@ -461,9 +646,11 @@ def run_host_abi(layers=4, reps=20):
     return res
 
 
-def run_moe(torch, ctx, steps, warmup, tokens_list=(512, 1)):
+def run_moe(torch, ctx, steps, warmup, tokens_list=(512, 1), want_cpu=True):
     """Config 4: hidden 2048, 128 experts, top-8, I=768, routed W4 gate_up +
-    W8 down; shared W8 FFN of intermediate 2048 through the dense path."""
+    W8 down; shared W8 FFN of intermediate 2048 through the dense path.
+    roofline: HBM, over the weight bytes one step must read (every expert a
+    token routes to, plus the shared FFN) and the step's time."""
     import ctypes
 
     import numpy as np
@@ -491,10 +678,16 @@ def run_moe(torch, ctx, steps, warmup, tokens_list=(512, 1)):
                        L.rk_npu_moe_w8_weights_free, "MoE bank", ctx.shared)
     work = npu._Handle(L.rk_npu_moe_w4w8_workspace_create(ctx.domain, ctypes.byref(cfg)),
                        L.rk_npu_moe_w8_workspace_free, "MoE workspace", ctx.shared)
-    del keep, arr
+    del arr
+    if not want_cpu:
+        del keep
     gen = Gen(torch, 4)
-    sgu = ctx.weights(8, gen.codes("moe/sh/gu", 8, h, 2 * sh_inter), gen.scales("moe/sh/gu", 2 * sh_inter))
-    sdn = ctx.weights(8, gen.codes("moe/sh/dn", 8, sh_inter, h), gen.scales("moe/sh/dn", h))
+    sh = [gen.codes("moe/sh/gu", 8, h, 2 * sh_inter), gen.scales("moe/sh/gu", 2 * sh_inter),
+          gen.codes("moe/sh/dn", 8, sh_inter, h), gen.scales("moe/sh/dn", h)]
+    sgu = ctx.weights(8, sh[0], sh[1])
+    sdn = ctx.weights(8, sh[2], sh[3])
+    sh_host = [v.cpu().numpy() for v in sh] if want_cpu else None
+    del sh
     results = []
     for T in tokens_list:
         logits = g.standard_normal((T, experts)).astype(np.float32)
@@ -502,7 +695,8 @@ def run_moe(torch, ctx, steps, warmup, tokens_list=(512, 1)):
         rw = np.zeros((T, top), np.float32)
         for r in range(T):
             ids[r], rw[r] = oracle.routes(logits[r], top)
-        x = torch.from_numpy(g.standard_normal((T, h)).astype(np.float32)).cuda()
+        x_host = g.standard_normal((T, h)).astype(np.float32)
+        x = torch.from_numpy(x_host).cuda()
         d_ids = torch.from_numpy(ids).cuda()
         d_rw = torch.from_numpy(rw).cuda()
         y = torch.empty(T, h, dtype=torch.float32, device="cuda")
@@ -531,12 +725,32 @@ def run_moe(torch, ctx, steps, warmup, tokens_list=(512, 1)):
             res.update(value=round((routed_ops + shared_ops) / (ms * 1e-3) / 1e12, 2), unit="TOPS")
         else:
             res.update(value=round((routed_bytes + shared_bytes) / (ms * 1e-3) / 1e9, 1), unit="GB/s")
+        res["roofline"] = roof_of("hbm", f"MoE call T={T} (route, gather, grouped W4 gate_up + W8 down GEMMs, "
+                                         "combine) + shared FFN call", routed_bytes + shared_bytes, ms * 1e3,
+                                  steps * (10 if T == 1 else 1),
+                                  method="whole step (one MoE call + one shared FFN call), faster of eager and "
+                                         "graph replay; HIP events")
+        if want_cpu:
+            sample = min(T, 32)
+            gu_l = [(c[0], c[1]) for c in keep]
+            dn_l = [(c[2], c[3]) for c in keep]
+            shared = ((sh_host[0], sh_host[1]), (sh_host[2], sh_host[3]))
+            fn = lambda: oracle.moe(gu_l, dn_l, x_host[:sample], ids[:sample], rw[:sample], shared=shared)
+            sec, reps_c = cpu_median(fn, 4.0)
+            s_ops = (routed_ops + shared_ops) * sample / T
+            s_bytes = (min(experts, len(set(ids[:sample].ravel().tolist()))) *
+                       (h * 2 * inter // 2 + 4 * 2 * inter + inter * h + 4 * h) + shared_bytes)
+            res["cpu_baseline"] = (cpu_baseline(s_ops / sec / 1e12, "TOPS", sec, reps_c,
+                                                f"{sample} of {T} tokens (oracle MoE with the shared FFN)")
+                                   if T >= 64 else
+                                   cpu_baseline(s_bytes / sec / 1e9, "GB/s", sec, reps_c,
+                                                "the whole call (oracle MoE with the shared FFN)"))
         log(f"[bench] moe T={T}: {res['value']} {res['unit']} ({ms:.3f} ms)")
         results.append(res)
     return results
 
 
-def run_attention(torch, ctx, steps, layers=36, length=4096):
+def run_attention(torch, ctx, steps, layers=36, length=4096, want_cpu=True):
     """FP16 GQA attention (Qwen3-4B geometry: 32 query heads over 8 KV heads,
     head_dim 128) over per-layer KV caches of `length` rows, through the
     device entry points: a decode step (one query row per layer at the last
@@ -584,20 +798,43 @@ def run_attention(torch, ctx, steps, layers=36, length=4096):
             assert L.rk_npu_hip_attention_run(ws, caches[0], qr.data_ptr(), rows, pos, o.data_ptr(), 0,
                                               torch.cuda.current_stream().cuda_stream) == 0
             ms, ms_eager, ms_graph, ok = best_time(torch, step, steps, 2, lambda: [o.clone()])
+            us_layer = ms * 1e3 / layers
+            if want_cpu:
+                from oracle import oracle
+                qn = qr.float().cpu().numpy()
+                kn, vn = kd.float().cpu().numpy(), vd.float().cpu().numpy()
+                sec, reps_c = cpu_median(lambda: oracle.attention(qn, kn, vn, d ** -0.5, pos, True), 3.0)
             if rows == 1:
-                kv_bytes = layers * 2 * kh * length * d * 2
-                res.append({"workload": f"attention decode: GQA 32/8 heads, d=128, {length} cached rows, 1 query row, "
-                                        f"{layers} layers", "value": round(kv_bytes / (ms * 1e-3) / 1e9, 1),
-                            "unit": "GB/s", "ms_per_step": round(ms, 4), "us_per_layer": round(ms * 1e3 / layers, 2),
-                            "graph_matches_eager": ok})
+                kv_layer = 2 * kh * length * d * 2
+                kv_bytes = layers * kv_layer
+                r_ = {"workload": f"attention decode: GQA 32/8 heads, d=128, {length} cached rows, 1 query row, "
+                                  f"{layers} layers", "value": round(kv_bytes / (ms * 1e-3) / 1e9, 1),
+                      "unit": "GB/s", "ms_per_step": round(ms, 4), "us_per_layer": round(us_layer, 2),
+                      "graph_matches_eager": ok,
+                      "roofline": roof_of("hbm", "attention decode call (split kernel + combine), one layer",
+                                          kv_layer, us_layer, layers * steps,
+                                          method="per layer of the step: 36 calls on distinct caches in the step, "
+                                                 "faster of eager and graph replay; HIP events")}
+                if want_cpu:
+                    r_["cpu_baseline"] = cpu_baseline(kv_layer / sec / 1e9, "GB/s", sec, reps_c,
+                                                      "one layer's call (float64 numpy oracle)")
             else:
                 keys = sum(pos + r + 1 for r in range(rows))
-                flops = layers * 4.0 * qh * d * keys
-                res.append({"workload": f"attention prefill: GQA 32/8 heads, d=128, {rows} query rows ending at "
-                                        f"{length} cached rows, causal, {layers} layers",
-                            "value": round(flops / (ms * 1e-3) / 1e12, 2), "unit": "TFLOP/s",
-                            "ms_per_step": round(ms, 4), "us_per_layer": round(ms * 1e3 / layers, 2),
-                            "graph_matches_eager": ok})
+                flops_layer = 4.0 * qh * d * keys
+                flops = layers * flops_layer
+                r_ = {"workload": f"attention prefill: GQA 32/8 heads, d=128, {rows} query rows ending at "
+                                  f"{length} cached rows, causal, {layers} layers",
+                      "value": round(flops / (ms * 1e-3) / 1e12, 2), "unit": "TFLOP/s",
+                      "ms_per_step": round(ms, 4), "us_per_layer": round(us_layer, 2),
+                      "graph_matches_eager": ok,
+                      "roofline": roof_of("mfma", "attention prefill call (f16 MFMA kernel + combine), one layer",
+                                          flops_layer, us_layer, layers * steps, peak=F16_PEAK_TFLOPS,
+                                          method="per layer of the step: 36 calls on distinct caches in the step, "
+                                                 "faster of eager and graph replay; HIP events; peak: dense f16 MFMA")}
+                if want_cpu:
+                    r_["cpu_baseline"] = cpu_baseline(flops_layer / sec / 1e12, "TFLOP/s", sec, reps_c,
+                                                      "one layer's call (float64 numpy oracle)")
+            res.append(r_)
         return res
     finally:
         torch.cuda.synchronize()
@@ -697,6 +934,53 @@ def run_probes(torch, ctx, reps=20):
     return res
 
 
+ROOF_REPS = 50  # graph replays per roofline pass (36 launches each)
+
+
+def roofline_only(torch, ctx, which="all"):
+    """Every line's roofline passes (or one line's) and nothing else: the
+    launches of a kernel-trace profile of this command are the timed ones,
+    apart from two eager warm-up calls per pass (fn() before capture and on
+    the capture stream) and one warm replay."""
+    out = {}
+    if which in ("all", "decode"):
+        for rows in (1, 4):
+            r = run_decode(torch, ctx, rows, 0, 0, False, timed=False, reps=ROOF_REPS)
+            out[f"decode M={rows}"] = {"projections": r["projections"], "roofline": r["roofline"]}
+    if which in ("all", "prefill"):
+        r = run_prefill(torch, ctx, 4096, 0, 0, want_cpu=False, timed=False, reps=4)
+        out["prefill M=4096"] = {"projections": r["projections"], "roofline": r["roofline"]}
+    if which in ("all", "ffn512"):
+        out["ffn M=512"] = run_ffn512(torch, ctx, 0, 0, want_cpu=False, timed=False, reps=4)["roofline"]
+    if which in ("all", "up128"):
+        out["up M=128"] = run_up128(torch, ctx, 0, 0, want_cpu=False, timed=False, reps=20)["roofline"]
+    return out
+
+
+def summarize_trace(path, top=40):
+    """Per (kernel, grid) launch statistics of a rocprofv3 --kernel-trace CSV
+    (columns Kernel_Name, Grid_Size*, Workgroup_Size*, Start_Timestamp,
+    End_Timestamp in ns): count, mean / median / p10 / p90 duration in us,
+    ordered by total time. Grids are in work-items, as rocprofv3 writes them."""
+    groups = {}
+    with open(path, newline="") as f:
+        for row in csv.DictReader(f):
+            name = row.get("Kernel_Name", "?")
+            grid = row.get("Grid_Size_X") or row.get("Grid_Size") or "?"
+            wg = row.get("Workgroup_Size_X") or row.get("Workgroup_Size") or "?"
+            dur = (int(row["End_Timestamp"]) - int(row["Start_Timestamp"])) / 1e3
+            groups.setdefault((name, grid, wg), []).append(dur)
+    rows = sorted(groups.items(), key=lambda kv: -sum(kv[1]))[:top]
+    lines = [f"{'total_us':>12} {'count':>6} {'mean_us':>9} {'median':>9} {'p10':>9} {'p90':>9} {'grid':>9} {'wg':>4}  kernel"]
+    for (name, grid, wg), d in rows:
+        d.sort()
+        q = lambda p: d[min(len(d) - 1, int(p * len(d)))]
+        short = name if len(name) <= 150 else name[:147] + "..."
+        lines.append(f"{sum(d):12.1f} {len(d):6d} {statistics.mean(d):9.3f} {statistics.median(d):9.3f} "
+                     f"{q(0.1):9.3f} {q(0.9):9.3f} {grid:>9} {wg:>4}  {short}")
+    return "\n".join(lines)
+
+
 def npu_check(rc, what):
     if rc != 0:
         raise RuntimeError(f"{what}: rc {rc}")
@@ -717,7 +1001,15 @@ def main():
                     help="only measure the ceilings (MFMA int8 rate, HBM read floors per decode projection)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only run the workload of the FETCH_SIZE / WRITE_SIZE counter runs")
+    ap.add_argument("--roofline-only", nargs="?", const="all", choices=["all", "decode", "prefill", "ffn512", "up128"],
+                    help="only the roofline passes of every line (or of one: per-projection decode and prefill "
+                         "passes included), no step timing and no CPU baseline: the command to profile")
+    ap.add_argument("--summarize-trace", metavar="CSV",
+                    help="no GPU: per-kernel launch statistics of a rocprofv3 kernel-trace CSV")
     args = ap.parse_args()
+    if args.summarize_trace:
+        print(summarize_trace(args.summarize_trace))
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path "
               f"(--gpus {args.gpus} requested); run with --gpus 1", file=sys.stderr)
@@ -731,6 +1023,9 @@ def main():
     if args.probes:
         print(json.dumps(run_probes(torch, ctx)), flush=True)
         return
+    if args.roofline_only:
+        print(json.dumps(roofline_only(torch, ctx, args.roofline_only)), flush=True)
+        return
     if args.only:
         steps = max(4, args.steps // 2)
         res = {"prefill": lambda: run_prefill(torch, ctx, 4096, steps, 2),
@@ -741,19 +1036,26 @@ def main():
                "host": lambda: run_host_abi()}[args.only]()
         print(json.dumps(res), flush=True)
         return
-    primary = run_decode(torch, ctx, args.decode_rows, args.steps, args.warmup, not args.no_cpu_baseline)
+    cpu = not args.no_cpu_baseline
+    primary = run_decode(torch, ctx, args.decode_rows, args.steps, args.warmup, cpu, reps=ROOF_REPS)
     secondary = []
     if not args.primary_only:
-        m4 = run_decode(torch, ctx, 4, args.steps, args.warmup, False, want_roofline=True)
+        m4 = run_decode(torch, ctx, 4, args.steps, args.warmup, cpu, reps=ROOF_REPS)
         secondary.append({"workload": "decode M=4 (MTP/draft verify), same W4A8 set x36",
                           "value": round(m4["value"], 1), "unit": "GB/s", "ms_per_step": round(m4["ms_per_step"], 4),
-                          "roofline": m4["roofline"]})
-        secondary.append(run_prefill(torch, ctx, 4096, max(4, args.steps // 2), 2))
-        secondary.append(run_ffn512(torch, ctx, max(4, args.steps // 2), 2))
-        secondary.append(run_up128(torch, ctx, args.steps, args.warmup))
-        secondary.extend(run_host_abi())
-        secondary.extend(run_moe(torch, ctx, max(4, args.steps // 2), 2))
-        secondary.extend(run_attention(torch, ctx, max(4, args.steps // 2)))
+                          "projections": m4["projections"], "roofline": m4["roofline"],
+                          "cpu_baseline": m4.get("cpu_baseline")})
+        secondary.append(run_prefill(torch, ctx, 4096, max(4, args.steps // 2), 2, cpu))
+        secondary.append(run_ffn512(torch, ctx, max(4, args.steps // 2), 2, want_cpu=cpu))
+        up = run_up128(torch, ctx, args.steps, args.warmup, want_cpu=cpu)
+        secondary.append(up)
+        host = run_host_abi()
+        if cpu:
+            host[0]["cpu_baseline"] = dict(primary["cpu_baseline"], note="the same work as the primary line's sample")
+            host[1]["cpu_baseline"] = dict(up["cpu_baseline"], note="the same work as the M=128 up line's sample")
+        secondary.extend(host)
+        secondary.extend(run_moe(torch, ctx, max(4, args.steps // 2), 2, want_cpu=cpu))
+        secondary.extend(run_attention(torch, ctx, max(4, args.steps // 2), want_cpu=cpu))
     for s in secondary:
         s.pop("kernels", None)
         if "roofline" in s:
@@ -782,6 +1084,7 @@ def main():
                    "timing": "faster of eager launches and HIP graph replay of the same step "
                              "(replay checked bit-exact vs eager)", **config_extra},
         "roofline": roof,
+        "projections": primary["projections"],
         "cpu_baseline": primary.get("cpu_baseline"),
         "secondary": secondary,
     }
