@@ -160,13 +160,15 @@ def graph_time(torch, fn, reps, check=None):
     return e0.elapsed_time(e1) / reps, ok
 
 
-# HBM bytes per launch of the dominant decode kernel (gate_up GEMV, M=1), from
-# two rocprofv3 counter runs of `bench.py --traffic-probe` (FETCH_SIZE, then
-# WRITE_SIZE, KiB per dispatch, median over 108 dispatches), each scaled by
-# what the same counter reads for a 268,435,456-byte device copy in the same
-# run: FETCH_SIZE 131,090.2 KiB (factor 2.0), WRITE_SIZE 262,144 KiB (factor 1.0).
-# Summary and commands: profiles/traffic_gemv_gate_up_m1.txt.
-TRAFFIC_GEMV_GATE_UP = {1: int(round((12431.0 * 2.0 + 81.0625 * 1.0) * 1024))}
+# HBM bytes per launch of the dominant decode kernel (the gate_up GEMV) at
+# M=1 and M=4, from two rocprofv3 counter runs of `bench.py --traffic-probe`
+# (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch, medians over 216
+# dispatches), each scaled by what the same counter reads for the run's
+# 268,435,456-byte device copy: FETCH_SIZE 131,083.5 KiB (factor 2.0),
+# WRITE_SIZE 262,144 KiB (factor 1.0). Commands and every decode GEMV's
+# figures: profiles/traffic_decode_gemv_m1_m4.txt.
+TRAFFIC_GEMV_GATE_UP = {1: int(round((12434.0 * 2.0 + 81.1 * 1.0) * 1024)),
+                        4: int(round((12461.5 * 2.0 + 304.0 * 1.0) * 1024))}
 
 
 ROOF_METHOD = "graph of 36 back-to-back launches (distinct weights), HIP events on the replay stream"
@@ -843,10 +845,12 @@ def run_attention(torch, ctx, steps, layers=36, length=4096, want_cpu=True):
         L.rk_npu_attention_f16_workspace_free(ws)
 
 
-def traffic_probe(torch, ctx, rows=1, reps=3):
+def traffic_probe(torch, ctx, reps=3):
     """Workload for the HBM-traffic counter runs (no timing): a plain 256 MiB
-    device copy (known bytes: the calibration of FETCH_SIZE / WRITE_SIZE) and
-    the decode gate_up GEMV on 36 layers' distinct weights."""
+    device copy (known bytes: the calibration of FETCH_SIZE / WRITE_SIZE),
+    then, at M=1 and M=4, `reps` passes over 36 layers' distinct weights of
+    each decode projection in turn (qkv, o, gate_up + SwiGLU, the FFN call),
+    so every dispatch of a kernel reads its weights from HBM."""
     from open_rknpu2_lm_infer_amd import device as D
     src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda").random_(0, 256)
     dst = torch.empty_like(src)
@@ -854,15 +858,24 @@ def traffic_probe(torch, ctx, rows=1, reps=3):
         dst.copy_(src)
     torch.cuda.synchronize()
     del src, dst
-    gen = Gen(torch, 1)
-    t = DenseLayers(torch, ctx, gen, rows, (4, 4, 4, 4), tag=f"dec{rows}")
-    mid = torch.empty(rows, F, dtype=torch.float16, device="cuda")
-    for _ in range(reps):
-        for mats in t.w:
-            D.linear(ctx, mats["gate_up"], t.x_ffn, mid, rows, swiglu=True, ws=t.ws["gate_up"])
-    torch.cuda.synchronize()
-    log(f"[bench] traffic probe: copy 268435456 B x{reps}, gate_up GEMV x{reps * LAYERS} "
-        f"({lin_bytes(4, H, 2 * F, rows)} algorithmic B each)")
+    for rows in (1, 4):
+        gen = Gen(torch, 1)
+        t = DenseLayers(torch, ctx, gen, rows, (4, 4, 4, 4), tag=f"dec{rows}")
+        mid = torch.empty(rows, F, dtype=torch.float16, device="cuda")
+        r = rows
+        calls = (lambda m: D.linear(ctx, m["qkv"], t.x_qkv, t.y_qkv, r, ws=t.ws["qkv"]),
+                 lambda m: D.linear(ctx, m["o"], t.x_o, t.y_o, r, ws=t.ws["o"]),
+                 lambda m: D.linear(ctx, m["gate_up"], t.x_ffn, mid, r, swiglu=True, ws=t.ws["gate_up"]),
+                 lambda m: D.ffn(ctx, m["gate_up"], m["down"], t.x_ffn, t.y_ffn, r, gws=t.ws["gate_up"],
+                                 dws=t.ws["down"]))
+        for call in calls:
+            for _ in range(reps):
+                for m in t.w:
+                    call(m)
+            torch.cuda.synchronize()
+        del t
+        log(f"[bench] traffic probe M={rows}: qkv, o, gate_up, FFN call x{reps * LAYERS} each")
+    log("[bench] traffic probe: copy 268435456 B x" + str(reps))
 
 
 def run_probes(torch, ctx, reps=20):
@@ -930,8 +943,75 @@ def run_probes(torch, ctx, reps=20):
             row["library call"] = {"us": round(us, 3), "gbs": round(nbytes / (us * 1e-6) / 1e9, 1)}
         res["hbm_read"].append(row)
         log(f"[probe] {name}: {row}")
+    # The decode step against one layer's weights (50 MB, resident in the
+    # 256 MB last-level cache) replayed 36 times: what the step would take if
+    # its weight reads cost nothing beyond the cache.
+    def layer0_x36():
+        m = t.w[0]
+        for _ in range(LAYERS):
+            D.linear(ctx, m["qkv"], t.x_qkv, t.y_qkv, 1, ws=t.ws["qkv"])
+            D.linear(ctx, m["o"], t.x_o, t.y_o, 1, ws=t.ws["o"])
+            D.ffn(ctx, m["gate_up"], m["down"], t.x_ffn, t.y_ffn, 1, gws=t.ws["gate_up"], dws=t.ws["down"])
+    ms_step, _ = graph_time(torch, t.step, reps)
+    ms_warm, _ = graph_time(torch, layer0_x36, reps)
+    nbytes = t.bytes_per_layer() * LAYERS
+    res["decode_step_cache_warm"] = {
+        "36 distinct layers (the bench step)": {"ms": round(ms_step, 4), "gbs": round(nbytes / ms_step / 1e6, 1)},
+        "layer 0 x 36 (weights cache-resident)": {"ms": round(ms_warm, 4), "gbs": round(nbytes / ms_warm / 1e6, 1)}}
+    log(f"[probe] decode step, cache-warm bound: {res['decode_step_cache_warm']}")
     del t
     return res
+
+
+# GEMM shapes of the tile sweep: (name, bits, M, K, N, SwiGLU)
+SWEEP_SHAPES = (("M128 up 2560x9728 W8", 8, 128, H, F, False), ("M512 gate_up 2560x19456 W4", 4, 512, H, 2 * F, True),
+                ("M512 down 9728x2560 W8", 8, 512, F, H, False), ("M4096 qkv 2560x6144 W8", 8, 4096, H, Q + 2 * KV, False),
+                ("M4096 o 4096x2560 W8", 8, 4096, Q, H, False),
+                ("M4096 gate_up 2560x19456 W4", 4, 4096, H, 2 * F, True),
+                ("M4096 down 9728x2560 W8", 8, 4096, F, H, False),
+                ("M4096 lm_head 2560x151936 W8", 8, 4096, H, VOCAB, False))
+
+
+def tile_sweep(torch, ctx, only=None, reps=5):
+    """Every GEMM tile (HM_GEMM_VARIANT 0..4: 256x256, 256x128, 128x128, 64x128,
+    32x128) unsplit, and the split-K counts 2, 3, 4, 6, 8 (HM_SPLITS) of the
+    128x128 and 64x128 tiles, plus the plan's own choice, on the GEMM shapes of
+    the bench: one library call (quantization launch included) per distinct
+    weight copy, enough copies that they exceed the last-level cache, in a
+    graph. Workspaces are created under each setting so split partials fit."""
+    from open_rknpu2_lm_infer_amd import device as D
+    gen = Gen(torch, 7)
+    configs = [(-1, 0)] + [(v, 1) for v in range(5)] + [(v, sp) for v in (2, 3) for sp in (2, 3, 4, 6, 8)]
+    out = {}
+    for name, bits, m, k, n, sw in SWEEP_SHAPES:
+        if only and not any(o in name for o in only):
+            continue
+        copies = max(4, min(LAYERS, math.ceil(600e6 / (k * n * bits // 8))))
+        codes, scales = gen.codes(name, bits, k, n), gen.scales(name, n)
+        ws_ = [ctx.weights(bits, codes, scales) for _ in range(copies)]
+        del codes
+        x = gen.acts(name + "/x", m, k, True)
+        y = torch.empty(m, n // 2 if sw else n, dtype=torch.float16, device="cuda")
+        row = {}
+        # one untimed pass first (the first timed setting of a shape read ~5%
+        # slow), the plan's own choice timed last
+        with D.plan_switch("HM_GEMM_VARIANT", -1):
+            per_launch_us(torch, [functools.partial(D.linear, ctx, w, x, y, m, swiglu=sw, ws=ctx.workspace(bits, m, k, n))
+                                  for w in ws_], 1)
+        for v, sp in configs[1:] + configs[:1]:
+            with D.plan_switch("HM_GEMM_VARIANT", v), D.plan_switch("HM_SPLITS", sp):
+                wsp = ctx.workspace(bits, m, k, n, cached=False)
+                us = per_launch_us(torch, [functools.partial(D.linear, ctx, w, x, y, m, swiglu=sw, ws=wsp)
+                                           for w in ws_], reps)
+            key = "plan" if v < 0 else f"tile{v}" + (f"/k{sp}" if sp > 1 else "")
+            row[key] = round(us, 2)
+        best = min(row, key=row.get)
+        out[name] = {"us": row, "best": best, "tops_best": round(2.0 * m * k * n / row[best] / 1e6, 1),
+                     "copies": copies}
+        log(f"[sweep] {name}: best {best} {row[best]} us, plan {row['plan']} us")
+        del ws_
+        torch.cuda.empty_cache()
+    return out
 
 
 ROOF_REPS = 50  # graph replays per roofline pass (36 launches each)
@@ -957,7 +1037,7 @@ def roofline_only(torch, ctx, which="all"):
     return out
 
 
-def summarize_trace(path, top=40):
+def summarize_trace(path, top=60):
     """Per (kernel, grid) launch statistics of a rocprofv3 --kernel-trace CSV
     (columns Kernel_Name, Grid_Size*, Workgroup_Size*, Start_Timestamp,
     End_Timestamp in ns): count, mean / median / p10 / p90 duration in us,
@@ -978,6 +1058,25 @@ def summarize_trace(path, top=40):
         short = name if len(name) <= 150 else name[:147] + "..."
         lines.append(f"{sum(d):12.1f} {len(d):6d} {statistics.mean(d):9.3f} {statistics.median(d):9.3f} "
                      f"{q(0.1):9.3f} {q(0.9):9.3f} {grid:>9} {wg:>4}  {short}")
+    return "\n".join(lines)
+
+
+def summarize_counters(path, top=60):
+    """Per (kernel, grid) medians of each counter of a rocprofv3 --pmc CSV
+    (one row per dispatch and counter: Kernel_Name, Grid_Size, Counter_Name,
+    Counter_Value), ordered by dispatch count then name."""
+    groups = {}
+    with open(path, newline="") as f:
+        for row in csv.DictReader(f):
+            key = (row.get("Kernel_Name", "?"), row.get("Grid_Size") or row.get("Grid_Size_X") or "?")
+            groups.setdefault(key, {}).setdefault(row["Counter_Name"], []).append(float(row["Counter_Value"]))
+    items = sorted(groups.items(), key=lambda kv: (-max(len(v) for v in kv[1].values()), kv[0][0]))[:top]
+    lines = []
+    for (name, grid), counters in items:
+        short = name if len(name) <= 150 else name[:147] + "..."
+        vals = "  ".join(f"{c}={statistics.median(v):.1f}" for c, v in sorted(counters.items()))
+        n = max(len(v) for v in counters.values())
+        lines.append(f"{n:6d} grid={grid:>9}  {vals}  {short}")
     return "\n".join(lines)
 
 
@@ -1004,11 +1103,19 @@ def main():
     ap.add_argument("--roofline-only", nargs="?", const="all", choices=["all", "decode", "prefill", "ffn512", "up128"],
                     help="only the roofline passes of every line (or of one: per-projection decode and prefill "
                          "passes included), no step timing and no CPU baseline: the command to profile")
+    ap.add_argument("--tile-sweep", nargs="*", metavar="SHAPE",
+                    help="only time every GEMM tile / split-K setting on the bench's GEMM shapes (names "
+                         "containing any given word; all by default)")
     ap.add_argument("--summarize-trace", metavar="CSV",
                     help="no GPU: per-kernel launch statistics of a rocprofv3 kernel-trace CSV")
+    ap.add_argument("--summarize-counters", metavar="CSV",
+                    help="no GPU: per-kernel counter medians of a rocprofv3 --pmc CSV")
     args = ap.parse_args()
     if args.summarize_trace:
         print(summarize_trace(args.summarize_trace))
+        return
+    if args.summarize_counters:
+        print(summarize_counters(args.summarize_counters))
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path "
@@ -1025,6 +1132,9 @@ def main():
         return
     if args.roofline_only:
         print(json.dumps(roofline_only(torch, ctx, args.roofline_only)), flush=True)
+        return
+    if args.tile_sweep is not None:
+        print(json.dumps(tile_sweep(torch, ctx, args.tile_sweep)), flush=True)
         return
     if args.only:
         steps = max(4, args.steps // 2)

@@ -153,6 +153,8 @@ int rk_npu_hip_inject_alloc_failures(int count);
  *   HM_FFN_SPIN      polls a one-launch FFN's down blocks make for their
  *                    gate_up blocks before giving up (65536); negative: they
  *                    give up at once (tests of the failure report)
+ *   HM_GEMV_PREQ     -1: 4 rows are quantized by a launch before the GEMV;
+ *                    0: inside the GEMV blocks wherever the rows fit
  * Unknown names return RK_NPU_ERR_PARAM. */
 int rk_npu_hip_set_switch(const char* name, int value, int* previous);
 

@@ -305,14 +305,14 @@ static const int kBN[] = {256, 128, 128, 128, 128};
 // variable, read once when the library first plans a launch; afterwards only
 // rk_npu_hip_set_switch changes it, so no launch reads the environment.
 enum SwitchId { SW_GEMM_VARIANT, SW_SPLITS, SW_FORCE_GEMM, SW_GEMV_QW, SW_GEMV_SPLITS, SW_FFN_FUSED, SW_FFN_SPIN,
-                SW_COUNT };
+                SW_GEMV_PREQ, SW_COUNT };
 struct SwitchDef {
     const char* name;
     int fallback;
 };
 static const SwitchDef kSwitches[SW_COUNT] = {
     {"HM_GEMM_VARIANT", -1}, {"HM_SPLITS", 0},         {"HM_FORCE_GEMM", 0}, {"HM_GEMV_QW", -1},
-    {"HM_GEMV_SPLITS", 0},   {"HM_FFN_FUSED", 0},      {"HM_FFN_SPIN", 1 << 16}};
+    {"HM_GEMV_SPLITS", 0},   {"HM_FFN_FUSED", 0},      {"HM_FFN_SPIN", 1 << 16}, {"HM_GEMV_PREQ", -1}};
 
 static std::atomic<int>* switch_table() {
     static std::atomic<int> table[SW_COUNT];
@@ -377,7 +377,11 @@ static Plan plan_gemm(int rows, const Geometry& g, int variant) {
             const int cus = device_cus();
             const long long t256 = (long long)((rows + 255) / 256) * (g.N_pad / 256);
             const long long t128 = (long long)((rows + 127) / 128) * (g.N_pad / 128);
-            if (t256 >= 8LL * cus || (g.K_pad >= 8192 && t128 > 2LL * cus)) v = V256x256;
+            // 256x256 for very wide outputs (lm_head), and for K >= 4096 once the
+            // 128x128 tiles overflow two per CU: at M=4096 the 256x256 tile runs
+            // o 4096x2560 in 68 us against 73 and down 9728x2560 in 158 against
+            // 172 (bench.py --tile-sweep), although its 160 tiles leave CUs idle.
+            if (t256 >= 8LL * cus || (g.K_pad >= 4096 && t128 > 2LL * cus)) v = V256x256;
         }
     }
     p.variant = v;
@@ -713,10 +717,16 @@ static void launch_gemv_split(const GemvParams& V, int grid, int rounds, size_t 
 // (qwn = 1), or by every thread of the block.
 template <typename T, int MR, int BITS, int EPI>
 static void launch_gemv_mr(const GemvParams& V, int groups, size_t lds, hipStream_t s, bool preq, int qwn) {
-    if constexpr (MR >= 4) {
-        (void)preq;  // 4 or more rows are always quantized beforehand (enqueue_linear)
+    if constexpr (MR > 4) {
+        (void)preq;  // more than 4 rows are always quantized beforehand (enqueue_linear)
         (void)qwn;
         launch_gemv_w<float, MR, BITS, EPI, true, 0>(V, groups, lds, s);
+    } else if constexpr (MR == 4) {
+        (void)qwn;  // 4 rows: beforehand, or by every thread of the block (HM_GEMV_PREQ=0)
+        if (preq)
+            launch_gemv_w<float, MR, BITS, EPI, true, 0>(V, groups, lds, s);
+        else
+            launch_gemv_w<T, MR, BITS, EPI, false, 0>(V, groups, lds, s);
     } else {
         if (preq)
             launch_gemv_w<float, MR, BITS, EPI, true, 0>(V, groups, lds, s);  // activations unused
@@ -790,8 +800,12 @@ int enqueue_linear(Workspace* ws, const Weights* w, const void* x, int x_type, l
         // Rows the kernel cannot quantize from registers (unaligned or ragged
         // rows, or more than GEMV_XMAX chunks per thread) are quantized first;
         // so are 4 or more rows, where every block re-quantizing all rows costs
-        // more than one extra launch (M=4 decode set: 1002 -> 1090 GB/s).
-        const bool preq = pv.mr >= 4 || !V.vec || (g.K_pad / 16) * pv.mr > 256 * GEMV_XMAX;
+        // more than one extra launch (M=4 decode set, 36 layers in a graph:
+        // 1.57 ms per step with the launch, 1.68 ms with HM_GEMV_PREQ=0, which
+        // quantizes 4 rows in the blocks wherever they fit: qkv 8.4 -> 9.5 us,
+        // gate_up 14.6 -> 16.7 us).
+        const bool preq_rows = pv.mr > 4 || (pv.mr == 4 && switch_value(SW_GEMV_PREQ) != 0);
+        const bool preq = preq_rows || !V.vec || (g.K_pad / 16) * pv.mr > 256 * GEMV_XMAX;
         // One or two rows that fit the quantization wave of the block are
         // quantized by that wave beside a long weight stream (5 to 8 rounds
         // per group: gate/up 2560x19456 W4 M=1 7.5 -> 6.7 us). Shorter streams

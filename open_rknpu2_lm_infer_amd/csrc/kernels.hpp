@@ -77,11 +77,20 @@ __device__ __forceinline__ int orig_col(int p, int half) {
     return w < 32 ? (q << 5) + w : half + (q << 5) + (w - 32);
 }
 
+// f32 -> f16 (RNE) of a value already rounded to f32. The empty asm keeps
+// the compiler from fusing the conversion with the multiply that produced v
+// into one mixed-precision instruction (one rounding straight to f16, which
+// differs from rounding to f32 and then to f16) where it can see the type.
+__device__ __forceinline__ __half f32_to_f16(float v) {
+    asm volatile("" : "+v"(v));
+    return __float2half_rn(v);
+}
+
 __device__ __forceinline__ void store_out(void* c, int c_type, size_t idx, float v) {
     if (c_type == DT_F32)
         static_cast<float*>(c)[idx] = v;
     else
-        static_cast<__half*>(c)[idx] = __float2half_rn(v);
+        static_cast<__half*>(c)[idx] = f32_to_f16(v);
 }
 
 template <typename T>

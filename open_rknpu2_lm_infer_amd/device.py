@@ -85,8 +85,19 @@ class DeviceContext:
         h = _Handle(raw, free, f"W{bits} weights from checkpoint storage", self.shared)
         return DeviceWeights(h, bits, k, n_total)
 
-    def workspace(self, bits: int, rows: int, k: int, n: int) -> _Handle:
+    def workspace(self, bits: int, rows: int, k: int, n: int, cached: bool = True) -> _Handle:
+        """The context's workspace for (bits, rows, k, n), created on first use;
+        cached=False creates a new one (sized by the plan switches in force,
+        e.g. for split-K partials under HM_SPLITS) and does not keep it."""
         key = (bits, rows, k, n)
+        if not cached:
+            saved = self._ws.pop(key, None)
+            try:
+                return self.workspace(bits, rows, k, n)
+            finally:
+                self._ws.pop(key, None)
+                if saved is not None:
+                    self._ws[key] = saved
         if key not in self._ws:
             L = F.lib()
             if bits == 4:

@@ -43,13 +43,37 @@ def test_device_linear_matches_oracle_f32_and_f16(ctx, bits, rows):
 
 
 @pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("rows", [3, 4])
+def test_four_row_gemv_quantized_in_blocks(ctx, bits, rows):
+    """HM_GEMV_PREQ=0: the 4-row GEMV quantizes its rows inside every block
+    instead of after a quantization launch; plain and SwiGLU outputs, f32 and
+    f16 activations, identical to the oracle."""
+    k, n = 640, 768
+    codes, scales = R.weights(5, f"dl{bits}", bits, k, n)
+    w = ctx.weights(bits, dev(codes), dev(scales))
+    x = R.activations(5, f"dlQ-x{rows}", rows, k)
+    with D.plan_switch("HM_GEMV_PREQ", 0):
+        for xin in (dev(x), dev(x).half()):
+            y = torch.empty(rows, n, dtype=torch.float32, device="cuda")
+            D.linear(ctx, w, xin, y, rows)
+            m = torch.empty(rows, n // 2, dtype=torch.float32, device="cuda")
+            D.linear(ctx, w, xin, m, rows, swiglu=True)
+            torch.cuda.synchronize()
+            assert np.array_equal(y.cpu().numpy(), oracle.linear(codes, scales, x))
+            assert np.array_equal(m.cpu().numpy(), oracle.linear_swiglu(codes, scales, x))
+
+
+@pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize("rows,variant,n", [(1100, None, 768), (2100, None, 768), (2100, "0", 768),
-                                            (4100, "0", 768), (2100, "0", 640), (300, "0", 896)])
+                                            (4100, "0", 768), (2100, "0", 640), (300, "0", 896),
+                                            (4100, "0", 640), (300, "1", 896), (4100, "1", 640)])
 def test_device_linear_large_row_tiles(ctx, bits, rows, variant, n):
-    """Row counts that select the 128x128 tile, and the 256x256 tile (chosen by
-    the plan for very wide outputs or long K; forced here at a small shape).
-    n = 640 and 896 leave 128 padded columns in the last 256-wide tile, as the
-    2560x151936 lm_head does (plain and SwiGLU stores masked at the edge)."""
+    """Row counts that select the 128x128 tile, and the 256x256 tile (variant
+    0: chosen by the plan for very wide outputs or long K) and the 256x128
+    tile (variant 1), forced here at small shapes. n = 640 and 896 leave 128
+    padded columns in the last 256-wide tile, as the 2560x151936 lm_head does
+    (plain and SwiGLU stores masked at the edge); 4100 and 300 rows end inside
+    a 256-row tile."""
     with D.plan_switch("HM_GEMM_VARIANT", -1 if variant is None else int(variant)):
         _large_row_tiles(ctx, bits, rows, n)
 
