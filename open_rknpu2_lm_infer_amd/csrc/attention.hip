@@ -876,7 +876,11 @@ static int run_host(rk_npu_attention_f16_workspace* workspace, rk_npu_attention_
     const double t0 = now_us();
     const size_t n = (size_t)c->cfg.query_heads * rows * c->cfg.head_dim;
     int rc = RK_NPU_OK;
-    if (hipSetDevice(device_of(w->domain)) != hipSuccess ||
+    // Device-path appends and runs (rk_npu_hip_attention_cache_append / _run)
+    // are enqueued on the caller's streams and may still be writing the
+    // cache's rows or this workspace's partials: wait for them first, as the
+    // host cache calls do.
+    if (hipSetDevice(device_of(w->domain)) != hipSuccess || hipDeviceSynchronize() != hipSuccess ||
         hipMemcpyAsync(w->q, q, n * sizeof(__half), hipMemcpyHostToDevice, w->stream) != hipSuccess ||
         hipStreamSynchronize(w->stream) != hipSuccess)
         rc = RK_NPU_ERR_DEVICE;

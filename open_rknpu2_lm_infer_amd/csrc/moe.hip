@@ -671,7 +671,7 @@ int rk_npu_moe_w8_run_f32(rk_npu_moe_w8_workspace* workspace, const rk_npu_moe_w
     const double t2 = now_us();
     if (hipMemcpyAsync(st ? static_cast<void*>(st) : static_cast<void*>(output), ws->out, xb, hipMemcpyDeviceToHost,
                        s) != hipSuccess ||
-        hipStreamSynchronize(s) != hipSuccess)
+        host_wait(s) != hipSuccess)
         return RK_NPU_ERR_DEVICE;
     if (st) std::memcpy(output, st, xb);
     if (timings) {

@@ -139,6 +139,9 @@ int enqueue_ffn(Workspace* gws, const Weights* gw, Workspace* dws, const Weights
 int ffn_take_error(Workspace* dws);
 
 int device_of(Domain* d);
+// Wait for a host-buffer call's stream (block in hipStreamSynchronize, or
+// poll hipStreamQuery with HM_HOST_SPIN=1).
+hipError_t host_wait(hipStream_t s);
 struct BusyGuard {
     std::atomic<bool>* flag;
     bool ok;

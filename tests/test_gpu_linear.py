@@ -230,10 +230,12 @@ def test_allocation_failure_calls_reclaim_then_retries():
 @pytest.mark.parametrize("bits", [4, 8])
 def test_host_call_staging_small_and_large(backend, bits):
     """Host-buffer calls below the 8 MiB pinned stage (A and C copied through
-    it) and above it (direct pageable copies), back to back on the same
-    workspace: both bit-exact against the oracle."""
+    it) and above it (direct pageable copies), each bit-exact against the
+    oracle. Rows 1, 256 and 3 run on the workspaces of buckets 1, 256 and 4;
+    the 4-row call after the 3-row one reuses the bucket-4 workspace with
+    larger A and C, so its pinned stage grows (freed and allocated again)."""
     n = 128
-    for rows, k in ((1, 8256), (256, 8256), (3, 8256)):
+    for rows, k in ((1, 8256), (256, 8256), (3, 8256), (4, 8256)):
         print(f"bits={bits} rows={rows} k={k} a_bytes={rows * k * 4}", flush=True)
         codes, scales = R.weights(7, f"stage{bits}", bits, k, n)
         x = R.activations(7, f"stage-x{rows}", rows, k)
