@@ -1188,12 +1188,19 @@ struct GemvParams {
     // slot_count[0] of assignment perm[s] (token perm[s] / top, expert
     // ids[perm[s]]): weights and column scales of that expert, activation row
     // s (or the token's pre-quantized row), output row s, partial maxima row s.
+    // perm == nullptr: slot s is assignment s itself (no routing launch); its
+    // blocks return at once when routes[s] is not positive, and when ids[s]
+    // is outside [0, experts) after setting bit 0 of *error.
     const uint8_t* const* b_tab;
     const float* const* s_tab;
     const int* perm;
     const int* ids;
     const int* slot_count;
     int top;
+    const float* routes;
+    int experts;
+    unsigned* error;
+    int x_by_token;  // grouped, rows quantized in the block: activation row = token, not slot
     // Split K (one row, plain epilogue, row maxima as partials): block b is
     // piece b % ksplit of group b / ksplit over its share of the 64-k units.
     // Each piece adds (1 << 40) + (its exact int32 column sum + 2^31) into the
@@ -1470,11 +1477,22 @@ __device__ __forceinline__ void gemv_block(GemvParams P, const int bid, const in
     if constexpr (GROUPED) {
         static_assert(MR == 1 && GPB == 1, "one slot row per block");
         const int s = blockIdx.y;
-        if (s >= P.slot_count[0]) return;  // uniform over the block
-        const int a = P.perm[s], tok = a / P.top, e = P.ids[a];
+        int a = s;
+        if (P.perm) {
+            if (s >= P.slot_count[0]) return;  // uniform over the block
+            a = P.perm[s];
+        } else {
+            if (!(P.routes[s] > 0.0f)) return;  // a skipped route: no contribution
+            const int e0 = P.ids[s];
+            if (e0 < 0 || e0 >= P.experts) {
+                if (threadIdx.x == 0) atomicOr(P.error, 1u);
+                return;
+            }
+        }
+        const int tok = a / P.top, e = P.ids[a];
         P.b = P.b_tab[e];
         P.colscale = P.s_tab[e];
-        P.x = static_cast<const T*>(P.x) + (size_t)s * P.lda;
+        P.x = static_cast<const T*>(P.x) + (size_t)(P.x_by_token ? tok : s) * P.lda;
         if (P.part_in) P.part_in += (size_t)s * P.part_count;
         P.c = static_cast<uint8_t*>(P.c) + (size_t)s * P.ldc * (P.c_type == DT_F32 ? 4 : 2);
         if (P.part_out) P.part_out += (size_t)s * gridDim.x;

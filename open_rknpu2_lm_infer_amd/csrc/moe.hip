@@ -341,8 +341,25 @@ static void launch_slot_gemv(const GemvParams& V, int slots, hipStream_t s) {
 static int enqueue_moe(MoeWork* ws, const MoeBank* b, int rows, const float* input, const int* ids,
                        const float* routes, float* out, hipStream_t s) {
     const int A = rows * ws->top;
-    int rc = enqueue_quant(ws->xws, input, DT_F32, ws->h, rows, QUANT_MOE, RowMax{nullptr, 0}, nullptr, s);
-    if (rc != RK_NPU_OK) return rc;
+    // Decode-sized batches (at most 64 slots): one GEMV block row per
+    // assignment (slot = assignment, no routing launch: the blocks of a
+    // skipped route return at once, those of an out-of-range expert id flag
+    // the error word); gate/up on the tokens' quantized rows -> SwiGLU middle
+    // [slot][inter] and per-block row maxima -> down quantizes each middle
+    // row itself from them. (T=1: 43 -> 26 us with the slot GEMVs.)
+    const bool slot_gemv = A <= 64 && (ws->inter % 16) == 0 && b->ggu.half != 0 &&
+                           (ws->mws->g.K_pad / 16) <= 256 * GEMV_XMAX;
+    // On the slot path the gate/up blocks quantize their token's row
+    // themselves when it is 16-byte aligned and fits their registers (no
+    // quantization launch); otherwise the rows are quantized first.
+    const bool slot_quant = slot_gemv && (ws->h % 16) == 0 && (reinterpret_cast<uintptr_t>(input) & 15) == 0 &&
+                            (b->ggu.K_pad / 16) <= 256 * GEMV_XMAX;
+    int rc = RK_NPU_OK;
+    if (!slot_quant) {
+        rc = enqueue_quant(ws->xws, input, DT_F32, ws->h, rows, QUANT_MOE, RowMax{nullptr, 0}, nullptr, s);
+        if (rc != RK_NPU_OK) return rc;
+    }
+    if (!slot_gemv) {
     RouteParams R;
     R.ids = ids;
     R.routes = routes;
@@ -358,13 +375,8 @@ static int enqueue_moe(MoeWork* ws, const MoeBank* b, int rows, const float* inp
     R.rowmax_count = A;
     R.error = ws->error;
     hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(1024), 0, s, R);
+    }
 
-    // Decode-sized batches (at most 64 slots): one GEMV block row per slot.
-    // gate/up on the tokens' quantized rows -> SwiGLU middle [slot][inter] and
-    // per-block row maxima -> down quantizes each middle row itself from them.
-    // (T=1: 43 -> 26 us.)
-    const bool slot_gemv = A <= 64 && (ws->inter % 16) == 0 && b->ggu.half != 0 &&
-                           (ws->mws->g.K_pad / 16) <= 256 * GEMV_XMAX;
     if (slot_gemv) {
         GemvParams V{};
         V.rule = QUANT_MOE;
@@ -372,14 +384,22 @@ static int enqueue_moe(MoeWork* ws, const MoeBank* b, int rows, const float* inp
         V.M = 1;
         V.b_tab = b->d_gu;
         V.s_tab = b->d_gus;
-        V.perm = ws->perm;
+        V.perm = nullptr;
         V.ids = ids;
-        V.slot_count = ws->counts;
+        V.routes = routes;
+        V.experts = ws->experts;
+        V.error = ws->error;
         V.top = ws->top;
-        V.x = ws->xws->codes;  // unused (rows quantized beforehand)
-        V.diag_codes = ws->xws->codes;
-        V.diag_scale = ws->xws->rowscale;
-        V.diag_rowsum = ws->xws->rowsum;
+        if (slot_quant) {
+            V.x = input;  // the token's f32 row, quantized in every block
+            V.lda = ws->h;
+            V.x_by_token = 1;
+        } else {
+            V.x = ws->xws->codes;  // unused (rows quantized beforehand)
+            V.diag_codes = ws->xws->codes;
+            V.diag_scale = ws->xws->rowscale;
+            V.diag_rowsum = ws->xws->rowsum;
+        }
         V.M_alloc = ws->xws->M_alloc;
         V.c = ws->mws->a_f32;  // middle [slot][inter]
         V.ldc = ws->inter;
@@ -390,7 +410,10 @@ static int enqueue_moe(MoeWork* ws, const MoeBank* b, int rows, const float* inp
         V.K_pad = b->ggu.K_pad;
         V.N_pad = b->ggu.N_pad;
         V.half = b->ggu.half;
-        launch_slot_gemv<float, 4, EPI_SWIGLU_MAX, true>(V, A, s);
+        if (slot_quant)
+            launch_slot_gemv<float, 4, EPI_SWIGLU_MAX, false>(V, A, s);
+        else
+            launch_slot_gemv<float, 4, EPI_SWIGLU_MAX, true>(V, A, s);
 
         GemvParams D{};
         D.rule = QUANT_MOE;
@@ -398,9 +421,11 @@ static int enqueue_moe(MoeWork* ws, const MoeBank* b, int rows, const float* inp
         D.M = 1;
         D.b_tab = b->d_dn;
         D.s_tab = b->d_dns;
-        D.perm = ws->perm;
+        D.perm = nullptr;
         D.ids = ids;
-        D.slot_count = ws->counts;
+        D.routes = routes;
+        D.experts = ws->experts;
+        D.error = ws->error;
         D.top = ws->top;
         D.x = ws->mws->a_f32;
         D.lda = ws->inter;
@@ -507,7 +532,7 @@ static int enqueue_moe(MoeWork* ws, const MoeBank* b, int rows, const float* inp
     }
     CombineParams Cb;
     Cb.contrib = ws->mws->c_f32;
-    Cb.pos = ws->pos;
+    Cb.pos = slot_gemv ? nullptr : ws->pos;
     Cb.routes = routes;
     Cb.shared = shared;
     Cb.rows = rows;

@@ -220,7 +220,7 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void moe_gemm_kernel(MoeGemmParam
 // ---------------------------------------------------------------------------
 struct CombineParams {
     const float* contrib;  // [slots][h]
-    const int* pos;
+    const int* pos;        // slot of each assignment (-1: skipped); nullptr: slot = assignment
     const float* routes;
     const float* shared;  // [rows][h] or nullptr
     int rows, top, h;
@@ -233,8 +233,9 @@ static __global__ __launch_bounds__(256) void moe_combine_kernel(CombineParams P
     if (c >= P.h) return;
     float sum = 0.0f;
     for (int rank = 0; rank < P.top; ++rank) {
-        const int s = P.pos[r * P.top + rank];
-        if (s >= 0) sum = __builtin_fmaf(P.contrib[(size_t)s * P.h + c], P.routes[r * P.top + rank], sum);
+        const int a = r * P.top + rank;
+        const int s = P.pos ? P.pos[a] : (P.routes[a] > 0.0f ? a : -1);
+        if (s >= 0) sum = __builtin_fmaf(P.contrib[(size_t)s * P.h + c], P.routes[a], sum);
     }
     if (P.shared) sum = sum + P.shared[(size_t)r * P.h + c];
     P.out[(size_t)r * P.h + c] = sum;

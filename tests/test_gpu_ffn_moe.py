@@ -10,6 +10,10 @@ from open_rknpu2_lm_infer_amd import _ffi as F
 from open_rknpu2_lm_infer_amd import npu
 from tests import refdata as R
 
+# imported before the library loads (as in the other device-test modules):
+# the device-path test below hands torch tensors to the C ABI
+torch = pytest.importorskip("torch")
+
 pytestmark = pytest.mark.gpu
 
 
@@ -237,3 +241,56 @@ def test_resident_moe_equals_paged_composition_on_gpu():
                 s = fma_vec(by_job[(r, k)], w[r, k], s)
         want[r] = s
     assert np.array_equal(out, want)
+
+
+@pytest.mark.parametrize("rows", [1, 3])
+def test_moe_device_entry_aligned_unaligned_and_bad_ids(rows):
+    """rk_npu_hip_moe_run on device buffers (the decode-sized slot path): an
+    aligned input row is quantized inside the routed gate/up blocks, an input
+    off 16-byte alignment is quantized by a launch first; both equal the
+    oracle, with a skipped (zero) route and a repeated expert. An out-of-range
+    expert id is reported by rk_npu_hip_moe_status (once: the report clears)."""
+    from open_rknpu2_lm_infer_amd import device as D
+    h, inter, experts, top = 256, 96, 6, 4
+    gate, down = moe_bank(h, inter, experts, 8, f"moedev{rows}")
+    L = F.lib()
+    ctx = D.DeviceContext(9)
+    arr = (F.rk_npu_moe_w8_expert * experts)()
+    for e in range(experts):
+        arr[e] = F.rk_npu_moe_w8_expert(gate[e].codes.ctypes.data_as(F.i8p), gate[e].scales.ctypes.data_as(F.f32p),
+                                        down[e].codes.ctypes.data_as(F.i8p), down[e].scales.ctypes.data_as(F.f32p))
+    cfg = F.rk_npu_moe_w8_config()
+    L.rk_npu_moe_w8_config_init(ctypes.byref(cfg), h, inter, experts, 0, top, 8)
+    bank = npu._Handle(L.rk_npu_moe_w4w8_weights_create(ctx.domain, ctypes.byref(cfg.weights), arr),
+                       L.rk_npu_moe_w8_weights_free, "MoE bank", ctx.shared)
+    work = npu._Handle(L.rk_npu_moe_w4w8_workspace_create(ctx.domain, ctypes.byref(cfg)),
+                       L.rk_npu_moe_w8_workspace_free, "MoE workspace", ctx.shared)
+    x = R.activations(4, f"moedev-x{rows}", rows, h)
+    ids, w = routed(rows, experts, top, f"moedev-r{rows}")
+    ids[0, 1] = ids[0, 0]  # a repeated expert
+    w[-1, 2] = 0.0         # a skipped route
+    ref = oracle.moe([(g.codes, g.scales) for g in gate], [(d.codes, d.scales) for d in down], x, ids, w)
+    d_ids = torch.from_numpy(ids).cuda()
+    d_w = torch.from_numpy(w).cuda()
+    y = torch.empty(rows, h, dtype=torch.float32, device="cuda")
+    buf = torch.zeros(rows * h + 4, dtype=torch.float32, device="cuda")
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for offset in (0, 1):  # 1 float: the input is off 16-byte alignment
+        xin = buf[offset:offset + rows * h]
+        xin.copy_(torch.from_numpy(x.reshape(-1)))
+        y.fill_(float("nan"))
+        rc = L.rk_npu_hip_moe_run(work.raw, bank.raw, rows, ctypes.c_void_p(xin.data_ptr()),
+                                  ctypes.c_void_p(d_ids.data_ptr()), ctypes.c_void_p(d_w.data_ptr()),
+                                  ctypes.c_void_p(y.data_ptr()), stream)
+        assert rc == 0
+        assert L.rk_npu_hip_moe_status(work.raw) == 0
+        assert np.array_equal(y.cpu().numpy(), ref), f"input offset {offset} floats"
+    bad = ids.copy()
+    bad[0, 0] = experts  # out of range
+    d_bad = torch.from_numpy(bad).cuda()
+    rc = L.rk_npu_hip_moe_run(work.raw, bank.raw, rows, ctypes.c_void_p(buf.data_ptr()),
+                              ctypes.c_void_p(d_bad.data_ptr()), ctypes.c_void_p(d_w.data_ptr()),
+                              ctypes.c_void_p(y.data_ptr()), stream)
+    assert rc == 0
+    assert L.rk_npu_hip_moe_status(work.raw) == F.RK_NPU_ERR_PARAM
+    assert L.rk_npu_hip_moe_status(work.raw) == 0
