@@ -385,14 +385,27 @@ static Plan plan_gemm(int rows, const Geometry& g, int variant) {
             if (t256 >= 8LL * cus || (g.K_pad >= 4096 && t128 > 2LL * cus)) v = V256x256;
         }
     }
+    const int KT = g.K_pad / 64;
+    const int cus = device_cus();
+    int f = 1;
+    // Long K over more than 256 rows with too few 64x128 tiles for the CUs:
+    // the 128x128 tile split into as many K pieces as one round of blocks
+    // holds (9728x2560 down at M = 512: 80 tiles x 3 pieces 37.4 us against
+    // 64x128 x 3 pieces 41.1 us, bench.py --tile-sweep).
+    const long long t64 = (long long)((rows + 63) / 64) * (g.N_pad / 128);
+    if (variant < 0 && switch_value(SW_GEMM_VARIANT) < 0 && v == V64x128 && rows > 256 && KT >= 128 && t64 < cus) {
+        const int t128 = ((rows + 127) / 128) * (g.N_pad / 128);
+        const int f128 = std::min(std::min(cus / t128, KT / 24), 8);
+        if (f128 >= 2) {
+            v = V128x128;
+            f = f128;
+        }
+    }
     p.variant = v;
     p.bm = kBM[v];
     p.bn = kBN[v];
     p.tiles = ((rows + p.bm - 1) / p.bm) * (g.N_pad / p.bn);
-    const int KT = g.K_pad / 64;
-    const int cus = device_cus();
-    int f = 1;
-    if ((v == V64x128 || v == V128x128) && p.tiles < cus && KT >= 128)
+    if (f == 1 && (v == V64x128 || v == V128x128) && p.tiles < cus && KT >= 128)
         f = std::max(1, std::min(std::min((3 * cus / 2 + p.tiles - 1) / p.tiles, KT / 24), 8));
     const int forced_f = switch_value(SW_SPLITS);
     p.ksplit = forced_f > 0 ? std::min(forced_f, KT) : f;

@@ -86,6 +86,11 @@ __device__ __forceinline__ __half f32_to_f16(float v) {
     return __float2half_rn(v);
 }
 
+template <int V>
+struct IntTag {
+    static constexpr int value = V;
+};
+
 __device__ __forceinline__ void store_out(void* c, int c_type, size_t idx, float v) {
     if (c_type == DT_F32)
         static_cast<float*>(c)[idx] = v;
@@ -893,24 +898,29 @@ __device__ __forceinline__ void gemm_epilogue(
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave / WGN, wn = wave % WGN;
     const int half_id = lane >> 5, l32 = lane & 31;
-    const int esz = c_type == DT_F32 ? 4 : 2;
     // Output columns this wave owns (SwiGLU: TN/2, contiguous from out0).
     constexpr int OUTC = (EPI == EPI_PLAIN) ? TN : TN / 2;
     const int out0 = (EPI == EPI_PLAIN) ? n0 + wn * TN : (n0 + wn * TN) >> 1;
     const int n_out = (EPI == EPI_PLAIN) ? N : N / 2;
 
     // STAGED (the output has a 16-byte aligned base and row pitch): rows are
-    // staged through LDS (SwiGLU values in f32, so the row max is taken on
-    // exact values; plain values in the output type) and written as 16-byte
-    // runs. Otherwise each lane stores its own elements. Values and rounding
-    // are identical either way.
+    // staged through LDS in f32 (SwiGLU: the row max is taken on exact
+    // values) and written as 16-byte runs, fp16 outputs converted from the
+    // staged f32 values there. Otherwise each lane stores its own elements.
+    // Values and rounding (f32, then f32 -> fp16) are identical either way.
+    // Where registers allow (W8, or one row fragment per wave) a fragment's
+    // 16 row scales (and W4 corrections) are read from LDS at once, so no
+    // value waits on its own LDS read; with one block per CU (small M)
+    // nothing else hides those waits. (The W4 tiles of two row fragments per
+    // wave would lose a resident block to the registers; their epilogue runs
+    // under other blocks' main loops.)
     constexpr bool staged = STAGED;
-    const int ssz = (EPI == EPI_PLAIN) ? esz : 4;  // staged element size
+    constexpr bool BATCH = (BITS == 8) || (FM == 1);
     constexpr int WAVE_LDS = C::SMEM / NW;
     constexpr int FIT = WAVE_LDS / (32 * (OUTC * 4 + 16));
     static_assert(FIT >= 1, "epilogue staging does not fit in LDS");
     constexpr int FPI = FIT >= FM ? FM : ((FIT >= 2 && FM % 2 == 0) ? 2 : 1);
-    const int pitch = OUTC * ssz + 16;
+    constexpr int pitch = OUTC * 4 + 16;
     uint8_t* wl = smem + wave * WAVE_LDS;
     if (threadIdx.x < BM) {
         s_rs[threadIdx.x] = pre.rs;
@@ -923,19 +933,29 @@ __device__ __forceinline__ void gemm_epilogue(
 #pragma unroll
         for (int ii = 0; ii < FPI; ++ii) {
             const int i = i0 + ii;
+            float srow[BATCH ? 16 : 1];
+            int scorr[BATCH ? 16 : 1];
+            if constexpr (BATCH) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int local = wm * TM + i * 32 + (r >> 2) * 8 + half_id * 4 + (r & 3);
+                    srow[r] = s_rs[local];
+                    scorr[r] = (BITS == 4) ? s_rc[local] : 0;
+                }
+            }
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int rr = (r >> 2) * 8 + half_id * 4 + (r & 3);
                 const int local = wm * TM + i * 32 + rr;
                 uint8_t* lrow = wl + (ii * 32 + rr) * pitch;
-                const float s_row = s_rs[local];
-                const int corr = s_rc[local];
+                const float s_row = BATCH ? srow[BATCH ? r : 0] : s_rs[local];
+                const int corr = BATCH ? scorr[BATCH ? r : 0] : s_rc[local];
                 if (EPI == EPI_PLAIN) {
 #pragma unroll
                     for (int j = 0; j < FN; ++j) {
                         const float y = ((float)(acc[i][j][r] - corr) * s_row) * pre.cs[j];
                         if constexpr (staged) {
-                            store_out(lrow, c_type, j * 32 + l32, y);
+                            reinterpret_cast<float*>(lrow)[j * 32 + l32] = y;
                         } else {
                             const int p = n0 + wn * TN + j * 32 + l32;
                             int out_row, src_row;
@@ -973,22 +993,40 @@ __device__ __forceinline__ void gemm_epilogue(
         __syncthreads();
         if (EPI == EPI_PLAIN) {
             // 16-byte runs: chunk q of the staged rows -> (row, 16/esz columns).
-            const int per = 16 / esz, cpr = OUTC / per;
-            for (int q = lane; q < FPI * 32 * cpr; q += 64) {
-                const int lr = q / cpr, cc = (q - lr * cpr) * per;
-                int out_row, src_row;
-                if (!row_of(wm * TM + i0 * 32 + lr, out_row, src_row)) continue;
-                const int p = out0 + cc;
-                const int col = orig_col(p, half), valid = N - p;
-                const uint8_t* src = wl + lr * pitch + cc * esz;
-                uint8_t* dst = static_cast<uint8_t*>(c) + ((size_t)out_row * ldc + col) * esz;
-                if (valid >= per) {
-                    *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(src);
-                } else {
-                    for (int t = 0; t < valid; ++t)
-                        for (int bb = 0; bb < esz; ++bb) dst[t * esz + bb] = src[t * esz + bb];
+            auto runs = [&](auto per_tag) {
+                constexpr int per = decltype(per_tag)::value, cpr = OUTC / per;
+                for (int q = lane; q < FPI * 32 * cpr; q += 64) {
+                    const int lr = q / cpr, cc = (q - lr * cpr) * per;
+                    int out_row, src_row;
+                    if (!row_of(wm * TM + i0 * 32 + lr, out_row, src_row)) continue;
+                    const int p = out0 + cc;
+                    const int col = orig_col(p, half), valid = N - p;
+                    const float* src = reinterpret_cast<const float*>(wl + lr * pitch) + cc;
+                    const size_t at = (size_t)out_row * ldc + col;
+                    if (valid >= per) {
+                        if constexpr (per == 4) {
+                            *reinterpret_cast<float4*>(static_cast<float*>(c) + at) =
+                                *reinterpret_cast<const float4*>(src);
+                        } else {
+                            const float4 lo = reinterpret_cast<const float4*>(src)[0];
+                            const float4 hi = reinterpret_cast<const float4*>(src)[1];
+                            const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+                            unsigned w[4];
+#pragma unroll
+                            for (int e = 0; e < 4; ++e)
+                                w[e] = (unsigned)__half_as_ushort(f32_to_f16(v[2 * e])) |
+                                       ((unsigned)__half_as_ushort(f32_to_f16(v[2 * e + 1])) << 16);
+                            *reinterpret_cast<uint4*>(static_cast<__half*>(c) + at) = uint4{w[0], w[1], w[2], w[3]};
+                        }
+                    } else {
+                        for (int t = 0; t < valid; ++t) store_out(c, c_type, at + t, src[t]);
+                    }
                 }
-            }
+            };
+            if (c_type == DT_F32)
+                runs(IntTag<4>{});
+            else
+                runs(IntTag<8>{});
         } else {
             // 4 staged f32 values per lane: max |o| over the row's lanes (CPR
             // consecutive lanes), conversion to the output type, one store.

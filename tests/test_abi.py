@@ -110,9 +110,12 @@ def test_plans():
     # 64x128 tiles up to 1024 rows, then 128x128; above 2048 rows 256x256 for
     # very wide outputs and for long K once 128x128 tiles overflow two per CU;
     # K split in pieces when the tiles leave CUs idle and K is long (256 CUs
-    # assumed without a GPU)
+    # assumed without a GPU): above 256 rows on the 128x128 tile, as many
+    # pieces as one round of blocks holds; up to 256 rows on 64x128
     assert L.rk_npu_hip_linear_plan(512, 9728, 2560, 8, ctypes.byref(plan)) == 0
-    assert (plan.kind, plan.block_m, plan.block_n, plan.k_splits, plan.grid) == (1, 64, 128, 3, 8 * 20 * 3)
+    assert (plan.kind, plan.block_m, plan.block_n, plan.k_splits, plan.grid) == (1, 128, 128, 3, 4 * 20 * 3)
+    assert L.rk_npu_hip_linear_plan(256, 9728, 2560, 8, ctypes.byref(plan)) == 0
+    assert (plan.kind, plan.block_m, plan.block_n, plan.k_splits, plan.grid) == (1, 64, 128, 5, 4 * 20 * 5)
     assert L.rk_npu_hip_linear_plan(512, 4096, 2560, 8, ctypes.byref(plan)) == 0
     assert (plan.kind, plan.block_m, plan.block_n, plan.k_splits, plan.grid) == (1, 64, 128, 1, 8 * 20)
     assert L.rk_npu_hip_linear_plan(2048, 9728, 2560, 8, ctypes.byref(plan)) == 0

@@ -112,6 +112,25 @@ def test_unaligned_output_matches_oracle(ctx, bits, dtype):
         assert np.array_equal(y.cpu().numpy(), ref.astype(np.float16) if dtype == "f16" else ref)
 
 
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("rows", [300, 512])
+def test_long_k_split_plan_above_256_rows(ctx, bits, rows):
+    """Long K (8192) over more than 256 rows: the plan splits K on the 128x128
+    tile (pieces summed through int32 partials, then the epilogue); plain
+    fp16 and SwiGLU f32 outputs identical to the oracle."""
+    k, n = 8192, 256
+    codes, scales = R.weights(5, f"lks{bits}", bits, k, n)
+    w = ctx.weights(bits, dev(codes), dev(scales))
+    x = R.activations(5, f"lks-x{rows}", rows, k)
+    y = torch.empty(rows, n, dtype=torch.float16, device="cuda")
+    D.linear(ctx, w, dev(x).half(), y, rows)
+    m = torch.empty(rows, n // 2, dtype=torch.float32, device="cuda")
+    D.linear(ctx, w, dev(x), m, rows, swiglu=True)
+    torch.cuda.synchronize()
+    assert np.array_equal(y.cpu().numpy(), oracle.linear(codes, scales, x).astype(np.float16))
+    assert np.array_equal(m.cpu().numpy(), oracle.linear_swiglu(codes, scales, x))
+
+
 @pytest.mark.parametrize("splits", [2, 3])
 def test_split_k_switch_is_bit_exact(ctx, splits):
     """HM_SPLITS: K pieces per tile sum through int32 partials; same result."""
