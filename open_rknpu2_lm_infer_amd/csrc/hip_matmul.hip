@@ -415,7 +415,10 @@ static Plan plan_gemm(int rows, const Geometry& g, int variant) {
 
 Plan plan_linear(int rows, const Geometry& g) {
     const int mr = rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : 8;
-    if (rows <= 8 && g.K_pad * mr <= GEMV_MAX_LDS && switch_value(SW_FORCE_GEMM) == 0) {
+    // (2 to 8 rows take their GEMV dot products on the matrix cores, which
+    // needs K_pad % 128 == 0 for W8 and % 256 for W4; other K take the GEMM)
+    if (rows <= 8 && g.K_pad * mr <= GEMV_MAX_LDS && switch_value(SW_FORCE_GEMM) == 0 &&
+        (mr == 1 || g.K_pad % (g.bits == 8 ? 128 : 256) == 0)) {
         Plan p{};
         p.kind = 0;
         p.mr = mr;
@@ -783,7 +786,7 @@ int enqueue_linear(Workspace* ws, const Weights* w, const void* x, int x_type, l
     const Geometry& g = w->g;
     const Plan pv = plan_linear(rows, g);
     if (pv.kind == 0) {
-        GemvParams V;
+        GemvParams V{};
         V.x = x;
         V.lda = lda;
         V.rule = rule;

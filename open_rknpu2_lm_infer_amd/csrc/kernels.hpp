@@ -1850,7 +1850,60 @@ __device__ __forceinline__ void gemv_block(GemvParams P, const int bid, const in
         }
     }
 
-    // 4. Dots: chunk q = tid + NTHR*r of the group's stream.
+    // 4. Dots: chunk q = tid + NTHR*r of the group's stream. One row:
+    // v_dot4 per chunk. 2 to 8 rows, on the matrix cores (the plan requires
+    // chunks per tile to be a multiple of 64, K_pad % 128 == 0 for W8 and
+    // % 256 for W4, so that a wave's round lies in one tile): a wave's 64 chunks of a round are
+    // planes p0..p0+7 (p0 a multiple of 8) of one tile, lane L holding plane
+    // p0 + (L >> 3), column L & 7. Read as the B operand of
+    // v_mfma_i32_16x16x64_i8 (lane L: column n = L & 15, k = 16 * (L >> 4) +
+    // 0..15), column n takes plane p0 + 2g + (n >> 3) for k chunk g: columns
+    // n < 8 see the even planes, n >= 8 the odd ones. One MFMA against the
+    // even planes' activation codes (A lane L: row L & 15, the same k chunk)
+    // and one against the odd planes' give, in columns 0-7 of the first and
+    // 8-15 of the second, exact partial sums of the 8 tile columns; W4 planes
+    // hold two 16-k chunks (low and high nibbles), so four MFMAs. Rows past
+    // MR read row (L & 15) % MR; their outputs are not used.
+    v4i accE[TPB], accO[TPB];
+    if constexpr (MR >= 2) {
+#pragma unroll
+        for (int t = 0; t < TPB; ++t) accE[t] = accO[t] = v4i{0, 0, 0, 0};
+    }
+    auto consume_mf = [&](int w, const auto& buf) {
+        const int mrow = lane & (MR - 1), g = lane >> 4;
+#pragma unroll
+        for (int i = 0; i < RW; ++i) {
+            const int q0 = wave * 64 + NTHR * (w * RW + i);  // the wave's first chunk (uniform)
+            if (q0 >= CPG) continue;
+            int tq, rq;
+            locate(q0, tq, rq);
+            const int p0 = rq >> 3;
+            const v4i wv = __builtin_bit_cast(v4i, buf[i]);
+            auto codes = [&](int kg) { return *reinterpret_cast<const v4i*>(sa + (kg * MR + mrow) * 16); };
+            v4i e = tq == 0 ? accE[0] : accE[TPB - 1];
+            v4i o = tq == 0 ? accO[0] : accO[TPB - 1];
+            if constexpr (BITS == 8) {
+                const v4i ae = codes(p0 + 2 * g), ao = codes(p0 + 2 * g + 1);
+                e = __builtin_amdgcn_mfma_i32_16x16x64_i8(ae, wv, e, 0, 0, 0);
+                o = __builtin_amdgcn_mfma_i32_16x16x64_i8(ao, wv, o, 0, 0, 0);
+            } else {
+                const int kb = 4 * ((p0 >> 1) + g);
+                const v4i a0 = codes(kb), a1 = codes(kb + 1), a2 = codes(kb + 2), a3 = codes(kb + 3);
+                const v4i lo = wv & 0x0F0F0F0F, hi = (wv >> 4) & 0x0F0F0F0F;
+                e = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, lo, e, 0, 0, 0);
+                o = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, lo, o, 0, 0, 0);
+                e = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2, hi, e, 0, 0, 0);
+                o = __builtin_amdgcn_mfma_i32_16x16x64_i8(a3, hi, o, 0, 0, 0);
+            }
+            if (tq == 0) {
+                accE[0] = e;
+                accO[0] = o;
+            } else {
+                accE[TPB - 1] = e;
+                accO[TPB - 1] = o;
+            }
+        }
+    };
     int acc[TPB][MR];
 #pragma unroll
     for (int t = 0; t < TPB; ++t)
@@ -1903,32 +1956,52 @@ __device__ __forceinline__ void gemv_block(GemvParams P, const int bid, const in
     };
     // Windows ping-pong between the two register sets (longer K only); with
     // one set, a further window is requested after the previous one is used.
-    if constexpr (NW == 2) {
-        for (int w = 0; w < NWIN; w += 2) {
-            consume(w, wa);
-            if (w + 2 < NWIN) load_window(w + 2, wa);
-            if (w + 1 < NWIN) {
-                consume(w + 1, wb);
-                if (w + 3 < NWIN) load_window(w + 3, wb);
+    auto run_windows = [&](auto&& use) {
+        if constexpr (NW == 2) {
+            for (int w = 0; w < NWIN; w += 2) {
+                use(w, wa);
+                if (w + 2 < NWIN) load_window(w + 2, wa);
+                if (w + 1 < NWIN) {
+                    use(w + 1, wb);
+                    if (w + 3 < NWIN) load_window(w + 3, wb);
+                }
+            }
+        } else {
+            for (int w = 0; w < NWIN; ++w) {
+                if (w > 0) load_window(w, wa);
+                use(w, wa);
             }
         }
-    } else {
-        for (int w = 0; w < NWIN; ++w) {
-            if (w > 0) load_window(w, wa);
-            consume(w, wa);
-        }
-    }
+    };
+    constexpr bool mfd = MR >= 2;
+    if constexpr (mfd)
+        run_windows(consume_mf);
+    else
+        run_windows(consume);
 
     // 5. Reduce over threads of the same column: lane moves within a wave, LDS
-    // across waves; wave 0 finishes the 8 columns.
+    // across waves; wave 0 finishes the 8 columns. (Matrix-core dots: lane L
+    // holds rows 4 * (L >> 4) + 0..3 of column L & 15; column c < 8 is the
+    // even-plane sum of lane c plus the odd-plane sum of lane c + 8.)
+    if constexpr (mfd) {
 #pragma unroll
-    for (int t = 0; t < TPB; ++t)
+        for (int t = 0; t < TPB; ++t)
 #pragma unroll
-        for (int m = 0; m < MR; ++m) {
-            int v = acc[t][m];
-            v = sum_mod8(v);
-            if (lane < 8) red[wave][t][m][c8] = v;
-        }
+            for (int i = 0; i < 4; ++i) {
+                const int v = accE[t][i] + __shfl_down(accO[t][i], 8, 16);
+                const int m = 4 * (lane >> 4) + i;
+                if ((lane & 15) < 8 && m < MR) red[wave][t][m][lane & 7] = v;
+            }
+    } else {
+#pragma unroll
+        for (int t = 0; t < TPB; ++t)
+#pragma unroll
+            for (int m = 0; m < MR; ++m) {
+                int v = acc[t][m];
+                v = sum_mod8(v);
+                if (lane < 8) red[wave][t][m][c8] = v;
+            }
+    }
     wait_lgkmcnt0();
     __builtin_amdgcn_s_barrier();
     if constexpr (SPLITK) {

@@ -104,6 +104,16 @@ def test_plans():
     assert (plan.kind, plan.block_m, plan.block_n, plan.k_splits, plan.grid) == (0, 1, 8, 1, 19456 // 8)
     assert L.rk_npu_hip_linear_plan(8, 2560, 6144, 8, ctypes.byref(plan)) == 0
     assert (plan.kind, plan.block_m) == (0, 8)
+    # 2 to 8 rows need K_pad % 128 == 0 (W8) or % 256 (W4) for the GEMV's
+    # matrix-core dots; other K take the GEMM
+    assert L.rk_npu_hip_linear_plan(4, 640, 768, 8, ctypes.byref(plan)) == 0
+    assert (plan.kind, plan.block_m) == (0, 4)
+    assert L.rk_npu_hip_linear_plan(4, 640, 768, 4, ctypes.byref(plan)) == 0
+    assert (plan.kind, plan.block_m, plan.block_n) == (1, 32, 128)
+    assert L.rk_npu_hip_linear_plan(1, 640, 768, 4, ctypes.byref(plan)) == 0
+    assert (plan.kind, plan.block_m) == (0, 1)
+    assert L.rk_npu_hip_linear_plan(4, 768, 768, 4, ctypes.byref(plan)) == 0
+    assert (plan.kind, plan.block_m) == (0, 4)
     # a K too long for the GEMV's quantized rows in LDS (8 x 9728 bytes) takes the GEMM
     assert L.rk_npu_hip_linear_plan(8, 9728, 2560, 8, ctypes.byref(plan)) == 0
     assert (plan.kind, plan.block_m, plan.block_n) == (1, 32, 128)

@@ -48,8 +48,8 @@ def test_four_row_gemv_quantized_in_blocks(ctx, bits, rows):
     """HM_GEMV_PREQ=0: the 4-row GEMV quantizes its rows inside every block
     instead of after a quantization launch; plain and SwiGLU outputs, f32 and
     f16 activations, identical to the oracle."""
-    k, n = 640, 768
-    codes, scales = R.weights(5, f"dl{bits}", bits, k, n)
+    k, n = 768, 768
+    codes, scales = R.weights(5, f"dlq{bits}", bits, k, n)
     w = ctx.weights(bits, dev(codes), dev(scales))
     x = R.activations(5, f"dlQ-x{rows}", rows, k)
     with D.plan_switch("HM_GEMV_PREQ", 0):
@@ -61,6 +61,35 @@ def test_four_row_gemv_quantized_in_blocks(ctx, bits, rows):
             torch.cuda.synchronize()
             assert np.array_equal(y.cpu().numpy(), oracle.linear(codes, scales, x))
             assert np.array_equal(m.cpu().numpy(), oracle.linear_swiglu(codes, scales, x))
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("k", [640, 768, 2560, 9728])
+def test_gemv_matrix_core_dots(ctx, bits, k):
+    """2 to 8 rows: the GEMV's dot products on the matrix cores (K_pad a
+    multiple of 128 for W8, 256 for W4; W4 at K = 640 takes the GEMM), rows
+    quantized in the block or beforehand (HM_GEMV_PREQ), fp16 and f32 rows,
+    plain and SwiGLU, the 512-thread two-window blocks at K = 9728: identical
+    to the oracle."""
+    n = 256
+    codes, scales = R.weights(5, f"gmf{bits}-{k}", bits, k, n)
+    w = ctx.weights(bits, dev(codes), dev(scales))
+    for rows in (2, 3, 4, 5, 8):
+        if rows * k > 60 * 1024:
+            continue  # rows too long for the GEMV's LDS: the GEMM runs them
+        x = R.activations(5, f"gmf-x{rows}-{k}", rows, k)
+        ref, ref_sw = oracle.linear(codes, scales, x), oracle.linear_swiglu(codes, scales, x)
+        for preq in (1, 0):
+            for xin in (dev(x), dev(x).half()):
+                print(f"W{bits} K={k} rows={rows} preq={preq} {xin.dtype}", flush=True)
+                with D.plan_switch("HM_GEMV_PREQ", preq):
+                    y = torch.empty(rows, n, dtype=torch.float32, device="cuda")
+                    D.linear(ctx, w, xin, y, rows)
+                    m = torch.empty(rows, n // 2, dtype=torch.float32, device="cuda")
+                    D.linear(ctx, w, xin, m, rows, swiglu=True)
+                    torch.cuda.synchronize()
+                assert np.array_equal(y.cpu().numpy(), ref)
+                assert np.array_equal(m.cpu().numpy(), ref_sw)
 
 
 @pytest.mark.parametrize("bits", [4, 8])
