@@ -155,6 +155,9 @@ int rk_npu_hip_inject_alloc_failures(int count);
  *                    give up at once (tests of the failure report)
  *   HM_GEMV_PREQ     -1: 4 rows are quantized by a launch before the GEMV;
  *                    0: inside the GEMV blocks wherever the rows fit
+ *   HM_GEMV_COMBINE  1: a one-token MoE call with a shared expert runs the
+ *                    combine in the shared down GEMV's epilogue where that
+ *                    GEMV allows; 0: always as a separate launch
  *   HM_HOST_SPIN     0: a host-buffer call (rk_npu_*_run_f32, _run_dynamic,
  *                    the MoE run) waits for its work in hipStreamSynchronize;
  *                    1: by polling its stream (slower here)

@@ -305,7 +305,7 @@ static const int kBN[] = {256, 128, 128, 128, 128};
 // variable, read once when the library first plans a launch; afterwards only
 // rk_npu_hip_set_switch changes it, so no launch reads the environment.
 enum SwitchId { SW_GEMM_VARIANT, SW_SPLITS, SW_FORCE_GEMM, SW_GEMV_QW, SW_GEMV_SPLITS, SW_FFN_FUSED, SW_FFN_SPIN,
-                SW_GEMV_PREQ, SW_HOST_SPIN, SW_COUNT };
+                SW_GEMV_PREQ, SW_HOST_SPIN, SW_GEMV_COMBINE, SW_COUNT };
 struct SwitchDef {
     const char* name;
     int fallback;
@@ -313,7 +313,7 @@ struct SwitchDef {
 static const SwitchDef kSwitches[SW_COUNT] = {
     {"HM_GEMM_VARIANT", -1}, {"HM_SPLITS", 0},         {"HM_FORCE_GEMM", 0}, {"HM_GEMV_QW", -1},
     {"HM_GEMV_SPLITS", 0},   {"HM_FFN_FUSED", 0},      {"HM_FFN_SPIN", 1 << 16}, {"HM_GEMV_PREQ", -1},
-    {"HM_HOST_SPIN", 0}};
+    {"HM_HOST_SPIN", 0},     {"HM_GEMV_COMBINE", 1}};
 
 static std::atomic<int>* switch_table() {
     static std::atomic<int> table[SW_COUNT];
@@ -710,6 +710,21 @@ static void launch_gemv_w(const GemvParams& V, int groups, size_t lds, hipStream
         hipLaunchKernelGGL((gemv_kernel<T, MR, BITS, EPI, 8, 2, PREQ, 1, 512>), dim3(groups), dim3(512), lds, s, V);
 }
 
+// The one-row plain GEMV with the MoE combine in its epilogue.
+template <int BITS>
+static void launch_gemv_combine(const GemvParams& V, int groups, int rounds, size_t lds, hipStream_t s) {
+    if (rounds <= 3)
+        hipLaunchKernelGGL((gemv_combine_kernel<BITS, 3>), dim3(groups), dim3(256), lds, s, V);
+    else if (rounds <= 4)
+        hipLaunchKernelGGL((gemv_combine_kernel<BITS, 4>), dim3(groups), dim3(256), lds, s, V);
+    else if (rounds <= 5)
+        hipLaunchKernelGGL((gemv_combine_kernel<BITS, 5>), dim3(groups), dim3(256), lds, s, V);
+    else if (rounds <= 6)
+        hipLaunchKernelGGL((gemv_combine_kernel<BITS, 6>), dim3(groups), dim3(256), lds, s, V);
+    else
+        hipLaunchKernelGGL((gemv_combine_kernel<BITS, 8>), dim3(groups), dim3(256), lds, s, V);
+}
+
 // Split-K GEMV (one row, plain epilogue): rounds of the largest piece.
 template <typename T, int BITS>
 static void launch_gemv_split(const GemvParams& V, int grid, int rounds, size_t lds, hipStream_t s) {
@@ -782,8 +797,10 @@ static void launch_gemv_epi(int epi, int mr, const GemvParams& V, int grid, size
 }
 
 int enqueue_linear(Workspace* ws, const Weights* w, const void* x, int x_type, long lda, int rows, int rule,
-                   RowMax in_max, void* c, int c_type, long ldc, int epi, RowMax* out_max, hipStream_t s) {
+                   RowMax in_max, void* c, int c_type, long ldc, int epi, RowMax* out_max, hipStream_t s,
+                   const GemvCombine* comb) {
     const Geometry& g = w->g;
+    if (comb && comb->combined) *comb->combined = false;
     const Plan pv = plan_linear(rows, g);
     if (pv.kind == 0) {
         GemvParams V{};
@@ -863,7 +880,21 @@ int enqueue_linear(Workspace* ws, const Weights* w, const void* x, int x_type, l
         char name[64];
         std::snprintf(name, sizeof(name), "gemv<mr=%d,w%d,epi=%d>", pv.mr, g.bits, epi);
         const int slot = prof_begin(s, 0, g.bits, epi, rows, g.K, g.N, name);
-        if (ksplit > 1) {
+        const bool combine = comb && switch_value(SW_GEMV_COMBINE) != 0 && rows == 1 && epi == EPI_PLAIN && !preq &&
+                             qwn == 0 && ksplit == 1 &&
+                             x_type == DT_F32 && c_type == DT_F32 && comb->top >= 1 && comb->top <= GEMV_COMB_TOP &&
+                             w_rounds <= 8 && comb->h == g.N;
+        if (combine) {
+            V.comb_contrib = comb->contrib;
+            V.comb_routes = comb->routes;
+            V.comb_top = comb->top;
+            V.comb_h = comb->h;
+            if (g.bits == 8)
+                launch_gemv_combine<8>(V, grid, w_rounds, lds, s);
+            else
+                launch_gemv_combine<4>(V, grid, w_rounds, lds, s);
+            if (comb->combined) *comb->combined = true;
+        } else if (ksplit > 1) {
             V.ksplit = ksplit;
             const size_t piece_lds = (size_t)64 * piece_units;
             if (x_type == DT_F32) {
@@ -1104,7 +1135,8 @@ int ffn_take_error(Workspace* dws) {
 }
 
 int enqueue_ffn(Workspace* gws, const Weights* gw, Workspace* dws, const Weights* dw, const void* A, int a_type,
-                void* C, int c_type, int rows, int rule, hipStream_t s) {
+                void* C, int c_type, int rows, int rule, hipStream_t s, const GemvCombine* comb) {
+    if (comb && comb->combined) *comb->combined = false;
     FfnFusedPlan fp;
     if (plan_ffn_fused(gw, dw, A, a_type, rows, fp) &&
         enqueue_ffn_fused(gws, gw, dws, dw, A, a_type, C, c_type, rule, fp, s))
@@ -1115,7 +1147,7 @@ int enqueue_ffn(Workspace* gws, const Weights* gw, Workspace* dws, const Weights
                             EPI_SWIGLU_MAX, &mid_max, s);
     if (rc == RK_NPU_OK)
         rc = enqueue_linear(dws, dw, gws->c_f32, DT_F32, F, rows, rule, mid_max, C, c_type, dw->g.N, EPI_PLAIN,
-                            nullptr, s);
+                            nullptr, s, comb);
     return rc;
 }
 

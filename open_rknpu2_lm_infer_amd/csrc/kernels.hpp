@@ -1257,7 +1257,15 @@ struct GemvParams {
     int producers, consumers;
     int spin_limit;
     int fuse_block, fuse_blocks;
+    // MoE combine in the epilogue (FUSE_COMBINE: one token row, routes of its
+    // top <= GEMV_COMB_TOP ranks, slot = assignment): the output column is
+    // sum_rank fma(comb_contrib[rank][col], routes[rank], .) + this GEMV's
+    // value, the moe_combine_kernel arithmetic, stored as f32.
+    const float* comb_contrib;
+    const float* comb_routes;
+    int comb_top, comb_h;
 };
+constexpr int GEMV_COMB_TOP = 8;
 
 // Synchronisation words of a one-launch FFN, kept zero between launches (the
 // launch's last block clears them). Arrivals are spread over SLOTS counters
@@ -1293,7 +1301,7 @@ __device__ __forceinline__ unsigned ffn_slot_count(int n, int s) {
     return (unsigned)(n / FFN_SLOTS + (s < n % FFN_SLOTS ? 1 : 0));
 }
 
-enum { FUSE_NONE = 0, FUSE_PRODUCER = 1, FUSE_CONSUMER = 2 };
+enum { FUSE_NONE = 0, FUSE_PRODUCER = 1, FUSE_CONSUMER = 2, FUSE_COMBINE = 3 };
 
 __device__ __forceinline__ unsigned ld_agent(const unsigned* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1499,6 +1507,7 @@ __device__ __forceinline__ void gemv_block(GemvParams P, const int bid, const in
     static_assert(FUSE == FUSE_NONE || (MR == 1 && GPB == 1 && !PREQ && !GROUPED), "the one-launch FFN runs one row");
     static_assert(FUSE != FUSE_PRODUCER || (EPI == EPI_SWIGLU_MAX && QWN == 1), "producers: the SwiGLU GEMV, quantization wave");
     static_assert(FUSE != FUSE_CONSUMER || (SPLITK && QWN == 0), "consumers: split-K pieces quantized by the whole block");
+    static_assert(FUSE != FUSE_COMBINE || (EPI == EPI_PLAIN && !SPLITK && QWN == 0), "combine: the plain one-row GEMV");
     if constexpr (SPLITK) {
         static_assert(MR == 1 && GPB == 1 && EPI == EPI_PLAIN && !PREQ && !GROUPED && QWN == 0,
                       "split K: one row, plain epilogue, in-block quantization");
@@ -1659,6 +1668,19 @@ __device__ __forceinline__ void gemv_block(GemvParams P, const int bid, const in
                 const bool ok = m < P.M && idx < P.part_count;
                 pv[m][i] = *(ok ? P.part_in + (size_t)m * P.part_count + idx : own_cs);  // masked at use
             }
+        }
+    }
+    // MoE combine: the routes and this thread's column of every routed
+    // contribution (written by an earlier launch), requested with the rows.
+    float comb_r[FUSE == FUSE_COMBINE ? GEMV_COMB_TOP : 1], comb_c[FUSE == FUSE_COMBINE ? GEMV_COMB_TOP : 1];
+    if constexpr (FUSE == FUSE_COMBINE) {
+        const int p = 8 * tile[0] + c8;
+        const int col = p < P.N ? orig_col(p, P.half) : 0;
+#pragma unroll
+        for (int r = 0; r < GEMV_COMB_TOP; ++r) {
+            const int a = r < P.comb_top ? r : 0;
+            comb_r[r] = P.comb_routes[a];
+            comb_c[r] = P.comb_contrib[(size_t)a * P.comb_h + col];
         }
     }
     // (the empty asm statements keep the compiler from sinking these loads
@@ -2059,8 +2081,18 @@ __device__ __forceinline__ void gemv_block(GemvParams P, const int bid, const in
                 }
                 const int p = 8 * tile[gp * TPG] + c8;
                 if (EPI == EPI_PLAIN) {
-                    if (lane < 8 && row_ok && p < P.N)
-                        store_out(P.c, P.c_type, (size_t)m * P.ldc + orig_col(p, P.half), y[0]);
+                    if constexpr (FUSE == FUSE_COMBINE) {
+                        // ranks in order, single-rounding fma, then the add
+                        float sum = 0.0f;
+#pragma unroll
+                        for (int r = 0; r < GEMV_COMB_TOP; ++r)
+                            if (r < P.comb_top && comb_r[r] > 0.0f) sum = __builtin_fmaf(comb_c[r], comb_r[r], sum);
+                        if (lane < 8 && row_ok && p < P.N)
+                            static_cast<float*>(P.c)[(size_t)m * P.ldc + orig_col(p, P.half)] = sum + y[0];
+                    } else {
+                        if (lane < 8 && row_ok && p < P.N)
+                            store_out(P.c, P.c_type, (size_t)m * P.ldc + orig_col(p, P.half), y[0]);
+                    }
                 } else {
                     const float o = hm_swiglu(y[0], y[TPG - 1]);
                     const size_t oi = (size_t)m * P.ldc + ((p >> 6) << 5) + (p & 31);
@@ -2101,6 +2133,16 @@ template <typename T, int MR, int BITS, int EPI, int RW, int NW, bool PREQ, int 
 __global__ __launch_bounds__(NTHR + 64 * QWN) void gemv_kernel(GemvParams P) {
     extern __shared__ __attribute__((aligned(16))) int8_t sa[];
     gemv_block<T, MR, BITS, EPI, RW, NW, PREQ, GPB, NTHR, GROUPED, QWN, SPLITK>(P, blockIdx.x, gridDim.x, sa);
+}
+
+// The plain one-row GEMV whose epilogue also combines a token's routed
+// expert contributions with its value (the MoE shared expert's down
+// projection at one token; GemvParams::comb_*).
+template <int BITS, int RW>
+__global__ __launch_bounds__(256) void gemv_combine_kernel(GemvParams P) {
+    extern __shared__ __attribute__((aligned(16))) int8_t sa[];
+    gemv_block<float, 1, BITS, EPI_PLAIN, RW, 1, false, 1, 256, false, 0, false, FUSE_COMBINE>(P, blockIdx.x, gridDim.x,
+                                                                                             sa);
 }
 
 // The FFN of one row in one launch. Block b first computes gate/up tile pair

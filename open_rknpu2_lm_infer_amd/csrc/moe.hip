@@ -523,7 +523,18 @@ static int enqueue_moe(MoeWork* ws, const MoeBank* b, int rows, const float* inp
     }
 
     const float* shared = nullptr;
-    if (b->shared) {
+    if (b->shared && slot_gemv && rows == 1) {
+        // One token: the shared expert's down GEMV can run the combine in its
+        // epilogue and write `out` itself; when it does not, `out` holds the
+        // shared expert's output and the combine runs in place.
+        bool combined = false;
+        const GemvCombine comb{ws->mws->c_f32, routes, ws->top, ws->h, &combined};
+        rc = enqueue_ffn(ws->sgws, b->shared_gu, ws->sdws, b->shared_dn, input, DT_F32, out, DT_F32, rows, QUANT_MOE,
+                         s, &comb);
+        if (rc != RK_NPU_OK) return rc;
+        if (combined) return hipGetLastError() == hipSuccess ? RK_NPU_OK : RK_NPU_ERR_DEVICE;
+        shared = out;
+    } else if (b->shared) {
         // The shared expert is an ordinary fused FFN with the MoE rounding rule.
         rc = enqueue_ffn(ws->sgws, b->shared_gu, ws->sdws, b->shared_dn, input, DT_F32, ws->sdws->c_f32, DT_F32,
                          rows, QUANT_MOE, s);

@@ -128,11 +128,23 @@ int enqueue_quant(Workspace* ws, const void* x, int x_type, long lda, int rows, 
 // A full dynamic-int8 linear from activations x: the GEMV quantizes inside
 // its blocks; the GEMM path quantizes with a separate kernel first. With a
 // SwiGLU+max epilogue, *out_max tells where the middle's row maxima are.
+// A MoE combine that a one-row plain GEMV can run in its epilogue: the output
+// becomes sum_rank fma(contrib[rank][col], routes[rank], .) + the GEMV's
+// value (moe_combine_kernel's arithmetic, slot = assignment), in f32.
+// *combined tells whether the launch did it (else the caller combines).
+struct GemvCombine {
+    const float* contrib;
+    const float* routes;
+    int top, h;
+    bool* combined;
+};
 int enqueue_linear(Workspace* ws, const Weights* w, const void* x, int x_type, long lda, int rows, int rule,
-                   RowMax in_max, void* c, int c_type, long ldc, int epi, RowMax* out_max, hipStream_t s);
-// gate_up (SwiGLU + row max) -> requant of the middle (same rule) -> down.
+                   RowMax in_max, void* c, int c_type, long ldc, int epi, RowMax* out_max, hipStream_t s,
+                   const GemvCombine* comb = nullptr);
+// gate_up (SwiGLU + row max) -> requant of the middle (same rule) -> down
+// (with comb: the down launch may also run the MoE combine).
 int enqueue_ffn(Workspace* gws, const Weights* gw, Workspace* dws, const Weights* dw, const void* A, int a_type,
-                void* C, int c_type, int rows, int rule, hipStream_t s);
+                void* C, int c_type, int rows, int rule, hipStream_t s, const GemvCombine* comb = nullptr);
 
 // RK_NPU_ERR_DEVICE (and cleared) when a one-launch FFN on this down
 // workspace gave up waiting for its gate_up blocks since the last check.

@@ -134,17 +134,29 @@ def test_moe_matches_oracle(dn_bits, rows):
     assert np.array_equal(again, out)
 
 
-def test_moe_with_shared_w8_expert():
-    h, inter, experts, top, rows = 128, 64, 8, 2, 5
+@pytest.mark.parametrize("rows,top,qw,fuse", [(5, 2, -1, 1), (1, 2, -1, 1), (1, 8, -1, 1), (1, 8, 1, 1),
+                                               (1, 8, -1, 0)])
+def test_moe_with_shared_w8_expert(rows, top, qw, fuse):
+    """Routed experts plus a shared W8 expert, equal to the oracle. At one
+    token the shared expert's down GEMV also runs the combine in its
+    epilogue; with a quantization wave forced on (HM_GEMV_QW=1) it cannot,
+    nor with HM_GEMV_COMBINE=0, and the combine runs afterwards in place on
+    the output. A repeated expert and a skipped (zero) route at one token."""
+    from open_rknpu2_lm_infer_amd import device as D
+    h, inter, experts = 128, 64, 8
     backend = npu.Backend(npu.ModelOptions(chunk=16))
     gate, down = moe_bank(h, inter, experts, 4, "moesh")
     sg = npu.QuantMatrix(8, h, 2 * inter, *R.weights(4, "sh-gu", 8, h, 2 * inter))
     sd = npu.QuantMatrix(8, inter, h, *R.weights(4, "sh-dn", 8, inter, h))
     moe = backend.load_moe_with_shared(gate, down, top, (sg, sd))
-    x = R.activations(4, "moesh-x", rows, h)
-    ids, w = routed(rows, experts, top, "moesh-r")
+    x = R.activations(4, f"moesh-x{rows}", rows, h)
+    ids, w = routed(rows, experts, top, f"moesh-r{rows}-{top}")
+    if rows == 1:
+        ids[0, 1] = ids[0, 0]  # a repeated expert
+        w[0, top - 1] = 0.0    # a skipped route
     out = np.zeros((rows, h), np.float32)
-    moe.run(x, ids, w, out, rows)
+    with D.plan_switch("HM_GEMV_QW", qw), D.plan_switch("HM_GEMV_COMBINE", fuse):
+        moe.run(x, ids, w, out, rows)
     ref = oracle.moe([(g.codes, g.scales) for g in gate], [(d.codes, d.scales) for d in down], x, ids, w,
                      shared=((sg.codes, sg.scales), (sd.codes, sd.scales)))
     assert np.array_equal(out, ref)
