@@ -960,7 +960,66 @@ def run_probes(torch, ctx, reps=20):
         "layer 0 x 36 (weights cache-resident)": {"ms": round(ms_warm, 4), "gbs": round(nbytes / ms_warm / 1e6, 1)}}
     log(f"[probe] decode step, cache-warm bound: {res['decode_step_cache_warm']}")
     del t
+    res["moe_t1_shared_in_bank"] = moe_shared_bank_t1(torch, ctx, reps * 10)
+    log(f"[probe] MoE T=1 with the shared expert in the bank: {res['moe_t1_shared_in_bank']}")
     return res
+
+
+def moe_shared_bank_t1(torch, ctx, steps):
+    """One token through a MoE bank that holds the shared expert (h2048, 128
+    experts, top-8, I768, W4 gate_up + W8 down, shared W8 expert of the same
+    I): the shared down GEMV running the combine in its epilogue against the
+    combine as its own launch (HM_GEMV_COMBINE=0); outputs compared bit for
+    bit. Faster of eager and graph replay, HIP events."""
+    import ctypes
+
+    import numpy as np
+
+    from open_rknpu2_lm_infer_amd import _ffi as F_
+    from open_rknpu2_lm_infer_amd import device as D
+    from open_rknpu2_lm_infer_amd import npu
+    from oracle import oracle
+    h, inter, experts, top = 2048, 768, 128, 8
+    g = np.random.default_rng(0x5EED0004 + 1)
+    L = F_.lib()
+    keep, arr = [], (F_.rk_npu_moe_w8_expert * (experts + 1))()
+    for e in range(experts + 1):
+        lo = -8 if e < experts else -127  # routed gate_up W4, the shared expert W8
+        gc = g.integers(lo, -lo, (h, 2 * inter), dtype=np.int8)
+        gs = g.uniform(0.001, 0.01, 2 * inter).astype(np.float32)
+        dc = g.integers(-127, 128, (inter, h), dtype=np.int8)
+        ds = g.uniform(0.001, 0.01, h).astype(np.float32)
+        keep.append((gc, gs, dc, ds))
+        arr[e] = F_.rk_npu_moe_w8_expert(gc.ctypes.data_as(F_.i8p), gs.ctypes.data_as(F_.f32p),
+                                         dc.ctypes.data_as(F_.i8p), ds.ctypes.data_as(F_.f32p))
+    cfg = F_.rk_npu_moe_w8_config()
+    L.rk_npu_moe_w8_config_init(ctypes.byref(cfg), h, inter, experts, 1, top, 1)
+    bank = npu._Handle(L.rk_npu_moe_w4w8_weights_create(ctx.domain, ctypes.byref(cfg.weights), arr),
+                       L.rk_npu_moe_w8_weights_free, "MoE bank", ctx.shared)
+    work = npu._Handle(L.rk_npu_moe_w4w8_workspace_create(ctx.domain, ctypes.byref(cfg)),
+                       L.rk_npu_moe_w8_workspace_free, "MoE workspace", ctx.shared)
+    del arr, keep
+    ids, rw = oracle.routes(g.standard_normal(experts).astype(np.float32), top)
+    x = torch.from_numpy(g.standard_normal((1, h)).astype(np.float32)).cuda()
+    d_ids = torch.from_numpy(ids[None, :].astype(np.int32)).cuda()
+    d_rw = torch.from_numpy(rw[None, :].astype(np.float32)).cuda()
+    y = torch.empty(1, h, dtype=torch.float32, device="cuda")
+
+    def step():
+        npu_check(L.rk_npu_hip_moe_run(work.raw, bank.raw, 1, ctypes.c_void_p(x.data_ptr()),
+                                       ctypes.c_void_p(d_ids.data_ptr()), ctypes.c_void_p(d_rw.data_ptr()),
+                                       ctypes.c_void_p(y.data_ptr()), D.current_stream()), "MoE run")
+    out, outs = {}, []
+    for label, fuse in (("combine in the shared down GEMV", 1), ("combine as its own launch", 0)):
+        with D.plan_switch("HM_GEMV_COMBINE", fuse):
+            ms, ms_eager, ms_graph, ok = best_time(torch, step, steps, 10, lambda: [y.clone()])
+            step()
+            torch.cuda.synchronize()
+            outs.append(y.cpu().numpy().copy())
+        out[label] = {"us": round(ms * 1e3, 2), "eager_us": round(ms_eager * 1e3, 2),
+                      "graph_us": round(ms_graph * 1e3, 2), "graph_matches_eager": ok}
+    out["bit_identical"] = bool(np.array_equal(outs[0], outs[1]))
+    return out
 
 
 # GEMM shapes of the tile sweep: (name, bits, M, K, N, SwiGLU)
