@@ -96,6 +96,27 @@ def test_queries_and_config_init_without_a_device():
         (2048, 768, 128, 8, 512)
 
 
+def test_documented_switches_exist():
+    """Every plan switch rk_npu_hip.h documents is one rk_npu_hip_set_switch
+    knows (set to its current value and restored); unknown names fail."""
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    text = open(os.path.join(root, "include", "rk_npu_hip.h")).read()
+    block = text[text.index("Plan switches for tests and measurements"):text.index("int rk_npu_hip_set_switch")]
+    names = re.findall(r"^ \*   (HM_[A-Z0-9_]+)\s", block, re.M)
+    assert len(names) >= 10
+    L = F.lib()
+    for name in names:
+        prev = ctypes.c_int()
+        assert L.rk_npu_hip_set_switch(name.encode(), 0, ctypes.byref(prev)) == 0, name
+        assert L.rk_npu_hip_set_switch(name.encode(), prev.value, None) == 0, name
+    assert L.rk_npu_hip_set_switch(b"HM_NO_SUCH_SWITCH", 1, None) == F.RK_NPU_ERR_PARAM
+    # and every switch of the library's table is documented
+    src = open(os.path.join(root, "open_rknpu2_lm_infer_amd", "csrc", "hip_matmul.hip")).read()
+    table = src[src.index("static const SwitchDef kSwitches"):]
+    table = table[:table.index("};")]
+    assert set(re.findall(r'"(HM_[A-Z0-9_]+)"', table)) == set(names)
+
+
 def test_plans():
     L = F.lib()
     plan = F.rk_npu_hip_plan()
