@@ -760,7 +760,11 @@ __device__ __forceinline__ void gemm_mainloop(uint8_t* smem, const int8_t* __res
     constexpr int BH = (BITS == 8) ? 2 : 1;
     constexpr int NF = 2 * FM + BH * FN;
     constexpr int T = 2 * FM * FN;           // MFMAs per stage
-    constexpr int G = T >= 4 ? T / 4 : 1;    // issue groups per stage
+    // issue groups per stage: one per 2 MFMAs on the 16-MFMA stages of the
+    // 256x256 tile (o 4096x2560 63.6 -> 60.9 us, down 9728x2560 154.7 ->
+    // 148.6 us at M=4096 against one per 4), one per 4 MFMAs otherwise
+    // (finer groups left the 128x128 tiles unchanged or slower)
+    constexpr int G = T >= 16 ? T / 2 : (T >= 4 ? T / 4 : 1);
     const int a_lane = (half_id * BM + wm * TM + l32) * 16;
     const int b_lane = (half_id * BN + wn * TN + l32) * 16;
 
