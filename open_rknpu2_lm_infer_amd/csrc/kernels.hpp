@@ -1637,11 +1637,24 @@ __device__ __forceinline__ void gemv_block(GemvParams P, const int bid, const in
     // Rounds of activation chunks (and of partial maxima) that hold work for
     // some thread of the block are requested; the others are not issued at
     // all (every vector-memory instruction costs the CU's load path, masked
-    // or not). These branches are uniform and precede the weight stream, so
-    // they cannot make the compiler wait on it. Within an issued round a
+    // or not). These branches are uniform and precede the weight stream; the
+    // row-max reduction below starts from an opaque zero so that the compiler
+    // cannot hoist its first step to their join, where it waited for every
+    // load before the weights were requested. Within an issued round a
     // masked-off lane reads bytes it loads anyway (its first weight chunk or
     // its column scale), never one shared address: thousands of requests to
     // one line would queue on one cache channel.
+    // Blocks that quantize their rows themselves request them at raised issue
+    // priority and drop it for the weight stream, so the rows' loads of the
+    // CU's later blocks are issued ahead of its earlier blocks' pending weight
+    // loads (decode M=1 W4: qkv 2560x6144 4.56 -> 4.34 us, down 9728x2560
+    // 7.31 -> 7.21 us, o 4096x2560 3.75 -> 3.80 us, step 0.815 -> 0.806 ms,
+    // the same box, the two builds alternated).
+    if constexpr (!QW) {
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_setprio(3);
+        __builtin_amdgcn_sched_barrier(0);
+    }
     const uint8_t* own = tb0 + (size_t)min(tid, CPT - 4) * 16;  // 64 readable bytes (CPT >= 16)
     v4u xraw[XMAX][4];
     const T* x = static_cast<const T*>(P.x);
@@ -1704,6 +1717,11 @@ __device__ __forceinline__ void gemv_block(GemvParams P, const int bid, const in
         }
     };
     v4u wa[RW], wb[NW == 2 ? RW : 1];
+    if constexpr (!QW) {
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_setprio(0);
+        __builtin_amdgcn_sched_barrier(0);
+    }
     load_window(0, wa);
     if (NW == 2 && NWIN > 1) load_window(1, wb);
     float cs[TPB];
@@ -1755,9 +1773,14 @@ __device__ __forceinline__ void gemv_block(GemvParams P, const int bid, const in
     } else {
         // 2. Row maxima (from the activations or the precomputed partials),
         // block max through LDS, row scales.
+        // (from a zero the compiler cannot see through: with a literal 0 it
+        // took the first partial's max right after the partials' loads, before
+        // the weight stream, and waited there for every load in flight)
+        float zero;
+        asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
         float mx[MR];
 #pragma unroll
-        for (int m = 0; m < MR; ++m) mx[m] = 0.0f;
+        for (int m = 0; m < MR; ++m) mx[m] = zero;
         if constexpr (FUSE == FUSE_CONSUMER) {
             // every wave waits for the producers and takes the row max from
             // their slot maxima; then its threads load their middle chunks
