@@ -211,12 +211,29 @@ __device__ __forceinline__ void load16(const __half* p, float (&v)[16]) {
         }
     }
 }
+// Loads through a pointer into global memory (HBM or mapped host memory),
+// which every activation, weight, scale and partial pointer here is. Said at
+// the load itself because a pointer the kernel reads from a device table (the
+// MoE expert weights and scales) is otherwise generic: loads through it, and
+// through every address selected between it and another, become flat loads,
+// which count on both the vector-memory and the LDS counters, so a wait for
+// any one result becomes a wait for every load in flight (the grouped decode
+// GEMV waited for its rows before requesting its weights).
+template <typename V>
+__device__ __forceinline__ V gload(const void* p) {
+    return *(const __attribute__((address_space(1))) V*)p;
+}
+template <typename V>
+__device__ __forceinline__ V gload_nt(const void* p) {
+    return __builtin_nontemporal_load((const __attribute__((address_space(1))) V*)p);
+}
+
 // 16 activations as raw 16-byte words (2 for fp16, 4 for f32), so a load can
 // be issued now and converted later without waiting on anything else.
 template <typename T>
 __device__ __forceinline__ void load16_raw(const T* p, v4u (&r)[4]) {
 #pragma unroll
-    for (int q = 0; q < (int)(16 * sizeof(T) / 16); ++q) r[q] = reinterpret_cast<const v4u*>(p)[q];
+    for (int q = 0; q < (int)(16 * sizeof(T) / 16); ++q) r[q] = gload<v4u>(reinterpret_cast<const v4u*>(p) + q);
 }
 __device__ __forceinline__ void cvt16_raw(const v4u (&r)[4], float (&v)[16], float) {
 #pragma unroll
@@ -1543,6 +1560,12 @@ __device__ __forceinline__ void gemv_block(GemvParams P, const int bid, const in
         const int tok = a / P.top, e = P.ids[a];
         P.b = P.b_tab[e];
         P.colscale = P.s_tab[e];
+        // Both table loads have returned before the rows are requested (their
+        // masked-off address needs the weight pointer anyway); a table load
+        // still pending at the join of the rows' uniform branches made the
+        // compiler wait there for every row load before the weight stream.
+        asm volatile("" ::: "memory");
+        wait_vmcnt<0>();
         P.x = static_cast<const T*>(P.x) + (size_t)(P.x_by_token ? tok : s) * P.lda;
         if (P.part_in) P.part_in += (size_t)s * P.part_count;
         P.c = static_cast<uint8_t*>(P.c) + (size_t)s * P.ldc * (P.c_type == DT_F32 ? 4 : 2);
@@ -1666,8 +1689,8 @@ __device__ __forceinline__ void gemv_block(GemvParams P, const int bid, const in
         const int c = tid + NTHR * j, kg = c / MR, m = c % MR;
         if (PREQ) {
             const bool ok = c < chunks && m < P.M;
-            xraw[j][0] = *reinterpret_cast<const v4u*>(ok ? P.diag_codes + ((size_t)kg * P.M_alloc + m) * 16
-                                                          : reinterpret_cast<const int8_t*>(own));
+            xraw[j][0] = gload<v4u>(ok ? P.diag_codes + ((size_t)kg * P.M_alloc + m) * 16
+                                       : reinterpret_cast<const int8_t*>(own));
         } else {
             const bool ok = c < chunks && m < P.M && kg * 16 < P.K;
             load16_raw(ok ? x + (size_t)m * P.lda + kg * 16 : reinterpret_cast<const T*>(own), xraw[j]);
@@ -1683,7 +1706,7 @@ __device__ __forceinline__ void gemv_block(GemvParams P, const int bid, const in
             for (int m = 0; m < MR; ++m) {
                 const int idx = tid + NTHR * i;
                 const bool ok = m < P.M && idx < P.part_count;
-                pv[m][i] = *(ok ? P.part_in + (size_t)m * P.part_count + idx : own_cs);  // masked at use
+                pv[m][i] = gload<float>(ok ? P.part_in + (size_t)m * P.part_count + idx : own_cs);  // masked at use
             }
         }
     }
@@ -1713,7 +1736,7 @@ __device__ __forceinline__ void gemv_block(GemvParams P, const int bid, const in
 #pragma unroll
             for (int u = 1; u < TPB; ++u) base = (t == u) ? tb[u] : base;
             // (streamed once: non-temporal)
-            buf[i] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(base + (size_t)r * 16));
+            buf[i] = gload_nt<v4u>(base + (size_t)r * 16);
         }
     };
     v4u wa[RW], wb[NW == 2 ? RW : 1];
@@ -1726,7 +1749,7 @@ __device__ __forceinline__ void gemv_block(GemvParams P, const int bid, const in
     if (NW == 2 && NWIN > 1) load_window(1, wb);
     float cs[TPB];
 #pragma unroll
-    for (int t = 0; t < TPB; ++t) cs[t] = P.colscale[8 * tile[t] + c8];
+    for (int t = 0; t < TPB; ++t) cs[t] = gload<float>(P.colscale + 8 * tile[t] + c8);
     asm volatile("" ::: "memory");
 
     float scale[MR];
