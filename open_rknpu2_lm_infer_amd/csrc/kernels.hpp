@@ -1667,10 +1667,11 @@ __device__ __forceinline__ void gemv_block(GemvParams P, const int bid, const in
     // masked-off lane reads bytes it loads anyway (its first weight chunk or
     // its column scale), never one shared address: thousands of requests to
     // one line would queue on one cache channel.
-    // Blocks that quantize their rows themselves request them at raised issue
-    // priority and drop it for the weight stream, so the rows' loads of the
-    // CU's later blocks are issued ahead of its earlier blocks' pending weight
-    // loads (decode M=1 W4: qkv 2560x6144 4.56 -> 4.34 us, down 9728x2560
+    // Blocks without a quantization wave request their rows (or the rows'
+    // codes) at raised issue priority and drop it for the weight stream, so
+    // the rows' loads of the CU's later blocks are issued ahead of its
+    // earlier blocks' pending weight loads (decode M=1 W4: qkv 2560x6144
+    // 4.56 -> 4.34 us, down 9728x2560
     // 7.31 -> 7.21 us, o 4096x2560 3.75 -> 3.80 us, step 0.815 -> 0.806 ms,
     // the same box, the two builds alternated).
     if constexpr (!QW) {
