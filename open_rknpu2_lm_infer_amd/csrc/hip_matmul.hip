@@ -631,8 +631,11 @@ template <int BM, int BN, int WGM, int WGN, int BITS, int EPI>
 static void launch_split(const GemmParams& G, int tiles, hipStream_t s) {
     hipLaunchKernelGGL((gemm_kernel<BM, BN, WGM, WGN, BITS, EPI_PLAIN, true, SPLIT_PART>), dim3(tiles * G.splits),
                        dim3(WGM * WGN * 64), 0, s, G);
-    hipLaunchKernelGGL((gemm_kernel<BM, BN, WGM, WGN, BITS, EPI, true, SPLIT_FINISH>), dim3(tiles),
-                       dim3(WGM * WGN * 64), 0, s, G);
+    if constexpr (BM == 128 && BN == 128 && WGM == 2 && WGN == 2)
+        hipLaunchKernelGGL((gemm_split_finish_kernel<BITS, EPI>), dim3(tiles * 4), dim3(64), 0, s, G);
+    else
+        hipLaunchKernelGGL((gemm_kernel<BM, BN, WGM, WGN, BITS, EPI, true, SPLIT_FINISH>), dim3(tiles),
+                           dim3(WGM * WGN * 64), 0, s, G);
 }
 
 template <int BITS, int EPI>

@@ -1202,6 +1202,68 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_kernel(GemmParams P) {
     }
 }
 
+// Finish of a split 128x128 tile (2x2 waves) by four one-wave blocks: block b
+// sums the K pieces' partials of wave b % 4 of tile b / 4 (the part kernel's
+// layout, read as it lies: 1 KB runs per fragment quarter) and runs that
+// wave's 64x64 epilogue, which is the same dequantization and store as the
+// tile's, so the finish spreads over four times the blocks (the 80 tiles of
+// a 512-row 9728x2560 down projection ran on 80 of 256 CUs; FFN M=512 call
+// 79.6 -> 78.8 us).
+template <int BITS, int EPI>
+__global__ __launch_bounds__(64) void gemm_split_finish_kernel(GemmParams P) {
+    using C = TileCfg<128, 128, 2, 2, BITS>;  // the partials' layout
+    using W = TileCfg<64, 64, 1, 1, BITS>;    // one wave's sub-tile
+    static_assert(C::FM == W::FM && C::FN == W::FN, "a wave tile of the split tile is the sub-tile");
+    constexpr int FM = C::FM, FN = C::FN, NT = C::NT;
+    constexpr size_t TILE_INTS = (size_t)128 * 128;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[W::SMEM];
+    const int T = P.tiles_m * P.tiles_n;
+    const int tile = blockIdx.x >> 2, w = blockIdx.x & 3, wm = w / 2, wn = w % 2;
+    const int lane = threadIdx.x;
+    // tile -> (tm, tn) as in gemm_kernel
+    constexpr int G = 8;
+    const int group = tile / (G * P.tiles_n);
+    const int first_m = group * G;
+    const int gm = min(P.tiles_m - first_m, G);
+    const int in_g = tile - group * G * P.tiles_n;
+    const int tm = first_m + in_g % gm, tn = in_g / gm;
+    const int m0 = tm * 128 + wm * 64, n0 = tn * 128 + wn * 64;
+    const int M = P.M;
+    auto row_of = [&](int local, int& out_row, int& src_row) {
+        const int row = m0 + local;
+        out_row = row;
+        src_row = row < M ? row : 0;
+        return row < M;
+    };
+    const auto pre = epilogue_prefetch<64, 64, 1, 1, BITS>(P.rowscale, P.rowsum, P.colscale, n0, row_of);
+    v16i acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+    for (int q = 0; q < P.splits; ++q) {
+        const int* base = P.split_part + ((size_t)q * T + tile) * TILE_INTS;
+        v4i v[FM][FN][4];
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int h = 0; h < 4; ++h)
+                    v[i][j][h] = *reinterpret_cast<const v4i*>(base + ((size_t)((i * FN + j) * 4 + h) * NT + w * 64 + lane) * 4);
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[i][j][r] += v[i][j][r >> 2][r & 3];
+    }
+    gemm_epilogue<64, 64, 1, 1, BITS, EPI, true>(acc, n0, pre, P.N, P.half, P.c, P.ldc, P.c_type, P.rowmax, row_of,
+                                                 smem);
+}
+
 // ---------------------------------------------------------------------------
 // Decode GEMV / skinny GEMM (M <= 8) without MFMA: bandwidth bound, one launch.
 // A block owns one tile group for the whole K: one 8-column weight tile, or
