@@ -167,7 +167,7 @@ def graph_time(torch, fn, reps, check=None):
 # 268,435,456-byte device copy: FETCH_SIZE 131,083.5 KiB (factor 2.0),
 # WRITE_SIZE 262,144 KiB (factor 1.0). Commands and every decode GEMV's
 # figures: profiles/traffic_decode_gemv_m1_m4.txt.
-TRAFFIC_GEMV_GATE_UP = {1: int(round((12427.5 * 2.0 + 81.1 * 1.0) * 1024)),
+TRAFFIC_GEMV_GATE_UP = {1: int(round((12429.5 * 2.0 + 81.1 * 1.0) * 1024)),
                         4: int(round((12466.5 * 2.0 + 304.0 * 1.0) * 1024))}
 
 
