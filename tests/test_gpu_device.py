@@ -142,13 +142,15 @@ def test_unaligned_output_matches_oracle(ctx, bits, dtype):
 
 
 @pytest.mark.parametrize("bits", [4, 8])
-@pytest.mark.parametrize("rows", [300, 512])
-def test_long_k_split_plan_above_256_rows(ctx, bits, rows):
+@pytest.mark.parametrize("rows,n", [(300, 256), (512, 256), (300, 448)])
+def test_long_k_split_plan_above_256_rows(ctx, bits, rows, n):
     """Long K (8192) over more than 256 rows: the plan splits K on the 128x128
-    tile (pieces summed through int32 partials, then the epilogue); plain
-    fp16 and SwiGLU f32 outputs identical to the oracle."""
-    k, n = 8192, 256
-    codes, scales = R.weights(5, f"lks{bits}", bits, k, n)
+    tile (pieces summed through int32 partials, then one one-wave block per
+    64x64 wave tile for the epilogue); plain fp16 and SwiGLU f32 outputs
+    identical to the oracle. 300 rows and 448 columns leave wave tiles
+    partly and wholly past the output in both directions."""
+    k = 8192
+    codes, scales = R.weights(5, f"lks{bits}-{n}", bits, k, n)
     w = ctx.weights(bits, dev(codes), dev(scales))
     x = R.activations(5, f"lks-x{rows}", rows, k)
     y = torch.empty(rows, n, dtype=torch.float16, device="cuda")
