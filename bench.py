@@ -879,8 +879,9 @@ def traffic_probe(torch, ctx, reps=3):
 
 
 def run_probes(torch, ctx, reps=20):
-    """Ceilings measured on this box with the library's roofline probes
-    (rk_npu_hip_mfma_probe, rk_npu_hip_stream_probe), beside the decode
+    """Ceilings measured on this GPU with the roofline probes of the
+    measurement-only library libhip_probes.so (rk_npu_hip_mfma_probe,
+    rk_npu_hip_stream_probe), beside the decode
     projections' own per-launch times in the same setting: 36 launches on 36
     distinct buffers / weight sets captured in a graph, HIP events on the
     replay stream, so every read comes from HBM."""
@@ -888,13 +889,14 @@ def run_probes(torch, ctx, reps=20):
     from open_rknpu2_lm_infer_amd import _ffi as FFI
     from open_rknpu2_lm_infer_amd import device as D
     L = FFI.lib()
+    LP = FFI.probe_lib()
     cur = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     res = {"mfma_int8": [], "hbm_read": [], "decode_kernels": []}
     sink = torch.empty(4096 * 256, dtype=torch.int32, device="cuda")
     for blocks in (256, 512, 1024, 2048):
         iters = 512
         def fn():
-            npu_check(L.rk_npu_hip_mfma_probe(blocks, iters, ctypes.c_void_p(sink.data_ptr()), cur()), "mfma probe")
+            npu_check(LP.rk_npu_hip_mfma_probe(blocks, iters, ctypes.c_void_p(sink.data_ptr()), cur()), "mfma probe")
         ms, _ = graph_time(torch, fn, reps)
         ops = blocks * 4 * iters * 8 * 65536
         res["mfma_int8"].append({"blocks": blocks, "waves_per_simd": blocks // 256, "us": round(ms * 1e3, 2),
@@ -916,7 +918,7 @@ def run_probes(torch, ctx, reps=20):
                                          ("read, 1024x256", 1024, 256, 1), ("read, 2048x256", 2048, 256, 1)):
             def fn():
                 for b in bufs:
-                    npu_check(L.rk_npu_hip_stream_probe(ctypes.c_void_p(b.data_ptr()), b.numel(), blocks, thr, read,
+                    npu_check(LP.rk_npu_hip_stream_probe(ctypes.c_void_p(b.data_ptr()), b.numel(), blocks, thr, read,
                                                         ctypes.c_void_p(sinkb.data_ptr()), cur()), "stream probe")
             ms, _ = graph_time(torch, fn, reps)
             us = ms * 1e3 / LAYERS

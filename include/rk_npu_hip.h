@@ -186,22 +186,6 @@ int rk_npu_hip_profile_begin(int max_launches);
 int rk_npu_hip_profile_end(void);
 int rk_npu_hip_profile_read(rk_npu_hip_kernel_stat* stats, int capacity, int* count);
 
-/* Roofline probes for measurement tools (no reference counterpart; nothing
- * in the library uses them). Both only enqueue on `stream`.
- * rk_npu_hip_stream_probe: one launch of `blocks` x `threads` (a multiple
- * of 64 up to 512) threads that reads `bytes` (rounded down to 16) from the 16-byte aligned
- * device buffer `src` once with 16-byte non-temporal loads, the loads the
- * GEMV issues, or with read = 0 the same launch without loads (its fixed
- * cost); one uint32 per block is stored to `sink` ([blocks]).
- * rk_npu_hip_mfma_probe: `blocks` x 256 threads, each wave issuing `iters`
- * rounds of 8 independent v_mfma_i32_32x32x32_i8 on register operands
- * (65536 int8 ops each, no memory traffic): the dense int8 matrix-core rate
- * of the part at its loaded clock; one int32 per thread is stored to
- * `sink` ([blocks * 256]). */
-int rk_npu_hip_stream_probe(const void* src, uint64_t bytes, int blocks, int threads, int read, uint32_t* sink,
-                            void* stream);
-int rk_npu_hip_mfma_probe(int blocks, int iters, int32_t* sink, void* stream);
-
 /* Launch plan the library uses for a linear of this shape, for diagnostics:
  * kind 0 = GEMV (no MFMA), 1 = MFMA GEMM; tile sizes and K splits. */
 typedef struct rk_npu_hip_plan {

@@ -328,8 +328,6 @@ SIGNATURES = {
     "rk_npu_hip_workspace_codes": (c_int, [c_void_p, c_int, c_int, i8p, f32p, i32p]),
     "rk_npu_hip_inject_alloc_failures": (c_int, [c_int]),
     "rk_npu_hip_ffn_status": (c_int, [c_void_p, c_int]),
-    "rk_npu_hip_stream_probe": (c_int, [c_void_p, c_uint64, c_int, c_int, c_int, c_void_p, c_void_p]),
-    "rk_npu_hip_mfma_probe": (c_int, [c_int, c_int, c_void_p, c_void_p]),
     "rk_npu_hip_set_switch": (c_int, [c_char_p, c_int, POINTER(c_int)]),
     "rk_npu_hip_linear_plan": (c_int, [c_int, c_int, c_int, c_int, P(rk_npu_hip_plan)]),
     "rk_npu_hip_profile_begin": (c_int, [c_int]),
@@ -356,6 +354,14 @@ SIGNATURES = {
                                          c_void_p]),
 }
 
+# Measurement-only library (libhip_probes.so, csrc/probes.hip): the roofline
+# probes bench.py --probes runs. Not part of the product library or its ABI.
+PROBE_LIB_PATH = os.path.join(PKG_DIR, "libhip_probes.so")
+PROBE_SIGNATURES = {
+    "rk_npu_hip_stream_probe": (c_int, [c_void_p, c_uint64, c_int, c_int, c_int, c_void_p, c_void_p]),
+    "rk_npu_hip_mfma_probe": (c_int, [c_int, c_int, c_void_p, c_void_p]),
+}
+
 RECLAIM_CALLBACK = ctypes.CFUNCTYPE(None, c_void_p)
 
 _lib = None
@@ -379,6 +385,25 @@ def lib():
             f.argtypes = args
         _lib = L
     return _lib
+
+
+_probe_lib = None
+
+
+def probe_lib():
+    """Load libhip_probes.so (measurement only); raise if it has not been built."""
+    global _probe_lib
+    if _probe_lib is None:
+        if not os.path.exists(PROBE_LIB_PATH):
+            raise LibraryMissing(
+                f"{PROBE_LIB_PATH} is missing: build it with `python -m open_rknpu2_lm_infer_amd.build`")
+        L = ctypes.CDLL(PROBE_LIB_PATH)
+        for name, (res, args) in PROBE_SIGNATURES.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _probe_lib = L
+    return _probe_lib
 
 
 def strerror(rc: int) -> str:

@@ -9,27 +9,34 @@ PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG_DIR, "csrc")
 LIB_NAME = "libhip_matmul.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
-SOURCES = ["hip_matmul.hip", "moe.hip", "attention.hip", "unsupported_ops.hip", "probes.hip"]
+# The product library's sources: every .hip file of csrc/ but probes.hip
+# (measurement kernels for bench.py --probes), which is built into a library
+# of its own. The largest first, so the parallel compile ends soonest.
+PROBE_SOURCES = ["probes.hip"]
+SOURCES = sorted((f for f in os.listdir(CSRC) if f.endswith(".hip") and f not in PROBE_SOURCES),
+                 key=lambda f: (not f.startswith("launch_"), f))
+PROBE_LIB_PATH = os.path.join(PKG_DIR, "libhip_probes.so")
+FLAGS_FILE = os.path.join(CSRC, "hipcc_flags.txt")
 
-# Bit-exactness of the quantization, dequantization and SwiGLU paths relies on
-# single IEEE operations: no contraction, correctly rounded division, IEEE
-# denormals. Packed FP32 instructions are disabled for the device code.
-HIPCC_FLAGS = [
-    "--offload-arch=gfx950",
-    "-O3",
-    "-std=c++17",
-    "-fPIC",
-    "-ffp-contract=off",
-    "-fhip-fp32-correctly-rounded-divide-sqrt",
-    "-fno-gpu-flush-denormals-to-zero",
-    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-    "-Wall",
-]
 
-# Per-source additions. attention.hip: matrix-core results in VGPRs, so the
-# attention kernel's output accumulators (rescaled on the VALU between
-# products) are not copied to and from accumulation registers every tile.
-EXTRA_FLAGS = {"attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+def read_flags(path: str = FLAGS_FILE):
+    """(common flags, {source: extra flags}) from hipcc_flags.txt, the file
+    CMakeLists.txt reads too."""
+    common, extra = [], {}
+    with open(path) as f:
+        for line in f:
+            line = line.strip()
+            if not line or line.startswith("#"):
+                continue
+            head, _, rest = line.partition(" ")
+            if head.endswith(".hip"):
+                extra.setdefault(head, []).extend(rest.split())
+            else:
+                common.append(line)
+    return common, extra
+
+
+HIPCC_FLAGS, EXTRA_FLAGS = read_flags()
 
 
 def hipcc() -> str:
@@ -39,13 +46,9 @@ def hipcc() -> str:
     return "hipcc"
 
 
-def build(verbose: bool = False, jobs: int = 3) -> str:
-    """Compile every HIP source to an object, then link the shared library."""
-    build_dir = os.path.join(PKG_DIR, "_build")
-    os.makedirs(build_dir, exist_ok=True)
-    objs = []
-    procs = []
-    for src in SOURCES:
+def _compile(sources, build_dir, jobs, verbose):
+    objs, procs = [], []
+    for src in sources:
         obj = os.path.join(build_dir, os.path.splitext(src)[0] + ".o")
         cmd = [hipcc(), *HIPCC_FLAGS, *EXTRA_FLAGS.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj]
         if verbose:
@@ -56,12 +59,26 @@ def build(verbose: bool = False, jobs: int = 3) -> str:
             _wait(procs.pop(0))
     for p in procs:
         _wait(p)
-    tmp = LIB_PATH + ".tmp"
+    return objs
+
+
+def _link(objs, path, verbose):
+    tmp = path + ".tmp"
     cmd = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs]
     if verbose:
         print(" ".join(cmd), flush=True)
     subprocess.run(cmd, check=True)
-    os.replace(tmp, LIB_PATH)
+    os.replace(tmp, path)
+
+
+def build(verbose: bool = False, jobs: int = 8) -> str:
+    """Compile every HIP source to an object, then link the shared library
+    (libhip_matmul.so) and the measurement-probe library (libhip_probes.so)."""
+    build_dir = os.path.join(PKG_DIR, "_build")
+    os.makedirs(build_dir, exist_ok=True)
+    objs = _compile(SOURCES + PROBE_SOURCES, build_dir, jobs, verbose)
+    _link(objs[:len(SOURCES)], LIB_PATH, verbose)
+    _link(objs[len(SOURCES):], PROBE_LIB_PATH, verbose)
     return LIB_PATH
 
 

@@ -22,6 +22,7 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <new>
 
 #include "../../include/rk_npu_attention_f16.h"
@@ -637,6 +638,65 @@ __global__ __launch_bounds__(256) void attn_combine_rows_kernel(AttnParams P) {
 // ---------------------------------------------------------------------------
 // Host side.
 // ---------------------------------------------------------------------------
+// Device-path work (rk_npu_hip_attention_cache_append / _run, enqueued on the
+// caller's streams) that a later host call on the same cache or workspace must
+// wait for: an event recorded after that work on its stream. The host call
+// waits for the event only, not for the whole device. Work from a second
+// stream while the first's is still pending, or work under graph capture
+// (whose replays the host cannot see), makes the next wait a device-wide
+// synchronize instead.
+struct DevFence {
+    std::mutex mu;
+    hipEvent_t ev = nullptr;
+    hipStream_t last = nullptr;
+    bool used = false;   // ev holds the last device-path work
+    bool broad = false;  // wait for the whole device next time
+
+    // Note device-path work just enqueued on stream s.
+    void note(hipStream_t s) {
+        std::lock_guard<std::mutex> lock(mu);
+        hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(s, &st) != hipSuccess || st != hipStreamCaptureStatusNone) {
+            (void)hipGetLastError();
+            broad = true;
+            return;
+        }
+        if (used && s != last) {
+            const hipError_t q = hipEventQuery(ev);
+            (void)hipGetLastError();  // (not-ready is an answer, not an error)
+            if (q != hipSuccess) broad = true;
+        }
+        if (!ev && hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess) {
+            (void)hipGetLastError();
+            ev = nullptr;
+            broad = true;
+            return;
+        }
+        if (hipEventRecord(ev, s) != hipSuccess) {
+            (void)hipGetLastError();
+            broad = true;
+            return;
+        }
+        used = true;
+        last = s;
+    }
+    // Order stream s after the noted work (s == nullptr: the host waits).
+    hipError_t wait(hipStream_t s) {
+        std::lock_guard<std::mutex> lock(mu);
+        if (broad) {
+            const hipError_t e = hipDeviceSynchronize();
+            if (e == hipSuccess) broad = used = false;
+            return e;
+        }
+        if (!used) return hipSuccess;
+        return s ? hipStreamWaitEvent(s, ev, 0) : hipEventSynchronize(ev);
+    }
+    void destroy() {
+        if (ev) (void)hipEventDestroy(ev);
+        ev = nullptr;
+    }
+};
+
 struct AttnCache {
     uint32_t magic;
     Domain* domain;
@@ -646,6 +706,7 @@ struct AttnCache {
     int length, capacity;
     size_t bytes_each;  // of k and of v
     uint64_t generation;  // bumped whenever the K/V storage is replaced or reloaded
+    DevFence fence;       // device-path appends (writes) and runs (reads) of the rows
 };
 
 struct AttnWork {
@@ -658,6 +719,7 @@ struct AttnWork {
     size_t q_bytes, out_bytes, part_bytes;
     hipStream_t stream;
     std::atomic<bool> busy;
+    DevFence fence;  // device-path runs writing this workspace's partials
 };
 
 // The reference's checks (src/npu.rs:714-728) plus this library's limits.
@@ -878,9 +940,10 @@ static int run_host(rk_npu_attention_f16_workspace* workspace, rk_npu_attention_
     int rc = RK_NPU_OK;
     // Device-path appends and runs (rk_npu_hip_attention_cache_append / _run)
     // are enqueued on the caller's streams and may still be writing the
-    // cache's rows or this workspace's partials: wait for them first, as the
-    // host cache calls do.
-    if (hipSetDevice(device_of(w->domain)) != hipSuccess || hipDeviceSynchronize() != hipSuccess ||
+    // cache's rows or this workspace's partials: this call's stream waits for
+    // them first.
+    if (hipSetDevice(device_of(w->domain)) != hipSuccess || c->fence.wait(w->stream) != hipSuccess ||
+        w->fence.wait(w->stream) != hipSuccess ||
         hipMemcpyAsync(w->q, q, n * sizeof(__half), hipMemcpyHostToDevice, w->stream) != hipSuccess ||
         hipStreamSynchronize(w->stream) != hipSuccess)
         rc = RK_NPU_ERR_DEVICE;
@@ -974,6 +1037,8 @@ void rk_npu_attention_f16_workspace_free(rk_npu_attention_f16_workspace* workspa
         (void)hipStreamSynchronize(w->stream);
         (void)hipStreamDestroy(w->stream);
     }
+    (void)w->fence.wait(nullptr);
+    w->fence.destroy();
     domain_free(w->domain, w->q, w->q_bytes);
     domain_free(w->domain, w->out, w->out_bytes);
     domain_free(w->domain, w->part, w->part_bytes);
@@ -1011,7 +1076,8 @@ void rk_npu_attention_f16_cache_free(rk_npu_attention_f16_cache* cache) {
     AttnCache* c = as_cache(cache);
     if (!c) return;
     (void)hipSetDevice(device_of(c->domain));
-    (void)hipDeviceSynchronize();
+    (void)c->fence.wait(nullptr);
+    c->fence.destroy();
     domain_free(c->domain, c->k, c->bytes_each);
     domain_free(c->domain, c->v, c->bytes_each);
     c->magic = 0;
@@ -1021,7 +1087,7 @@ void rk_npu_attention_f16_cache_free(rk_npu_attention_f16_cache* cache) {
 int rk_npu_attention_f16_cache_reserve(rk_npu_ctx* ctx, rk_npu_attention_f16_cache* cache, int32_t capacity) {
     AttnCache* c = as_cache(cache);
     if (!ctx || !c || capacity < 0) return RK_NPU_ERR_PARAM;
-    if (hipSetDevice(device_of(c->domain)) != hipSuccess || hipDeviceSynchronize() != hipSuccess)
+    if (hipSetDevice(device_of(c->domain)) != hipSuccess || c->fence.wait(nullptr) != hipSuccess)
         return RK_NPU_ERR_DEVICE;
     return cache_grow(c, capacity);
 }
@@ -1030,7 +1096,7 @@ int rk_npu_attention_f16_cache_load(rk_npu_ctx* ctx, rk_npu_attention_f16_cache*
                                     const uint16_t* v, int32_t rows) {
     AttnCache* c = as_cache(cache);
     if (!ctx || !c || rows < 0 || (rows > 0 && (!k || !v))) return RK_NPU_ERR_PARAM;
-    if (hipSetDevice(device_of(c->domain)) != hipSuccess || hipDeviceSynchronize() != hipSuccess)
+    if (hipSetDevice(device_of(c->domain)) != hipSuccess || c->fence.wait(nullptr) != hipSuccess)
         return RK_NPU_ERR_DEVICE;
     c->length = 0;
     c->generation += 1;  // the contents are replaced (a reset when rows == 0)
@@ -1045,7 +1111,7 @@ int rk_npu_attention_f16_cache_append(rk_npu_ctx* ctx, rk_npu_attention_f16_cach
     AttnCache* c = as_cache(cache);
     if (!ctx || !c || rows < 1 || !k || !v) return RK_NPU_ERR_PARAM;
     if ((long)c->length + rows > round_up(c->cfg.max_capacity, 32)) return RK_NPU_ERR_PARAM;
-    if (hipSetDevice(device_of(c->domain)) != hipSuccess || hipDeviceSynchronize() != hipSuccess)
+    if (hipSetDevice(device_of(c->domain)) != hipSuccess || c->fence.wait(nullptr) != hipSuccess)
         return RK_NPU_ERR_DEVICE;
     if (c->length + rows > c->capacity) {
         const int grown = std::min(round_up(c->cfg.max_capacity, 32), std::max(c->length + rows, 2 * c->capacity));
@@ -1097,7 +1163,9 @@ int rk_npu_hip_attention_cache_append(rk_npu_attention_f16_cache* cache, const v
     if (!c || rows < 1 || !k_dev || !v_dev) return RK_NPU_ERR_PARAM;
     if ((long)c->length + rows > c->capacity) return RK_NPU_ERR_PARAM;  // (reserve first: no allocation here)
     if (hipSetDevice(device_of(c->domain)) != hipSuccess) return RK_NPU_ERR_DEVICE;
-    return cache_put(c, k_dev, v_dev, rows, hipMemcpyDeviceToDevice, static_cast<hipStream_t>(stream), true);
+    const int rc = cache_put(c, k_dev, v_dev, rows, hipMemcpyDeviceToDevice, static_cast<hipStream_t>(stream), true);
+    if (rc == RK_NPU_OK) c->fence.note(static_cast<hipStream_t>(stream));
+    return rc;
 }
 
 int rk_npu_hip_attention_run(rk_npu_attention_f16_workspace* workspace, rk_npu_attention_f16_cache* cache,
@@ -1111,8 +1179,13 @@ int rk_npu_hip_attention_run(rk_npu_attention_f16_workspace* workspace, rk_npu_a
         w->cfg.softmax_scale != c->cfg.softmax_scale)
         return RK_NPU_ERR_PARAM;
     if (hipSetDevice(device_of(w->domain)) != hipSuccess) return RK_NPU_ERR_DEVICE;
-    return enqueue_attention(w, c, static_cast<const __half*>(q_dev), rows, position, out_dev, out_f16 ? 1 : 0,
-                             static_cast<hipStream_t>(stream));
+    const int rc = enqueue_attention(w, c, static_cast<const __half*>(q_dev), rows, position, out_dev,
+                                     out_f16 ? 1 : 0, static_cast<hipStream_t>(stream));
+    if (rc == RK_NPU_OK) {
+        c->fence.note(static_cast<hipStream_t>(stream));
+        w->fence.note(static_cast<hipStream_t>(stream));
+    }
+    return rc;
 }
 
 }  // extern "C"

@@ -16,6 +16,7 @@
 #include <vector>
 
 #include "kernels.hpp"
+#include "launch.hpp"
 #include "runtime.hpp"
 
 namespace hm {
@@ -297,7 +298,7 @@ void weights_destroy(Weights* w) {
 
 // --- launch plans -------------------------------------------------------------
 
-enum GemmVariant { V256x256 = 0, V256x128 = 1, V128x128 = 2, V64x128 = 3, V32x128 = 4 };
+// (GemmVariant: launch.hpp)
 static const int kBM[] = {256, 256, 128, 64, 32};
 static const int kBN[] = {256, 128, 128, 128, 128};
 
@@ -351,7 +352,7 @@ constexpr int GEMV_MAX_LDS = 60 * 1024;
 // 38 us (3 pieces) and M=64 from 38 to 22 us (6 pieces); with K <= 4096 or
 // as many tiles as CUs the partial traffic costs more than it saves.
 // HM_SPLITS forces a piece count (experiments).
-static int device_cus() {
+int device_cus() {
     static std::atomic<int> cached{0};
     int c = cached.load();
     if (c > 0) return c;
@@ -480,6 +481,7 @@ Workspace* workspace_create(Domain* d, int bits, int M, int K, int N) {
     ws->stream = nullptr;
     ws->host_stage = nullptr;
     ws->host_stage_bytes = 0;
+    ws->fused_pending = false;
     const WsLayout L = ws_layout(ws->g, M);
     ws->bytes = L.total;
     uint8_t* base = static_cast<uint8_t*>(domain_alloc(d, L.total));
@@ -623,182 +625,6 @@ int enqueue_quant(Workspace* ws, const void* x, int x_type, long lda, int rows, 
     return hipGetLastError() == hipSuccess ? RK_NPU_OK : RK_NPU_ERR_DEVICE;
 }
 
-// Outputs without a 16-byte aligned base and row pitch take the 128x128
-// tile with per-lane stores (staged = false); all other launches stage rows
-// through LDS. A split plan (64x128 / 128x128 tiles, staged) is two launches:
-// the K pieces' partials, then the per-tile sum and epilogue.
-template <int BM, int BN, int WGM, int WGN, int BITS, int EPI>
-static void launch_split(const GemmParams& G, int tiles, hipStream_t s) {
-    hipLaunchKernelGGL((gemm_kernel<BM, BN, WGM, WGN, BITS, EPI_PLAIN, true, SPLIT_PART>), dim3(tiles * G.splits),
-                       dim3(WGM * WGN * 64), 0, s, G);
-    if constexpr (BM == 128 && BN == 128 && WGM == 2 && WGN == 2)
-        hipLaunchKernelGGL((gemm_split_finish_kernel<BITS, EPI>), dim3(tiles * 4), dim3(64), 0, s, G);
-    else
-        hipLaunchKernelGGL((gemm_kernel<BM, BN, WGM, WGN, BITS, EPI, true, SPLIT_FINISH>), dim3(tiles),
-                           dim3(WGM * WGN * 64), 0, s, G);
-}
-
-template <int BITS, int EPI>
-static void launch_gemm(int v, bool staged, const GemmParams& G, int tiles, hipStream_t s) {
-    if (!staged) {
-        hipLaunchKernelGGL((gemm_kernel<128, 128, 2, 2, BITS, EPI, false>), dim3(tiles), dim3(256), 0, s, G);
-        return;
-    }
-    if (G.splits > 1) {
-        if (v == V64x128)
-            launch_split<64, 128, 2, 2, BITS, EPI>(G, tiles, s);
-        else
-            launch_split<128, 128, 2, 2, BITS, EPI>(G, tiles, s);
-        return;
-    }
-    switch (v) {
-        case V256x256:
-            hipLaunchKernelGGL((gemm_kernel<256, 256, 2, 4, BITS, EPI, true>), dim3(tiles), dim3(512), 0, s, G);
-            break;
-        case V256x128:
-            hipLaunchKernelGGL((gemm_kernel<256, 128, 2, 2, BITS, EPI, true>), dim3(tiles), dim3(256), 0, s, G);
-            break;
-        case V128x128:
-            hipLaunchKernelGGL((gemm_kernel<128, 128, 2, 2, BITS, EPI, true>), dim3(tiles), dim3(256), 0, s, G);
-            break;
-        case V64x128:
-            hipLaunchKernelGGL((gemm_kernel<64, 128, 2, 2, BITS, EPI, true>), dim3(tiles), dim3(256), 0, s, G);
-            break;
-        default:
-            hipLaunchKernelGGL((gemm_kernel<32, 128, 1, 2, BITS, EPI, true>), dim3(tiles), dim3(128), 0, s, G);
-            break;
-    }
-}
-
-template <typename T, int MR, int BITS, int EPI, bool PREQ, int QWN>
-static void launch_gemv_w(const GemvParams& V, int groups, size_t lds, hipStream_t s) {
-    // Register windows sized to the group (rounds of 256 16-byte chunks), so
-    // no thread loads a chunk past the group's end and no registers hold one:
-    // fewer registers, more resident blocks, no wasted load issue. Groups of
-    // more than 8 rounds (the 9728-long down projection) take 512-thread
-    // blocks: half the serial loads, quantization and dot products per thread
-    // on the few blocks such a matrix has.
-    const int planes = BITS == 8 ? V.K_pad / 16 : V.K_pad / 32;
-    const int chunks = planes * 8 * (EPI == EPI_PLAIN ? 1 : 2);
-    const int rounds = (chunks + 255) / 256;
-    if constexpr (QWN == 1) {  // groups of 5 to 8 rounds (shorter ones, forced by HM_GEMV_QW, take 5)
-        if (rounds <= 5)
-            hipLaunchKernelGGL((gemv_kernel<T, MR, BITS, EPI, 5, 1, PREQ, 1, 256, false, 1>), dim3(groups), dim3(320),
-                               lds, s, V);
-        else if (rounds <= 6)
-            hipLaunchKernelGGL((gemv_kernel<T, MR, BITS, EPI, 6, 1, PREQ, 1, 256, false, 1>), dim3(groups), dim3(320),
-                               lds, s, V);
-        else
-            hipLaunchKernelGGL((gemv_kernel<T, MR, BITS, EPI, 8, 1, PREQ, 1, 256, false, 1>), dim3(groups), dim3(320),
-                               lds, s, V);
-        return;
-    }
-    if (rounds <= 3)
-        hipLaunchKernelGGL((gemv_kernel<T, MR, BITS, EPI, 3, 1, PREQ>), dim3(groups), dim3(256), lds, s, V);
-    else if (rounds <= 4)
-        hipLaunchKernelGGL((gemv_kernel<T, MR, BITS, EPI, 4, 1, PREQ>), dim3(groups), dim3(256), lds, s, V);
-    else if (rounds <= 5)
-        hipLaunchKernelGGL((gemv_kernel<T, MR, BITS, EPI, 5, 1, PREQ>), dim3(groups), dim3(256), lds, s, V);
-    else if (rounds <= 6)
-        hipLaunchKernelGGL((gemv_kernel<T, MR, BITS, EPI, 6, 1, PREQ>), dim3(groups), dim3(256), lds, s, V);
-    else if (rounds <= 8)
-        hipLaunchKernelGGL((gemv_kernel<T, MR, BITS, EPI, 8, 1, PREQ>), dim3(groups), dim3(256), lds, s, V);
-    else if (chunks <= 512 * 5)
-        hipLaunchKernelGGL((gemv_kernel<T, MR, BITS, EPI, 5, 1, PREQ, 1, 512>), dim3(groups), dim3(512), lds, s, V);
-    else if (chunks <= 512 * 6)
-        hipLaunchKernelGGL((gemv_kernel<T, MR, BITS, EPI, 6, 1, PREQ, 1, 512>), dim3(groups), dim3(512), lds, s, V);
-    else if (chunks <= 512 * 10)
-        hipLaunchKernelGGL((gemv_kernel<T, MR, BITS, EPI, 5, 2, PREQ, 1, 512>), dim3(groups), dim3(512), lds, s, V);
-    else
-        hipLaunchKernelGGL((gemv_kernel<T, MR, BITS, EPI, 8, 2, PREQ, 1, 512>), dim3(groups), dim3(512), lds, s, V);
-}
-
-// The one-row plain GEMV with the MoE combine in its epilogue.
-template <int BITS>
-static void launch_gemv_combine(const GemvParams& V, int groups, int rounds, size_t lds, hipStream_t s) {
-    if (rounds <= 3)
-        hipLaunchKernelGGL((gemv_combine_kernel<BITS, 3>), dim3(groups), dim3(256), lds, s, V);
-    else if (rounds <= 4)
-        hipLaunchKernelGGL((gemv_combine_kernel<BITS, 4>), dim3(groups), dim3(256), lds, s, V);
-    else if (rounds <= 5)
-        hipLaunchKernelGGL((gemv_combine_kernel<BITS, 5>), dim3(groups), dim3(256), lds, s, V);
-    else if (rounds <= 6)
-        hipLaunchKernelGGL((gemv_combine_kernel<BITS, 6>), dim3(groups), dim3(256), lds, s, V);
-    else
-        hipLaunchKernelGGL((gemv_combine_kernel<BITS, 8>), dim3(groups), dim3(256), lds, s, V);
-}
-
-// Split-K GEMV (one row, plain epilogue): rounds of the largest piece.
-template <typename T, int BITS>
-static void launch_gemv_split(const GemvParams& V, int grid, int rounds, size_t lds, hipStream_t s) {
-    if (rounds <= 3)
-        hipLaunchKernelGGL((gemv_kernel<T, 1, BITS, EPI_PLAIN, 3, 1, false, 1, 256, false, 0, true>), dim3(grid),
-                           dim3(256), lds, s, V);
-    else if (rounds <= 4)
-        hipLaunchKernelGGL((gemv_kernel<T, 1, BITS, EPI_PLAIN, 4, 1, false, 1, 256, false, 0, true>), dim3(grid),
-                           dim3(256), lds, s, V);
-    else if (rounds <= 5)
-        hipLaunchKernelGGL((gemv_kernel<T, 1, BITS, EPI_PLAIN, 5, 1, false, 1, 256, false, 0, true>), dim3(grid),
-                           dim3(256), lds, s, V);
-    else if (rounds <= 6)
-        hipLaunchKernelGGL((gemv_kernel<T, 1, BITS, EPI_PLAIN, 6, 1, false, 1, 256, false, 0, true>), dim3(grid),
-                           dim3(256), lds, s, V);
-    else
-        hipLaunchKernelGGL((gemv_kernel<T, 1, BITS, EPI_PLAIN, 8, 1, false, 1, 256, false, 0, true>), dim3(grid),
-                           dim3(256), lds, s, V);
-}
-
-// Rows quantized beforehand (preq), by a quantization wave of the block
-// (qwn = 1), or by every thread of the block.
-template <typename T, int MR, int BITS, int EPI>
-static void launch_gemv_mr(const GemvParams& V, int groups, size_t lds, hipStream_t s, bool preq, int qwn) {
-    if constexpr (MR > 4) {
-        (void)preq;  // more than 4 rows are always quantized beforehand (enqueue_linear)
-        (void)qwn;
-        launch_gemv_w<float, MR, BITS, EPI, true, 0>(V, groups, lds, s);
-    } else if constexpr (MR == 4) {
-        (void)qwn;  // 4 rows: beforehand, or by every thread of the block (HM_GEMV_PREQ=0)
-        if (preq)
-            launch_gemv_w<float, MR, BITS, EPI, true, 0>(V, groups, lds, s);
-        else
-            launch_gemv_w<T, MR, BITS, EPI, false, 0>(V, groups, lds, s);
-    } else {
-        if (preq)
-            launch_gemv_w<float, MR, BITS, EPI, true, 0>(V, groups, lds, s);  // activations unused
-        else if (qwn == 1)
-            launch_gemv_w<T, MR, BITS, EPI, false, 1>(V, groups, lds, s);
-        else
-            launch_gemv_w<T, MR, BITS, EPI, false, 0>(V, groups, lds, s);
-    }
-}
-
-template <typename T, int BITS, int EPI>
-static void launch_gemv(int mr, const GemvParams& V, int grid, size_t lds, hipStream_t s, bool preq, int qwn) {
-    switch (mr) {
-        case 1:
-            launch_gemv_mr<T, 1, BITS, EPI>(V, grid, lds, s, preq, qwn);
-            break;
-        case 2:
-            launch_gemv_mr<T, 2, BITS, EPI>(V, grid, lds, s, preq, qwn);
-            break;
-        case 4:
-            launch_gemv_mr<T, 4, BITS, EPI>(V, grid, lds, s, preq, qwn);
-            break;
-        default:
-            launch_gemv_mr<T, 8, BITS, EPI>(V, grid, lds, s, preq, qwn);
-            break;
-    }
-}
-
-template <typename T, int BITS>
-static void launch_gemv_epi(int epi, int mr, const GemvParams& V, int grid, size_t lds, hipStream_t s, bool preq,
-                            int qwn) {
-    if (epi == EPI_PLAIN)
-        launch_gemv<T, BITS, EPI_PLAIN>(mr, V, grid, lds, s, preq, qwn);
-    else
-        launch_gemv<T, BITS, EPI_SWIGLU_MAX>(mr, V, grid, lds, s, preq, qwn);
-}
-
 int enqueue_linear(Workspace* ws, const Weights* w, const void* x, int x_type, long lda, int rows, int rule,
                    RowMax in_max, void* c, int c_type, long ldc, int epi, RowMax* out_max, hipStream_t s,
                    const GemvCombine* comb) {
@@ -869,7 +695,8 @@ int enqueue_linear(Workspace* ws, const Weights* w, const void* x, int x_type, l
         const int units = g.K_pad / 64;
         int ksplit = 1;
         const int forced_splits = switch_value(SW_GEMV_SPLITS);
-        if (!preq && qwn == 0 && pv.mr == 1 && epi == EPI_PLAIN && in_max.p && (w_rounds > 8 || forced_splits > 0)) {
+        if (!preq && qwn == 0 && pv.mr == 1 && epi == EPI_PLAIN && in_max.p && ws->kacc &&
+            (w_rounds > 8 || forced_splits > 0)) {
             ksplit = forced_splits > 0 ? forced_splits : (1280 + grid / 2) / grid;
             ksplit = std::max(1, std::min(std::min(ksplit, 8), units / 8));
         }
@@ -892,35 +719,14 @@ int enqueue_linear(Workspace* ws, const Weights* w, const void* x, int x_type, l
             V.comb_routes = comb->routes;
             V.comb_top = comb->top;
             V.comb_h = comb->h;
-            if (g.bits == 8)
-                launch_gemv_combine<8>(V, grid, w_rounds, lds, s);
-            else
-                launch_gemv_combine<4>(V, grid, w_rounds, lds, s);
+            launch_gemv_combine_any(g.bits, V, grid, w_rounds, lds, s);
             if (comb->combined) *comb->combined = true;
         } else if (ksplit > 1) {
             V.ksplit = ksplit;
             const size_t piece_lds = (size_t)64 * piece_units;
-            if (x_type == DT_F32) {
-                if (g.bits == 8)
-                    launch_gemv_split<float, 8>(V, grid * ksplit, piece_rounds, piece_lds, s);
-                else
-                    launch_gemv_split<float, 4>(V, grid * ksplit, piece_rounds, piece_lds, s);
-            } else {
-                if (g.bits == 8)
-                    launch_gemv_split<__half, 8>(V, grid * ksplit, piece_rounds, piece_lds, s);
-                else
-                    launch_gemv_split<__half, 4>(V, grid * ksplit, piece_rounds, piece_lds, s);
-            }
-        } else if (x_type == DT_F32) {
-            if (g.bits == 8)
-                launch_gemv_epi<float, 8>(epi, pv.mr, V, grid, lds, s, preq, qwn);
-            else
-                launch_gemv_epi<float, 4>(epi, pv.mr, V, grid, lds, s, preq, qwn);
+            launch_gemv_split_any(x_type, g.bits, V, grid * ksplit, piece_rounds, piece_lds, s);
         } else {
-            if (g.bits == 8)
-                launch_gemv_epi<__half, 8>(epi, pv.mr, V, grid, lds, s, preq, qwn);
-            else
-                launch_gemv_epi<__half, 4>(epi, pv.mr, V, grid, lds, s, preq, qwn);
+            launch_gemv_any(x_type, g.bits, epi, pv.mr, V, grid, lds, s, preq, qwn);
         }
         prof_end(slot, s);
         if (out_max) *out_max = RowMax{ws->partmax, grid};
@@ -961,17 +767,7 @@ int enqueue_linear(Workspace* ws, const Weights* w, const void* x, int x_type, l
         char name[64];
         std::snprintf(name, sizeof(name), "gemm<%dx%d,w%d,epi=%d,k/%d>", p.bm, p.bn, g.bits, epi, p.ksplit);
         const int slot = prof_begin(s, 1, g.bits, epi, rows, g.K, g.N, name);
-#define HM_GEMM(B)                                                           \
-    if (epi == EPI_PLAIN)                                                    \
-        launch_gemm<B, EPI_PLAIN>(p.variant, staged, G, p.tiles, s);         \
-    else                                                                     \
-        launch_gemm<B, EPI_SWIGLU_MAX>(p.variant, staged, G, p.tiles, s);
-        if (g.bits == 8) {
-            HM_GEMM(8)
-        } else {
-            HM_GEMM(4)
-        }
-#undef HM_GEMM
+        launch_gemm_any(g.bits, epi, p.variant, staged, G, p.tiles, s);
         prof_end(slot, s);
         if (out_max) *out_max = RowMax{reinterpret_cast<const float*>(ws->rowmax), 1};
     }
@@ -1029,41 +825,6 @@ static bool plan_ffn_fused(const Weights* gw, const Weights* dw, const void* A, 
     return true;
 }
 
-// Blocks of the one-launch FFN kernel `fn` that fit the GPU at once with
-// `lds` bytes of dynamic shared memory (0 if unknown), cached per kernel.
-static long ffn_capacity(const void* fn, size_t lds) {
-    static std::mutex mu;
-    static std::map<std::pair<const void*, size_t>, long> cache;
-    std::lock_guard<std::mutex> lock(mu);
-    auto it = cache.find({fn, lds});
-    if (it != cache.end()) return it->second;
-    int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, FFN_THREADS, lds) != hipSuccess) {
-        (void)hipGetLastError();
-        per_cu = 0;
-    }
-    const long cap = (long)per_cu * device_cus();
-    cache[{fn, lds}] = cap;
-    return cap;
-}
-
-template <typename TX, int RWG, int BD>
-static bool launch_ffn_fused(const GemvParams& Pg, const GemvParams& Pd, int grid, size_t lds, hipStream_t s) {
-    constexpr int RWD = BD == 4 ? 3 : 5;
-    const void* fn = reinterpret_cast<const void*>(&ffn_m1_kernel<TX, 4, RWG, BD, RWD>);
-    if (ffn_capacity(fn, lds) < grid) return false;  // must be resident as a whole
-    hipLaunchKernelGGL((ffn_m1_kernel<TX, 4, RWG, BD, RWD>), dim3(grid), dim3(FFN_THREADS), lds, s, Pg, Pd);
-    return true;
-}
-
-template <typename TX, int BD>
-static bool launch_ffn_fused_rw(int rwg, const GemvParams& Pg, const GemvParams& Pd, int grid, size_t lds,
-                                hipStream_t s) {
-    if (rwg == 6) return launch_ffn_fused<TX, 6, BD>(Pg, Pd, grid, lds, s);
-    if (rwg == 7) return launch_ffn_fused<TX, 7, BD>(Pg, Pd, grid, lds, s);
-    return launch_ffn_fused<TX, 8, BD>(Pg, Pd, grid, lds, s);
-}
-
 static GemvParams gemv_params(Workspace* ws, const Weights* w, const void* x, long lda, int rows, int rule, void* c,
                               int c_type, long ldc) {
     const Geometry& g = w->g;
@@ -1113,21 +874,20 @@ static bool enqueue_ffn_fused(Workspace* gws, const Weights* gw, Workspace* dws,
     std::snprintf(name, sizeof(name), "ffn_m1<w4,w%d,k/%d>", dw->g.bits, fp.ksplit);
     const int slot = prof_begin(s, 0, dw->g.bits, EPI_SWIGLU_MAX, 1, gw->g.K, dw->g.N, name);
     bool launched;
-    if (a_type == DT_F32)
-        launched = dw->g.bits == 4 ? launch_ffn_fused_rw<float, 4>(fp.rwg, Pg, Pd, grid, lds, s)
-                                   : launch_ffn_fused_rw<float, 8>(fp.rwg, Pg, Pd, grid, lds, s);
-    else
-        launched = dw->g.bits == 4 ? launch_ffn_fused_rw<__half, 4>(fp.rwg, Pg, Pd, grid, lds, s)
-                                   : launch_ffn_fused_rw<__half, 8>(fp.rwg, Pg, Pd, grid, lds, s);
+    launched = launch_ffn_fused_any(a_type, dw->g.bits, fp.rwg, Pg, Pd, grid, lds, s);
     prof_end(slot, s);
+    if (launched) dws->fused_pending = true;
     return launched;
 }
 
 // The down workspace's one-launch FFN error word: nonzero when a consumer of
 // an earlier call gave up waiting for its producers (its output is then not
-// valid). Reading clears it. The caller has synchronized the stream.
+// valid). Reading clears it. The caller has synchronized the stream. The word
+// is read only when a one-launch FFN ran since the last read, so the
+// two-launch path (the default) adds no copy to the call.
 int ffn_take_error(Workspace* dws) {
-    if (!dws->sync) return RK_NPU_OK;
+    if (!dws->sync || !dws->fused_pending) return RK_NPU_OK;
+    dws->fused_pending = false;
     unsigned err = 0;
     unsigned* word = dws->sync + (4 * FFN_SLOTS + 2) * FFN_LINE;
     if (hipMemcpy(&err, word, 4, hipMemcpyDeviceToHost) != hipSuccess) return RK_NPU_ERR_DEVICE;
@@ -1175,8 +935,10 @@ static ScratchTable& scratch_table() {
 }
 
 // Once per device, with that device current (rk_npu_open): look up this
-// GPU's copy of the array and zero it (the split-K slots must start at zero;
-// every call leaves them zero again).
+// GPU's copy of the array and zero it once. Nothing in it needs to start at
+// zero for a call: the buffers a call reads (codes, scales, maxima, split
+// partials) are written by that call's own launches first, and the view holds
+// no split-K GEMV slots (see scratch_workspace).
 static int scratch_init(int dev) {
     ScratchTable& t = scratch_table();
     std::lock_guard<std::mutex> lock(t.mu);
@@ -1217,6 +979,7 @@ static bool scratch_workspace(uint8_t* base, const Weights* w, int rows, Workspa
     ws.busy.store(false);
     ws.host_stage = nullptr;
     ws.host_stage_bytes = 0;
+    ws.fused_pending = false;
     ws.a_f32 = nullptr;
     ws.c_f32 = nullptr;
     size_t off = 0;
@@ -1230,7 +993,9 @@ static bool scratch_workspace(uint8_t* base, const Weights* w, int rows, Workspa
     ws.rowsum = reinterpret_cast<int*>(take((size_t)ws.M_alloc * 4));
     ws.rowmax = reinterpret_cast<unsigned*>(take((size_t)ws.M_alloc * 4));
     ws.partmax = reinterpret_cast<float*>(take((size_t)g.N_pad * 4));
-    ws.kacc = reinterpret_cast<unsigned long long*>(take(((size_t)g.N_pad + 8) * 8));
+    // No split-K GEMV slots: that plan needs precomputed row maxima, which
+    // this entry never takes, and the planner requires the slots.
+    ws.kacc = nullptr;
     ws.sync = nullptr;  // (a linear call has no one-launch FFN)
     if (off > STATIC_SCRATCH_BYTES) return false;
     // the rest holds split-K partials; plans whose partials do not fit run unsplit

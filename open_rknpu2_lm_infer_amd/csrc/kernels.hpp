@@ -137,6 +137,13 @@ __device__ __forceinline__ int sum_mod8(int v) {
 }
 
 // max over each aligned group of 8 lanes, in every lane of the group
+// A non-negative row maximum as the bits an unsigned atomic max combines
+// (for non-negative floats the integer order is the float order). A NaN group
+// maximum (all of its values NaN) becomes 0, as fmaxf(0, NaN) does where the
+// partial maxima are combined with fmaxf instead: bits 0x7FC00000 would beat
+// every finite value and +inf.
+__device__ __forceinline__ unsigned max_bits(float m) { return __float_as_uint(fmaxf(m, 0.0f)); }
+
 __device__ __forceinline__ float max8(float v) {
     v = fmaxf(v, dpp_move<DPP_QUAD_XOR1>(v));
     v = fmaxf(v, dpp_move<DPP_QUAD_XOR2>(v));
@@ -1005,7 +1012,7 @@ __device__ __forceinline__ void gemm_epilogue(
 #pragma unroll
                         for (int off = 16; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
                         int out_row, src_row;
-                        if (l32 == 0 && row_of(local, out_row, src_row)) atomicMax(rowmax + out_row, __float_as_uint(mx));
+                        if (l32 == 0 && row_of(local, out_row, src_row)) atomicMax(rowmax + out_row, max_bits(mx));
                     }
                 }
             }
@@ -1085,7 +1092,7 @@ __device__ __forceinline__ void gemm_epilogue(
 #pragma unroll
                         for (int off = 1; off < CPR; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
                     }
-                    if ((lane % CPR) == 0 && row_ok) atomicMax(rowmax + out_row, __float_as_uint(mx));
+                    if ((lane % CPR) == 0 && row_ok) atomicMax(rowmax + out_row, max_bits(mx));
                 }
             }
         }
@@ -1612,12 +1619,15 @@ __device__ __forceinline__ void gemv_block(GemvParams P, const int bid, const in
             if (s >= P.slot_count[0]) return;  // uniform over the block
             a = P.perm[s];
         } else {
-            if (!(P.routes[s] > 0.0f)) return;  // a skipped route: no contribution
+            // Every id is checked, a skipped route's too (as the routing
+            // kernel of larger batches and the host entry do), before a
+            // skipped route returns without a contribution.
             const int e0 = P.ids[s];
             if (e0 < 0 || e0 >= P.experts) {
                 if (threadIdx.x == 0) atomicOr(P.error, 1u);
                 return;
             }
+            if (!(P.routes[s] > 0.0f)) return;
         }
         const int tok = a / P.top, e = P.ids[a];
         P.b = P.b_tab[e];
@@ -2222,7 +2232,7 @@ __device__ __forceinline__ void gemv_block(GemvParams P, const int bid, const in
                         mxo = max8(mxo);
                         if constexpr (FUSE == FUSE_PRODUCER) {
                             if (lane == 0 && row_ok)
-                                __hip_atomic_fetch_max(FfnSync{P.sync}.mx(bid % FFN_SLOTS), __float_as_uint(mxo),
+                                __hip_atomic_fetch_max(FfnSync{P.sync}.mx(bid % FFN_SLOTS), max_bits(mxo),
                                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                         } else {
                             if (lane == 0) P.part_out[(size_t)m * groups + g] = row_ok ? mxo : 0.0f;

@@ -1,7 +1,15 @@
 // Roofline probes (rk_npu_hip_stream_probe, rk_npu_hip_mfma_probe): kernels
-// that measure the two ceilings the hot path is judged against on the box
+// that measure the two ceilings the hot path is judged against on the GPU
 // it runs on, so the floors quoted for each projection come from committed
-// code. They compute nothing the library uses.
+// code. They compute nothing the library uses and are built into a
+// measurement-only library of their own (libhip_probes.so), not into the
+// product library or its ABI headers. Both only enqueue on `stream`.
+//   rk_npu_hip_stream_probe(src, bytes, blocks, threads, read, sink, stream):
+//     one launch of `blocks` x `threads` (a multiple of 64 up to 512)
+//     threads; sink holds one uint32 per block;
+//   rk_npu_hip_mfma_probe(blocks, iters, sink, stream): `blocks` x 256
+//     threads, each wave `iters` rounds of 8 MFMAs (65536 int8 ops each);
+//     sink holds one int32 per thread.
 //   stream: read `bytes` of device memory once with 16-byte non-temporal
 //     loads (the GEMV's load instruction) in one launch of a chosen grid, or
 //     launch the same grid with no loads (the launch's fixed cost);
@@ -11,7 +19,7 @@
 
 #include <cstdint>
 
-#include "../../include/rk_npu_hip.h"
+#include "../../include/rk_npu_quant_matmul.h"  // error codes
 
 namespace hm {
 

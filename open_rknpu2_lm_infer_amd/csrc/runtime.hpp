@@ -87,6 +87,7 @@ struct Workspace {
     size_t split_part_ints; // partial ints available
     unsigned long long* kacc;  // split-K GEMV column slots [N_pad] + row code-sum slot, kept zero between calls
     unsigned* sync;            // one-launch FFN synchronisation words (FfnSync), kept zero between calls
+    bool fused_pending;        // a one-launch FFN ran since its error word was last read (host side)
     // pinned host staging of the host-buffer calls (allocated on first use)
     void* host_stage;
     size_t host_stage_bytes;

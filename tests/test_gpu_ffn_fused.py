@@ -127,3 +127,35 @@ def test_one_launch_ffn_failure_is_reported_once(ctx):
                                        out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), None)
     assert rc == F.RK_NPU_ERR_DEVICE
     assert np.array_equal(hf.run(x), oracle.ffn(hf.gc, hf.gs, hf.dc, hf.ds, x))
+
+
+def test_one_launch_ffn_nan_group_matches_two_launches(ctx):
+    """A group of 8 middle values that are all NaN (gate columns whose scale
+    takes the dequantized product to +-inf, against up columns of zero codes:
+    silu(+-inf) * 0): both paths drop that group's maximum from the row max (the
+    one-launch producers map a NaN group maximum to 0 before their unsigned
+    atomic max, as fmaxf does over the two launches' partial maxima), so the
+    outputs are bit-identical, NaNs included."""
+    h, f = 2560, 384
+    x = R.activations(12, "fzn-x", 1, h)
+    gc, gs = R.weights(12, "fzn-g", 4, h, 2 * f)
+    gc, gs = gc.copy(), gs.copy()
+    # gate columns 0-7: codes of the row's signs (a positive dot product) and
+    # a scale that overflows it to +inf; their up columns: zero codes
+    gc[:, :8] = np.where(x[0] >= 0, 7, -7).astype(np.int8)[:, None]
+    gs[:8] = 3e38
+    gc[:, f:f + 8] = 0
+    dc, ds = R.weights(12, "fzn-d", 8, f, h)
+    mid = oracle.linear_swiglu(gc, gs, x)
+    assert np.isnan(mid[0, :8]).all() and np.isfinite(mid[0, 8:]).all()
+    gu, dn = ctx.weights(4, dev(gc), dev(gs)), ctx.weights(8, dev(dc), dev(ds))
+    y = torch.empty(1, h, dtype=torch.float32, device="cuda")
+    names = profiled_names(lambda: D.ffn(ctx, gu, dn, dev(x), y, 1))
+    assert any(n.startswith("ffn_m1") for n in names), names
+    with D.plan_switch("HM_FFN_FUSED", 0):
+        y2 = torch.empty(1, h, dtype=torch.float32, device="cuda")
+        D.ffn(ctx, gu, dn, dev(x), y2, 1)
+        torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int32), y2.view(torch.int32))
+    # the finite part of the row sets the down projection's scale in both
+    assert np.isfinite(y.cpu().numpy()).any()

@@ -255,13 +255,15 @@ def test_resident_moe_equals_paged_composition_on_gpu():
     assert np.array_equal(out, want)
 
 
-@pytest.mark.parametrize("rows", [1, 3])
+@pytest.mark.parametrize("rows", [1, 3, 20])
 def test_moe_device_entry_aligned_unaligned_and_bad_ids(rows):
-    """rk_npu_hip_moe_run on device buffers (the decode-sized slot path): an
-    aligned input row is quantized inside the routed gate/up blocks, an input
-    off 16-byte alignment is quantized by a launch first; both equal the
-    oracle, with a skipped (zero) route and a repeated expert. An out-of-range
-    expert id is reported by rk_npu_hip_moe_status (once: the report clears)."""
+    """rk_npu_hip_moe_run on device buffers: 1 and 3 rows take the decode-sized
+    slot path (an aligned input row is quantized inside the routed gate/up
+    blocks, an input off 16-byte alignment by a launch first), 20 rows (80
+    assignments) the routed grouped path; all equal the oracle, with a skipped
+    (zero) route and a repeated expert. An out-of-range expert id is reported
+    by rk_npu_hip_moe_status (once: the report clears), on a live route and on
+    a skipped one alike."""
     from open_rknpu2_lm_infer_amd import device as D
     h, inter, experts, top = 256, 96, 6, 4
     gate, down = moe_bank(h, inter, experts, 8, f"moedev{rows}")
@@ -272,7 +274,7 @@ def test_moe_device_entry_aligned_unaligned_and_bad_ids(rows):
         arr[e] = F.rk_npu_moe_w8_expert(gate[e].codes.ctypes.data_as(F.i8p), gate[e].scales.ctypes.data_as(F.f32p),
                                         down[e].codes.ctypes.data_as(F.i8p), down[e].scales.ctypes.data_as(F.f32p))
     cfg = F.rk_npu_moe_w8_config()
-    L.rk_npu_moe_w8_config_init(ctypes.byref(cfg), h, inter, experts, 0, top, 8)
+    L.rk_npu_moe_w8_config_init(ctypes.byref(cfg), h, inter, experts, 0, top, max(8, rows))
     bank = npu._Handle(L.rk_npu_moe_w4w8_weights_create(ctx.domain, ctypes.byref(cfg.weights), arr),
                        L.rk_npu_moe_w8_weights_free, "MoE bank", ctx.shared)
     work = npu._Handle(L.rk_npu_moe_w4w8_workspace_create(ctx.domain, ctypes.byref(cfg)),
@@ -297,12 +299,17 @@ def test_moe_device_entry_aligned_unaligned_and_bad_ids(rows):
         assert rc == 0
         assert L.rk_npu_hip_moe_status(work.raw) == 0
         assert np.array_equal(y.cpu().numpy(), ref), f"input offset {offset} floats"
-    bad = ids.copy()
-    bad[0, 0] = experts  # out of range
-    d_bad = torch.from_numpy(bad).cuda()
-    rc = L.rk_npu_hip_moe_run(work.raw, bank.raw, rows, ctypes.c_void_p(buf.data_ptr()),
-                              ctypes.c_void_p(d_bad.data_ptr()), ctypes.c_void_p(d_w.data_ptr()),
-                              ctypes.c_void_p(y.data_ptr()), stream)
-    assert rc == 0
-    assert L.rk_npu_hip_moe_status(work.raw) == F.RK_NPU_ERR_PARAM
-    assert L.rk_npu_hip_moe_status(work.raw) == 0
+    for live in (True, False):  # the bad id on a live route, then on a skipped one
+        bad = ids.copy()
+        bad[0, 0] = experts  # out of range
+        wb = w.copy()
+        if not live:
+            wb[0, 0] = 0.0
+        d_bad = torch.from_numpy(bad).cuda()
+        d_wb = torch.from_numpy(wb).cuda()
+        rc = L.rk_npu_hip_moe_run(work.raw, bank.raw, rows, ctypes.c_void_p(buf.data_ptr()),
+                                  ctypes.c_void_p(d_bad.data_ptr()), ctypes.c_void_p(d_wb.data_ptr()),
+                                  ctypes.c_void_p(y.data_ptr()), stream)
+        assert rc == 0
+        assert L.rk_npu_hip_moe_status(work.raw) == F.RK_NPU_ERR_PARAM, f"live route {live}"
+        assert L.rk_npu_hip_moe_status(work.raw) == 0
