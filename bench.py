@@ -330,7 +330,8 @@ def decode_passes(torch, ctx, t, reps):
     )
     out = {}
     for name, fn, work in specs:
-        us = per_launch_us(torch, [functools.partial(fn, m) for m in t.w], reps)
+        calls = [functools.partial(fn, m) for m in t.w]
+        us = per_launch_us(torch, calls, reps)
         out[name] = {"us": round(us, 3), "bytes": work, "gbs": round(work / us / 1e3, 1),
                      "frac_hbm": round(work / us / 1e3 / HBM_PEAK_GBS, 4)}
     us_dn = out["ffn call"]["us"] - out["gate_up"]["us"]
@@ -878,6 +879,32 @@ def traffic_probe(torch, ctx, reps=3):
     log("[bench] traffic probe: copy 268435456 B x" + str(reps))
 
 
+def lds_probe(torch, LP, cur, iters=4096):
+    """LDS read bandwidth per CU (rk_npu_hip_lds_probe): one block per CU of
+    4 or 8 waves, each wave streaming conflict-free 16-byte reads; bytes per
+    shader-clock cycle per CU from the in-kernel cycle counts (median over the
+    blocks), and the clock from the cycle and 100 MHz real-time counts."""
+    import ctypes
+    out = []
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    sink = torch.empty(cus * 8, dtype=torch.int32, device="cuda")
+    clocks = torch.empty(cus * 2, dtype=torch.int64, device="cuda")
+    for threads in (256, 512):
+        for _ in range(2):  # the first launch warms the clock
+            npu_check(LP.rk_npu_hip_lds_probe(cus, threads, iters, ctypes.c_void_p(sink.data_ptr()),
+                                              ctypes.c_void_p(clocks.data_ptr()), cur()), "lds probe")
+        torch.cuda.synchronize()
+        c = clocks.view(cus, 2).cpu().tolist()
+        cyc = statistics.median(r[0] for r in c)
+        ticks = statistics.median(r[1] for r in c)
+        nbytes = (threads // 64) * iters * 8 * 1024
+        out.append({"waves_per_cu": threads // 64, "bytes_per_cu": nbytes, "cycles": int(cyc),
+                    "bytes_per_clk_per_cu": round(nbytes / cyc, 1),
+                    "clock_ghz": round(cyc / (ticks * 10.0), 3) if ticks else None})
+        log(f"[probe] lds read {threads // 64} waves/CU: {out[-1]}")
+    return out
+
+
 def run_probes(torch, ctx, reps=20):
     """Ceilings measured on this GPU with the roofline probes of the
     measurement-only library libhip_probes.so (rk_npu_hip_mfma_probe,
@@ -902,6 +929,7 @@ def run_probes(torch, ctx, reps=20):
         res["mfma_int8"].append({"blocks": blocks, "waves_per_simd": blocks // 256, "us": round(ms * 1e3, 2),
                                  "tops": round(ops / (ms * 1e-3) / 1e12, 1)})
         log(f"[probe] mfma blocks={blocks}: {res['mfma_int8'][-1]['tops']} TOPS")
+    res["lds_read"] = lds_probe(torch, LP, cur)
     gen = Gen(torch, 1)
     t = DenseLayers(torch, ctx, gen, 1, (4, 4, 4, 4), tag="dec1")
     # per projection: (name, K, N, GEMV grid, GEMV threads per block)
@@ -1141,6 +1169,468 @@ def summarize_counters(path, top=60):
     return "\n".join(lines)
 
 
+# --- profiles/ --------------------------------------------------------------------
+# `bench.py --profile NAME INPUT...` prints the whole text of one file under
+# profiles/ from the outputs of the commands its header states (run from the
+# repository root on one MI355X, rocprofv3 with TMPDIR=/tmp), so every table
+# there is regenerated by committed code:
+#   roofline  BENCH_JSON ROOF_JSON TRACE_CSV    -> roofline_passes_kernel_trace.txt
+#   traffic   FETCH_CSV WRITE_CSV               -> traffic_decode_gemv_m1_m4.txt
+#   gemm-counters PMC1_CSV PMC2_CSV PROBES_JSON -> counters_gemm_prefill_m4096.txt
+#   probes    PROBES_JSON                       -> probes_hbm_read_floor_mfma_rate.txt
+#   sweep     SWEEP_JSON                        -> gemm_tile_sweep.txt
+#   moe       STATS_CSV MOE_JSON                -> moe_35b_a3b_t512_t1_kernel_stats.txt
+#   attention STATS_CSV ATTN_JSON PMC1_CSV PMC2_CSV -> attention_gqa_decode_prefill_kernel_stats.txt
+
+PROFILE_SETUP = "  cd /tmp && export TMPDIR=/tmp && cd <repo>"
+
+
+def _last_json(path):
+    for line in reversed(open(path).read().strip().splitlines()):
+        if line.strip().startswith("{"):
+            return json.loads(line)
+    raise ValueError(f"{path}: no JSON line")
+
+
+def _kname(name):
+    """A kernel's demangled name without the namespace and parameter list."""
+    name = name[5:] if name.startswith("void ") else name
+    name = name.replace("hm::", "")
+    i = name.rfind("(")
+    return name[:i] if i > 0 else name
+
+
+def _trace(path):
+    """(kernel, grid in work-items, workgroup) -> per-dispatch durations (us)
+    of a rocprofv3 --kernel-trace CSV."""
+    groups = {}
+    with open(path, newline="") as f:
+        for row in csv.DictReader(f):
+            grid = int(row.get("Grid_Size_X") or row.get("Grid_Size") or 0)
+            wg = int(row.get("Workgroup_Size_X") or row.get("Workgroup_Size") or 0)
+            d = (int(row["End_Timestamp"]) - int(row["Start_Timestamp"])) / 1e3
+            groups.setdefault((_kname(row.get("Kernel_Name", "?")), grid, wg), []).append(d)
+    return groups
+
+
+def _pick(groups, must, grid):
+    """The one group whose kernel name holds every string of `must` at this grid."""
+    hits = [k for k in groups if k[1] == grid and all(m in k[0] for m in must)]
+    if len(hits) != 1:
+        raise ValueError(f"{must} grid {grid}: {len(hits)} matches {hits[:4]}")
+    return hits[0]
+
+
+def _counters(path):
+    """Dispatch id -> ({counter: value}, kernel, grid, workgroup, duration us)
+    of a rocprofv3 --pmc CSV."""
+    disp = {}
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            k = r["Dispatch_Id"]
+            if k not in disp:
+                dur = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+                disp[k] = ({}, _kname(r["Kernel_Name"]), int(r["Grid_Size"]), int(r.get("Workgroup_Size") or 0), dur)
+            disp[k][0][r["Counter_Name"]] = float(r["Counter_Value"])
+    return disp
+
+
+def _sec(bench, prefix):
+    return next(x for x in bench["secondary"] if x["workload"].startswith(prefix))
+
+
+# Roofline passes: (label, [(name parts, grid)], work per call, bound,
+# the bench line's avg_us, the --roofline-only output's avg_us). A pass whose
+# library call is several launches adds their durations.
+def _roof_passes(bench, roof):
+    P, R = bench["projections"], roof["decode M=1"]["projections"]
+    dn = "down (ffn call - gate_up)"
+    return [
+        ("decode M=1 qkv 2560x6144 W4", [(["gemv_kernel<__half, 1, 4, 0,"], 196608)], lin_bytes(4, H, Q + 2 * KV, 1),
+         "hbm", P["qkv"]["us"], R["qkv"]["us"]),
+        ("decode M=1 o 4096x2560 W4", [(["gemv_kernel<__half, 1, 4, 0,"], 81920)], lin_bytes(4, Q, H, 1), "hbm",
+         P["o"]["us"], R["o"]["us"]),
+        ("decode M=1 gate_up 2560x19456 W4 +SwiGLU (the bench line's roofline kernel)",
+         [(["gemv_kernel<__half, 1, 4, 2,"], 389120)], lin_bytes(4, H, 2 * F, 1), "hbm", P["gate_up"]["us"],
+         R["gate_up"]["us"]),
+        ("decode M=1 down 9728x2560 W4 (second launch of the FFN call)",
+         [(["gemv_kernel<float, 1, 4, 0,", "true>"], 327680)], lin_bytes(4, F, H, 1), "hbm", P[dn]["us"], R[dn]["us"]),
+        ("decode M=4 gate_up W4 +SwiGLU (quantization launch + GEMV)",
+         [(["quant_rows_kernel<__half, 0,"], 1024), (["gemv_kernel<float, 4, 4, 2,"], 311296)],
+         lin_bytes(4, H, 2 * F, 4), "hbm", _sec(bench, "decode M=4")["roofline"]["avg_us"],
+         roof["decode M=4"]["roofline"]["avg_us"]),
+        ("prefill M=4096 gate_up W4 +SwiGLU (quantization launch + GEMM)",
+         [(["quant_tile_kernel<__half, 0,"], 262144), (["gemm_kernel<128, 128, 2, 2, 4, 2, true"], 1245184)],
+         2.0 * 4096 * H * 2 * F, "mfma", _sec(bench, "prefill")["roofline"]["avg_us"],
+         roof["prefill M=4096"]["roofline"]["avg_us"]),
+        ("FFN M=512 call (quantization, gate_up GEMM, requant, down GEMM pieces, finish)",
+         [(["quant_tile_kernel<__half, 0,"], 32768), (["gemm_kernel<64, 128, 2, 2, 4, 2, true"], 311296),
+          (["quant_tile_kernel<float, 0,"], 32768), (["gemm_kernel<128, 128, 2, 2, 8, 0, true, 1>"], 61440),
+          (["gemm_split_finish_kernel<8, 0>"], 20480)],
+         2.0 * 512 * (H * 2 * F + F * H), "mfma", _sec(bench, "FFN block")["roofline"]["avg_us"],
+         roof["ffn M=512"]["avg_us"]),
+        ("M=128 W8A8 up 2560x9728 call (quantization launch + GEMM)",
+         [(["quant_rows_kernel<__half, 0,"], 32768), (["gemm_kernel<64, 128, 2, 2, 8, 0, true, 0>"], 38912)],
+         lin_bytes(8, H, F, 128), "hbm", _sec(bench, "W8A8 linear")["roofline"]["avg_us"],
+         roof["up M=128"]["avg_us"]),
+    ]
+
+
+def profile_roofline(bench_json, roof_json, trace_csv):
+    bench, roof, groups = _last_json(bench_json), _last_json(roof_json), _trace(trace_csv)
+    out = ["Kernel trace of every roofline pass of bench.py, one MI355X (gfx950), one build.", "",
+           "Commands (repository root):", PROFILE_SETUP,
+           "  python3 bench.py > bench.json",
+           "  rocprofv3 --kernel-trace --stats --output-format csv -d <out> -o roof -- python3 -u bench.py "
+           "--roofline-only > roof.json",
+           "  python3 bench.py --profile roofline bench.json roof.json <out>/<host>/<pid>_roof_kernel_trace.csv", "",
+           "bench.py --roofline-only runs only the roofline passes: per pass, 36 library calls on 36 layers' distinct",
+           "weights captured in one HIP graph and replayed (decode 50 times, prefill and FFN M=512 4 times, M=128",
+           "20 times) after two eager calls; the trace holds those launches.",
+           "  rocprof mean / median: per-dispatch kernel duration (begin to end) under the profiler, summed over the",
+           "    launches of one library call;",
+           "  events: the same launches' graph replay period (HIP events on the replay stream) in the profiled run;",
+           "  bench: the bench line's avg_us (the same measurement without the profiler: what the line reports).",
+           "frac = work per call / time / peak (8 TB/s HBM, or 5.0 POP/s dense int8).", "",
+           f"{'pass':62} {'rocprof':>8} {'median':>8} {'events':>8} {'bench':>8} {'frac(rocprof)':>13} {'frac(bench)':>11}"]
+    fr = {}
+    for label, parts, work, bound, b_us, r_us in _roof_passes(bench, roof):
+        keys = [_pick(groups, m, g) for m, g in parts]
+        mean = sum(statistics.mean(groups[k]) for k in keys)
+        med = sum(statistics.median(groups[k]) for k in keys)
+        peak = 8e12 if bound == "hbm" else 5e15
+        f_r, f_b = work / (mean * 1e-6) / peak, work / (b_us * 1e-6) / peak
+        fr[label] = (mean, b_us, f_r, f_b)
+        out.append(f"{label[:62]:62} {mean:8.3f} {med:8.3f} {r_us:8.3f} {b_us:8.3f} {f_r:13.4f} {f_b:11.4f}")
+        out.append("    " + " + ".join(f"{k[0]} grid {k[1]} x{len(groups[k])}" for k in keys)
+                   + f"; work {work:.6g} {'B' if bound == 'hbm' else 'ops'} per call")
+    gu = next(v for k, v in fr.items() if "roofline kernel" in k)
+    out += ["", "Reading:",
+            f"- The bench line's roofline kernel (decode gate_up GEMV): {gu[1]:.3f} us per launch back to back in a",
+            f"  graph (frac {gu[3]:.4f}), {gu[0]:.3f} us per dispatch under the profiler (frac {gu[2]:.4f}). The profiler",
+            "  serializes dispatches (its graph period is the events column); without it one launch's drain overlaps",
+            "  the next launch's start, which is how the launches run in the step. Both fractions are reported here;",
+            "  the bench line's is the graph period's.",
+            f"- The decode step as a whole: {bench['value']:.2f} GB/s, {bench['value'] / 8000:.4f} of 8 TB/s "
+            f"({bench['ms_per_step']:.4f} ms per step of 36 layers).",
+            "- Algorithmic bytes (hbm): weights at storage width + f32 column scales + fp16 activations in and out;",
+            "  ops (mfma): 2*M*K*N.", "",
+            "Per-kernel launch statistics of the whole trace (top 45 by total time):"]
+    out += summarize_trace(trace_csv, top=45).splitlines()
+    return "\n".join(out)
+
+
+TRAFFIC_SPEC = [
+    ("M=1 qkv 2560x6144", ["gemv_kernel<__half, 1, 4, 0,"], 196608, lin_bytes(4, H, Q + 2 * KV, 1)),
+    ("M=1 o 4096x2560", ["gemv_kernel<__half, 1, 4, 0,"], 81920, lin_bytes(4, Q, H, 1)),
+    ("M=1 gate_up 2560x19456 +SwiGLU", ["gemv_kernel<__half, 1, 4, 2,"], 389120, lin_bytes(4, H, 2 * F, 1)),
+    ("M=1 down 9728x2560 (split K, f32 middle in)", ["gemv_kernel<float, 1, 4, 0,", "true>"], 327680,
+     lin_bytes(4, F, H, 1)),
+    ("M=4 qkv (rows quantized beforehand)", ["gemv_kernel<float, 4, 4, 0,"], 196608, lin_bytes(4, H, Q + 2 * KV, 4)),
+    ("M=4 o", ["gemv_kernel<float, 4, 4, 0,"], 81920, lin_bytes(4, Q, H, 4)),
+    ("M=4 gate_up +SwiGLU", ["gemv_kernel<float, 4, 4, 2,"], 311296, lin_bytes(4, H, 2 * F, 4)),
+    ("M=4 down (512-thread blocks)", ["gemv_kernel<float, 4, 4, 0,"], 163840, lin_bytes(4, F, H, 4)),
+]
+
+
+def _per_kernel(disp, counter):
+    """(kernel, grid) -> median of one counter over its dispatches."""
+    groups = {}
+    for vals, name, grid, _, _ in disp.values():
+        if counter in vals:
+            groups.setdefault((name, grid), []).append(vals[counter])
+    return {k: (statistics.median(v), len(v)) for k, v in groups.items()}
+
+
+def profile_traffic(fetch_csv, write_csv):
+    fe, wr = _per_kernel(_counters(fetch_csv), "FETCH_SIZE"), _per_kernel(_counters(write_csv), "WRITE_SIZE")
+    # the calibration copy: the dispatch writing 262,144 KiB
+    cal = [k for k, (v, _) in wr.items() if abs(v - 262144.0) < 64.0 and "copy" in k[0].lower()]
+    if len(cal) != 1:
+        raise ValueError(f"calibration copy: {cal}")
+    cf, cw = fe[cal[0]][0], wr[cal[0]][0]
+    ff, fw = 262144.0 / cf, 262144.0 / cw
+    out = ["HBM traffic of the decode GEMVs (M=1 and M=4, W4 weights, Qwen3-4B-shaped projections), one MI355X.", "",
+           "Commands (repository root; two counter runs of the same workload, each in its own process):",
+           PROFILE_SETUP,
+           "  rocprofv3 --pmc FETCH_SIZE --output-format csv -d <out_fetch> -o run -- python3 -u bench.py --traffic-probe",
+           "  rocprofv3 --pmc WRITE_SIZE --output-format csv -d <out_write> -o run -- python3 -u bench.py --traffic-probe",
+           "  python3 bench.py --profile traffic <out_fetch>/<host>/<pid>_run_counter_collection.csv "
+           "<out_write>/<host>/<pid>_run_counter_collection.csv", "",
+           "--traffic-probe: a 268,435,456-byte device copy (calibration), then at M=1 and M=4 three passes over 36",
+           "layers' distinct weights of each projection in turn (qkv, o, gate_up + SwiGLU, the FFN call), so every",
+           "dispatch reads its weights from HBM. Values are KiB per dispatch, medians over the dispatches.",
+           f"Calibration ({cal[0][0]}): FETCH_SIZE {cf:.1f} KiB and WRITE_SIZE {cw:.1f} KiB for 262,144 KiB read and",
+           f"written: bytes = FETCH_SIZE x {ff:.3f} x 1024 + WRITE_SIZE x {fw:.3f} x 1024.", "",
+           f"{'kernel (grid in work-items)':48} {'FETCH KiB':>10} {'WRITE KiB':>10} {'traffic B':>12} "
+           f"{'algorithmic B':>14} {'ratio':>6}"]
+    for label, must, grid, alg in TRAFFIC_SPEC:
+        kf = [k for k in fe if k[1] == grid and all(m in k[0] for m in must)]
+        kw = [k for k in wr if k[1] == grid and all(m in k[0] for m in must)]
+        if len(kf) != 1 or len(kw) != 1:
+            raise ValueError(f"{label}: {kf} {kw}")
+        (f, n), (w, _) = fe[kf[0]], wr[kw[0]]
+        t = f * ff * 1024 + w * fw * 1024
+        out.append(f"{label:48} {f:10.1f} {w:10.1f} {t:12.0f} {alg:14d} {t / alg:6.3f}")
+        out.append(f"    {kf[0][0]} grid {grid} ({n} dispatches)")
+    out += ["", "Algorithmic bytes: weights at 4 bits + f32 column scales + fp16 activations in and out (the f32",
+            "middle of the down projection and the row-max partials are not counted). A ratio near 1 means every",
+            "weight byte is read from HBM once and nothing else of size is: the gap to the 8 TB/s roofline is time,",
+            "not bytes. bench.py's primary roofline carries traffic = the M=1 gate_up row (TRAFFIC_GEMV_GATE_UP)."]
+    return "\n".join(out)
+
+
+GEMM_ROLES = [
+    ("qkv 2560x6144 W8 (1536 tiles of 128x128)", "gemm_kernel<128, 128, 2, 2, 8, 0, true, 0>", 393216, None,
+     2.0 * 4096 * H * (Q + 2 * KV)),
+    ("o 4096x2560 W8 (160 tiles of 256x256)", "gemm_kernel<256, 256, 2, 4, 8, 0, true, 0>", 81920, "short",
+     2.0 * 4096 * Q * H),
+    ("gate_up 2560x19456 W4 +SwiGLU (4864 tiles)", "gemm_kernel<128, 128, 2, 2, 4, 2, true, 0>", 1245184, None,
+     2.0 * 4096 * H * 2 * F),
+    ("down 9728x2560 W8 (160 tiles of 256x256)", "gemm_kernel<256, 256, 2, 4, 8, 0, true, 0>", 81920, "long",
+     2.0 * 4096 * F * H),
+    ("lm_head 2560x151936 W8 (9504 tiles)", "gemm_kernel<256, 256, 2, 4, 8, 0, true, 0>", 4866048, None,
+     2.0 * 4096 * H * VOCAB),
+]
+
+# LDS bytes read per MFMA (v_mfma_i32_32x32x32_i8: a 32x32 A fragment and a
+# 32x32 B fragment of one 32-k step) by tile: A 1 KB per row block, B 1 KB
+# (W8) or 0.5 KB (W4, packed) per column block, shared by the wave's MFMAs.
+def _lds_per_mfma(role):
+    fm, fn = (2, 2) if "128x128" in role or "4864" in role or "1536" in role else (4, 2)
+    w4 = "W4" in role
+    return (fm * 1024 + fn * (512 if w4 else 1024)) / (fm * fn)
+
+
+def profile_gemm_counters(pmc1_csv, pmc2_csv, probes_json):
+    r1, r2 = _counters(pmc1_csv), _counters(pmc2_csv)
+    probes = _last_json(probes_json)
+    lds_peak = max(x["bytes_per_clk_per_cu"] for x in probes.get("lds_read", [{"bytes_per_clk_per_cu": 0}]))
+
+    def pick(disp, sub, grid, split):
+        ks = [k for k, v in disp.items() if sub in v[1] and v[2] == grid]
+        if split:
+            durs = sorted(disp[k][4] for k in ks)
+            cut = (durs[0] + durs[-1]) / 2
+            ks = [k for k in ks if (disp[k][4] < cut) == (split == "short")]
+        return ks
+
+    med = lambda disp, ks, c: statistics.median(disp[k][0][c] for k in ks)
+    out = ["Hardware counters of the M=4096 prefill GEMMs (Qwen3-4B-shaped set + lm_head), one MI355X.", "",
+           "Commands (repository root; two counter runs, each in its own process, no tracing options):", PROFILE_SETUP,
+           "  rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CYCLES SQ_WAVE_CYCLES SQ_WAIT_ANY SQ_INSTS_LDS SQ_WAVES "
+           "GRBM_GUI_ACTIVE \\",
+           "      --output-format csv -d <out1> -o run -- python3 -u bench.py --roofline-only prefill",
+           "  rocprofv3 --pmc SQ_LDS_BANK_CONFLICT SQ_LDS_IDX_ACTIVE SQ_INSTS_VALU SQ_INSTS_SALU SQ_INSTS_SMEM "
+           "SQ_WAIT_INST_LDS GRBM_GUI_ACTIVE \\",
+           "      --output-format csv -d <out2> -o run -- python3 -u bench.py --roofline-only prefill",
+           "  python3 bench.py --probes > probes.json",
+           "  python3 bench.py --profile gemm-counters <out1>/<host>/<pid>_run_counter_collection.csv "
+           "<out2>/<host>/<pid>_run_counter_collection.csv probes.json", "",
+           "Per-dispatch medians; counters are summed over the 8 XCDs (GRBM_GUI_ACTIVE / 8 is one XCD's busy cycles).",
+           "  MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8 x 1024 SIMDs);",
+           "  clock = GRBM_GUI_ACTIVE / 8 / the dispatch's duration;",
+           "  LDS util = SQ_LDS_IDX_ACTIVE / (GRBM_GUI_ACTIVE / 8 x 256 CUs) (rocprofv3's LdsUtil), in the run of pass 2;",
+           "  LDS B/MFMA = LDS bytes the wave tile reads per v_mfma_i32_32x32x32_i8 (fragment geometry);",
+           "  WAIT_ANY, WAIT_LDS = SQ_WAIT_ANY, SQ_WAIT_INST_LDS per SQ_WAVE_CYCLES; confl = SQ_LDS_BANK_CONFLICT /",
+           "  SQ_LDS_IDX_ACTIVE; VALU/wave, LDS/wave = instructions per wave.",
+           "The o and down GEMMs share one kernel and grid; their dispatches are told apart by duration.", "",
+           f"{'GEMM (role)':44} {'dur us':>7} {'GHz':>5} {'POP/s':>6} {'MFMA':>5} {'LDS util':>8} {'B/MFMA':>6} "
+           f"{'WAIT_ANY':>8} {'WAIT_LDS':>8} {'confl':>6} {'VALU/wave':>9} {'LDS/wave':>8}"]
+    for label, sub, grid, split, ops in GEMM_ROLES:
+        k1, k2 = pick(r1, sub, grid, split), pick(r2, sub, grid, split)
+        if not k1 or not k2:
+            raise ValueError(f"{label}: no dispatches")
+        dur = statistics.median(r1[k][4] for k in k1)
+        grbm = med(r1, k1, "GRBM_GUI_ACTIVE") / 8
+        grbm2 = med(r2, k2, "GRBM_GUI_ACTIVE") / 8
+        wc = med(r1, k1, "SQ_WAVE_CYCLES")
+        waves = med(r1, k1, "SQ_WAVES")
+        lds_act = med(r2, k2, "SQ_LDS_IDX_ACTIVE")
+        out.append(f"{label:44} {dur:7.1f} {grbm / dur / 1e3:5.2f} {ops / (dur * 1e-6) / 1e15:6.2f} "
+                   f"{med(r1, k1, 'SQ_VALU_MFMA_BUSY_CYCLES') / (grbm * 1024):5.3f} {lds_act / (grbm2 * 256):8.3f} "
+                   f"{_lds_per_mfma(label):6.0f} {med(r1, k1, 'SQ_WAIT_ANY') / wc:8.3f} "
+                   f"{med(r2, k2, 'SQ_WAIT_INST_LDS') / wc:8.3f} {med(r2, k2, 'SQ_LDS_BANK_CONFLICT') / lds_act:6.3f} "
+                   f"{med(r2, k2, 'SQ_INSTS_VALU') / waves:9.0f} {med(r1, k1, 'SQ_INSTS_LDS') / waves:8.0f}")
+        out.append(f"    {sub} grid {grid} wg {r1[k1[0]][3]} ({len(k1)} + {len(k2)} dispatches)")
+    mf = probes.get("mfma_int8", [])
+    if mf:
+        out += ["", "Ceilings on the same build (bench.py --probes): int8 MFMA from registers "
+                + ", ".join(f"{x['tops'] / 1000:.2f} POP/s at {x['waves_per_simd']} waves/SIMD" for x in mf) + ";",
+                "LDS reads (conflict-free 16-byte, one block per CU) "
+                + ", ".join(f"{x['bytes_per_clk_per_cu']} B/clk/CU at {x['waves_per_cu']} waves/CU ({x['clock_ghz']} GHz)"
+                            for x in probes.get("lds_read", [])) + "."]
+    out += ["", "Reading: LDS utilisation stays at about a fifth of the cycles and the measured LDS read rate",
+            f"({lds_peak} B/clk/CU) is several times what the tiles ask for; bank conflicts are a few percent. The",
+            "matrix cores idle on the rest: the per-stage barrier and the waits for each stage's loads."]
+    return "\n".join(out)
+
+
+def profile_probes(probes_json):
+    d = _last_json(probes_json)
+    out = ["Ceilings measured on one MI355X with the measurement library's probes (libhip_probes.so,",
+           "csrc/probes.hip), beside the decode projections' own launches.", "",
+           "Command (repository root):", PROFILE_SETUP, "  python3 bench.py --probes > probes.json",
+           "  python3 bench.py --profile probes probes.json", "",
+           "rk_npu_hip_mfma_probe: back-to-back independent v_mfma_i32_32x32x32_i8 from registers, no memory",
+           "traffic (8 accumulators per wave), graph of one launch replayed 20 times:",
+           " blocks waves/SIMD       us     TOPS"]
+    for r in d["mfma_int8"]:
+        out.append(f"{r['blocks']:7d} {r['waves_per_simd']:10d} {r['us']:8.2f} {r['tops']:8.1f}")
+    tops = [r["tops"] for r in d["mfma_int8"]]
+    out += ["", f"The int8 rate the chip holds is {min(tops) / 1000:.1f}-{max(tops) / 1000:.1f} POP/s "
+            f"({min(tops) / 50:.0f}-{max(tops) / 50:.0f}% of the 5.0 POP/s dense figure): the clock drops",
+            "under sustained matrix-core load.", "",
+            "rk_npu_hip_lds_probe: one block per CU, every wave streaming conflict-free 16-byte LDS reads (8 in",
+            "flight); cycles and clock from the kernel's own s_memtime / s_memrealtime:"]
+    for r in d.get("lds_read", []):
+        out.append(f"    {r['waves_per_cu']} waves/CU: {r['bytes_per_clk_per_cu']} B/clk/CU at {r['clock_ghz']} GHz")
+    out += ["", "rk_npu_hip_stream_probe: one launch reading each projection's weight bytes (36 distinct buffers in",
+            "a graph, so every read comes from HBM) with the GEMV's 16-byte non-temporal loads, at several grids;",
+            "'empty' is the same grid with no loads (the launch's fixed cost); the projection's own GEMV launch",
+            "is timed in the same way:"]
+    best = {}
+    for p in d["hbm_read"]:
+        g = p["gemv_grid"]
+        out.append(f"{p['projection']} ({p['bytes']} B, GEMV grid {g[0]} x {g[1]} threads):")
+        reads = []
+        for k, v in p.items():
+            if isinstance(v, dict) and "us" in v:
+                out.append(f"    {k:42} {v['us']:8.3f} us" + (f" {v['gbs']:9.1f} GB/s" if v.get("gbs") else ""))
+                if k.startswith("read"):
+                    reads.append(v["us"])
+        best[p["projection"]] = min(reads)
+    c = d["decode_step_cache_warm"]
+    a, b = c["36 distinct layers (the bench step)"], c["layer 0 x 36 (weights cache-resident)"]
+    m = d["moe_t1_shared_in_bank"]
+    f1, f0 = m["combine in the shared down GEMV"], m["combine as its own launch"]
+    s = sum(best[k] for k in ("qkv", "o", "gate_up", "down"))
+    out += ["", "Decode step (36 distinct layers) against the same step on layer 0's weights replayed 36 times",
+            f"(50 MB, resident in the last-level cache): {a['ms']:.4f} ms ({a['gbs']:.1f} GB/s) against {b['ms']:.4f} ms",
+            f"({b['gbs']:.1f} GB/s): reading the weights from HBM costs {100 * (a['ms'] - b['ms']) / a['ms']:.0f}% "
+            "of the step; the rest is per-launch cost.", "",
+            "MoE T=1 with the shared expert in the bank (h2048, 128 experts, top-8, I768, W4 gate_up + W8 down,",
+            "shared W8 expert of the same I), faster of eager and graph replay per call:",
+            f"    combine in the shared down GEMV (default)     {f1['us']:7.2f} us   (eager {f1['eager_us']:.2f}, "
+            f"graph {f1['graph_us']:.2f})",
+            f"    combine as its own launch (HM_GEMV_COMBINE=0) {f0['us']:7.2f} us   (eager {f0['eager_us']:.2f}, "
+            f"graph {f0['graph_us']:.2f})",
+            f"    outputs bit-identical: {m['bit_identical']}", "",
+            f"Reading: one pass over a decode projection's weights takes at least {min(best.values()):.1f}-"
+            f"{max(best.values()):.1f} us per launch in a graph. The per-layer sum of the best read floors,",
+            f"{best['qkv']:.2f} + {best['o']:.2f} + {best['gate_up']:.2f} + {best['down']:.2f} = {s:.1f} us, bounds "
+            f"a step of one launch per projection at 36 x {s:.1f} = {36 * s:.0f} us;",
+            f"the decode step runs at {a['ms'] * 1000 / 36:.1f} us per layer ({a['ms']:.4f} ms)."]
+    return "\n".join(out)
+
+
+def profile_sweep(sweep_json):
+    d = _last_json(sweep_json)
+    out = ["Every GEMM tile and split-K setting on the bench's GEMM shapes, one MI355X.", "",
+           "Command (repository root):", PROFILE_SETUP, "  python3 bench.py --tile-sweep > sweep.json",
+           "  python3 bench.py --profile sweep sweep.json", "",
+           "Per shape: one library call per distinct weight copy (copies exceeding the last-level cache), the",
+           "quantization launch included, in a graph; us per call. 'plan' is the library's own choice; a tile",
+           "name with /N forces N split-K pieces.", ""]
+    for name, r in d.items():
+        us = r["us"]
+        out.append(f"{name} ({r['copies']} weight copies): best {r['best']} {us[r['best']]} us = {r['tops_best']} TOPS")
+        items = [f"{k} {us[k]}" for k in ["plan"] + [k for k in us if k != "plan"]]
+        first = [i for i in items if "/" not in i.split()[0]]
+        rest = [i for i in items if "/" in i.split()[0]]
+        out.append("    " + ", ".join(first))
+        for j in range(0, len(rest), 6):
+            out.append("    " + ", ".join(rest[j:j + 6]))
+    plan_gap = [(n, r["us"]["plan"] / r["us"][r["best"]] - 1) for n, r in d.items()]
+    worst = max(plan_gap, key=lambda x: x[1])
+    out += ["", f"Reading: the plan is within {100 * worst[1]:.1f}% of the best setting on every shape (worst: {worst[0]})."]
+    return "\n".join(out)
+
+
+def _stats_table(stats_csv, min_pct=0.1):
+    rows = list(csv.DictReader(open(stats_csv)))
+    tot = sum(float(r["TotalDurationNs"]) for r in rows)
+    lines = [f"{'kernel':84} {'calls':>6} {'avg_us':>8} {'min_us':>8} {'max_us':>8} {'pct':>5}"]
+    for r in sorted(rows, key=lambda r: -float(r["TotalDurationNs"])):
+        pct = 100 * float(r["TotalDurationNs"]) / tot
+        if pct < min_pct:
+            continue
+        lines.append(f"{_kname(r['Name'])[:84]:84} {int(r['Calls']):6d} {float(r['AverageNs']) / 1e3:8.2f} "
+                     f"{float(r['MinNs']) / 1e3:8.2f} {float(r['MaxNs']) / 1e3:8.2f} {pct:5.1f}")
+    lines.append(f"(kernels below {min_pct}% of the total omitted)")
+    return lines
+
+
+def profile_moe(stats_csv, moe_json):
+    res = _last_json(moe_json)
+    res = res if isinstance(res, list) else res.get("lines", res)
+    out = ["MoE 35B-A3B-class expert FFN (h 2048, 128 experts, top-8, I 768, W4 gate_up + W8 down; shared W8",
+           "FFN I 2048): kernel statistics, one MI355X.", "",
+           "Commands (repository root):", PROFILE_SETUP,
+           "  rocprofv3 --kernel-trace --stats --output-format csv -d <out> -o run -- python3 -u bench.py --only moe "
+           "> moe.json",
+           "  python3 bench.py --profile moe <out>/<host>/<pid>_run_kernel_stats.csv moe.json", "",
+           "Workload: rk_npu_hip_moe_run at T=512 and T=1 tokens, steps of both sizes mixed in the table (eager and",
+           "graph replays). T=512: token quantization, device routing (counting sort of the (token, rank) slots),",
+           "gather into slot order, grouped gate_up GEMM + SwiGLU + row max over the ragged expert groups, middle",
+           "requantization, grouped down GEMM, combine; the shared expert as a dense FFN. T=1: slot GEMVs (slot =",
+           "assignment, no routing launch) for gate_up and down, the shared expert's GEMVs, combine.", ""]
+    out += _stats_table(stats_csv)
+    out += ["", "bench.py --only moe in the same profiled run:"]
+    for r in (res if isinstance(res, list) else [res]):
+        out.append(f"    {r['workload']}: {r['value']} {r['unit']} ({r['ms_per_step'] * 1000:.1f} us per step)")
+    return "\n".join(out)
+
+
+def profile_attention(stats_csv, attn_json, pmc1_csv, pmc2_csv):
+    res = _last_json(attn_json)
+    res = res if isinstance(res, list) else [res]
+    out = ["FP16 GQA attention (32 query heads over 8 KV heads, head_dim 128), 36 per-layer KV caches of 4096",
+           "rows: kernel statistics and counters, one MI355X.", "",
+           "Commands (repository root):", PROFILE_SETUP,
+           "  rocprofv3 --kernel-trace --stats --output-format csv -d <out> -o run -- python3 -u bench.py "
+           "--only attention > attn.json",
+           "  rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_WAVE_CYCLES SQ_WAIT_ANY GRBM_GUI_ACTIVE --output-format csv \\",
+           "      -d <pmc1> -o run -- python3 -u bench.py --only attention",
+           "  rocprofv3 --pmc SQ_LDS_BANK_CONFLICT SQ_LDS_IDX_ACTIVE SQ_INSTS_LDS SQ_WAVES GRBM_GUI_ACTIVE "
+           "--output-format csv \\",
+           "      -d <pmc2> -o run -- python3 -u bench.py --only attention",
+           "  python3 bench.py --profile attention <out>/<host>/<pid>_run_kernel_stats.csv attn.json \\",
+           "      <pmc1>/<host>/<pid>_run_counter_collection.csv <pmc2>/<host>/<pid>_run_counter_collection.csv", "",
+           "Workload (bench.py run_attention): one rk_npu_hip_attention_run per layer cache; decode = 1 query row at",
+           "the last position (attn_split_kernel + attn_combine_kernel), prefill = 128 query rows ending at the last",
+           "position, causal (attn_mfma_kernel + attn_combine_rows_kernel); eager steps and graph replays both in",
+           "the table.", ""]
+    out += _stats_table(stats_csv)
+    r1, r2 = _counters(pmc1_csv), _counters(pmc2_csv)
+    out += ["", "Counters (per-dispatch medians; MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8 x 1024);",
+            "LDS util = SQ_LDS_IDX_ACTIVE / (GRBM_GUI_ACTIVE / 8 x 256); confl = SQ_LDS_BANK_CONFLICT / "
+            "SQ_LDS_IDX_ACTIVE):",
+            f"{'kernel':40} {'dur us':>7} {'MFMA':>6} {'WAIT_ANY':>8} {'LDS util':>8} {'confl':>6} {'LDS/wave':>8}"]
+    names = sorted({v[1] for v in r1.values() if v[1].startswith("attn_")})
+    for name in names:
+        k1 = [k for k, v in r1.items() if v[1] == name]
+        k2 = [k for k, v in r2.items() if v[1] == name]
+        md = lambda disp, ks, c: statistics.median(disp[k][0][c] for k in ks)
+        g1, g2 = md(r1, k1, "GRBM_GUI_ACTIVE") / 8, md(r2, k2, "GRBM_GUI_ACTIVE") / 8
+        la = md(r2, k2, "SQ_LDS_IDX_ACTIVE")
+        out.append(f"{name:40} {statistics.median(r1[k][4] for k in k1):7.2f} "
+                   f"{md(r1, k1, 'SQ_VALU_MFMA_BUSY_CYCLES') / (g1 * 1024):6.3f} "
+                   f"{md(r1, k1, 'SQ_WAIT_ANY') / md(r1, k1, 'SQ_WAVE_CYCLES'):8.3f} {la / (g2 * 256):8.3f} "
+                   f"{(md(r2, k2, 'SQ_LDS_BANK_CONFLICT') / la) if la else 0:6.3f} "
+                   f"{md(r2, k2, 'SQ_INSTS_LDS') / md(r2, k2, 'SQ_WAVES'):8.0f}")
+    out += ["", "bench.py --only attention in the same profiled run:"]
+    for r in res:
+        extra = f" ({r['us_per_layer']} us per layer)" if "us_per_layer" in r else ""
+        out.append(f"    {r['workload']}: {r['value']} {r['unit']}{extra}")
+    return "\n".join(out)
+
+
+PROFILES = {"roofline": (profile_roofline, 3), "traffic": (profile_traffic, 2),
+            "gemm-counters": (profile_gemm_counters, 3), "probes": (profile_probes, 1), "sweep": (profile_sweep, 1),
+            "moe": (profile_moe, 2), "attention": (profile_attention, 4)}
+
+
 def npu_check(rc, what):
     if rc != 0:
         raise RuntimeError(f"{what}: rc {rc}")
@@ -1171,7 +1661,16 @@ def main():
                     help="no GPU: per-kernel launch statistics of a rocprofv3 kernel-trace CSV")
     ap.add_argument("--summarize-counters", metavar="CSV",
                     help="no GPU: per-kernel counter medians of a rocprofv3 --pmc CSV")
+    ap.add_argument("--profile", nargs="+", metavar=("NAME", "INPUT"),
+                    help="no GPU: print one file of profiles/ from its commands' outputs (" +
+                         ", ".join(PROFILES) + ")")
     args = ap.parse_args()
+    if args.profile:
+        fn, n = PROFILES[args.profile[0]]
+        if len(args.profile) != n + 1:
+            ap.error(f"--profile {args.profile[0]} takes {n} inputs")
+        print(fn(*args.profile[1:]))
+        return
     if args.summarize_trace:
         print(summarize_trace(args.summarize_trace))
         return
@@ -1233,6 +1732,9 @@ def main():
             s["roofline"].pop("work_per_launch", None)
     roof = dict(primary["roofline"])
     roof.pop("work_per_launch", None)
+    # the whole step's fraction of HBM beside the dominant kernel's
+    roof["step_achieved"] = round(primary["value"], 2)
+    roof["step_frac"] = round(primary["value"] / HBM_PEAK_GBS, 4)
     config_extra = {"ms_eager": round(primary["ms_eager"], 4), "ms_graph": round(primary["ms_graph"], 4),
                     "graph_matches_eager": primary["graph_matches_eager"]}
     line = {

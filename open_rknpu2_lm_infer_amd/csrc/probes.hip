@@ -10,6 +10,10 @@
 //   rk_npu_hip_mfma_probe(blocks, iters, sink, stream): `blocks` x 256
 //     threads, each wave `iters` rounds of 8 MFMAs (65536 int8 ops each);
 //     sink holds one int32 per thread.
+//   rk_npu_hip_lds_probe(blocks, threads, iters, sink, clocks, stream):
+//     `blocks` x `threads` threads with 64 KB of LDS each, every wave reading
+//     iters x 8 KB from LDS; sink holds one uint32 per wave, clocks two
+//     uint64 per block (shader-clock cycles, 100 MHz ticks of the loop).
 //   stream: read `bytes` of device memory once with 16-byte non-temporal
 //     loads (the GEMV's load instruction) in one launch of a chosen grid, or
 //     launch the same grid with no loads (the launch's fixed cost);
@@ -83,6 +87,41 @@ __global__ __launch_bounds__(256) void mfma_probe_kernel(int iters, int* __restr
     sink[(size_t)blockIdx.x * blockDim.x + t] = s;
 }
 
+// LDS read bandwidth: every wave of the block streams conflict-free 16-byte
+// reads (lane l of a wave reads chunk l of a 1 KB row; 8 reads in flight)
+// out of a 64 KB buffer, `iters` rounds of 8 rows per wave. Wave 0 of each
+// block records the shader-clock cycles (s_memtime) and the 100 MHz real-time
+// ticks (s_memrealtime) the loop took, so bytes per clock per CU follow.
+__global__ __launch_bounds__(512) void lds_probe_kernel(int iters, unsigned* __restrict__ sink,
+                                                        unsigned long long* __restrict__ clocks) {
+    extern __shared__ v4u lds_buf[];  // 4096 chunks of 16 bytes
+    for (int i = threadIdx.x; i < 4096; i += blockDim.x) lds_buf[i] = v4u{(unsigned)i, (unsigned)i + 1, 7u, 9u};
+    __syncthreads();
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const unsigned long long c0 = __builtin_amdgcn_s_memtime();
+    const unsigned long long r0 = __builtin_amdgcn_s_memrealtime();
+    v4u x = {0u, 0u, 0u, 0u};
+    int row = wave * 8;
+    for (int it = 0; it < iters; ++it) {
+        v4u v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = lds_buf[((row + j) & 63) * 64 + lane];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x ^= v[j];
+        row += 64;
+    }
+    const unsigned long long c1 = __builtin_amdgcn_s_memtime();
+    const unsigned long long r1 = __builtin_amdgcn_s_memrealtime();
+    unsigned y = x.x ^ x.y ^ x.z ^ x.w;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) y ^= __shfl_xor(y, off);
+    if (lane == 0) sink[(size_t)blockIdx.x * (blockDim.x >> 6) + wave] = y;
+    if (threadIdx.x == 0) {
+        clocks[2 * blockIdx.x] = c1 - c0;
+        clocks[2 * blockIdx.x + 1] = r1 - r0;
+    }
+}
+
 }  // namespace hm
 
 using namespace hm;
@@ -102,6 +141,15 @@ int rk_npu_hip_stream_probe(const void* src, uint64_t bytes, int blocks, int thr
 int rk_npu_hip_mfma_probe(int blocks, int iters, int32_t* sink, void* stream) {
     if (blocks < 1 || blocks > (1 << 20) || iters < 1 || !sink) return RK_NPU_ERR_PARAM;
     hipLaunchKernelGGL(mfma_probe_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream), iters, sink);
+    return hipGetLastError() == hipSuccess ? RK_NPU_OK : RK_NPU_ERR_DEVICE;
+}
+
+int rk_npu_hip_lds_probe(int blocks, int threads, int iters, uint32_t* sink, uint64_t* clocks, void* stream) {
+    if (blocks < 1 || blocks > (1 << 20) || threads < 64 || threads > 512 || threads % 64 != 0 || iters < 1 ||
+        !sink || !clocks)
+        return RK_NPU_ERR_PARAM;
+    hipLaunchKernelGGL(lds_probe_kernel, dim3(blocks), dim3(threads), 65536, static_cast<hipStream_t>(stream), iters,
+                       sink, reinterpret_cast<unsigned long long*>(clocks));
     return hipGetLastError() == hipSuccess ? RK_NPU_OK : RK_NPU_ERR_DEVICE;
 }
 
