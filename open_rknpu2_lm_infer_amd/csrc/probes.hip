@@ -14,6 +14,9 @@
 //     `blocks` x `threads` threads with 64 KB of LDS each, every wave reading
 //     iters x 8 KB from LDS; sink holds one uint32 per wave, clocks two
 //     uint64 per block (shader-clock cycles, 100 MHz ticks of the loop).
+//   rk_npu_hip_wave_place_probe(blocks, threads, out, stream): every wave
+//     of `blocks` x `threads` stores its hardware id register (SIMD, CU) at
+//     out[block * waves + wave].
 //   stream: read `bytes` of device memory once with 16-byte non-temporal
 //     loads (the GEMV's load instruction) in one launch of a chosen grid, or
 //     launch the same grid with no loads (the launch's fixed cost);
@@ -122,6 +125,14 @@ __global__ __launch_bounds__(512) void lds_probe_kernel(int iters, unsigned* __r
     }
 }
 
+// Where the waves of a block run: wave w of block b stores the hardware id
+// register (HW_REG_HW_ID: bits 3:0 wave slot, 5:4 SIMD, 11:8 CU, 15:13 shader
+// engine) at out[b * waves + w].
+__global__ void wave_place_kernel(unsigned* __restrict__ out) {
+    const unsigned id = __builtin_amdgcn_s_getreg((31 << 11) | (0 << 6) | 4);
+    if ((threadIdx.x & 63) == 0) out[blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)] = id;
+}
+
 }  // namespace hm
 
 using namespace hm;
@@ -150,6 +161,13 @@ int rk_npu_hip_lds_probe(int blocks, int threads, int iters, uint32_t* sink, uin
         return RK_NPU_ERR_PARAM;
     hipLaunchKernelGGL(lds_probe_kernel, dim3(blocks), dim3(threads), 65536, static_cast<hipStream_t>(stream), iters,
                        sink, reinterpret_cast<unsigned long long*>(clocks));
+    return hipGetLastError() == hipSuccess ? RK_NPU_OK : RK_NPU_ERR_DEVICE;
+}
+
+int rk_npu_hip_wave_place_probe(int blocks, int threads, uint32_t* out, void* stream) {
+    if (blocks < 1 || blocks > (1 << 16) || threads < 64 || threads > 1024 || threads % 64 != 0 || !out)
+        return RK_NPU_ERR_PARAM;
+    hipLaunchKernelGGL(wave_place_kernel, dim3(blocks), dim3(threads), 0, static_cast<hipStream_t>(stream), out);
     return hipGetLastError() == hipSuccess ? RK_NPU_OK : RK_NPU_ERR_DEVICE;
 }
 
