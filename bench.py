@@ -1062,15 +1062,15 @@ SWEEP_SHAPES = (("M128 up 2560x9728 W8", 8, 128, H, F, False), ("M512 gate_up 25
 
 
 def tile_sweep(torch, ctx, only=None, reps=5):
-    """Every GEMM tile (HM_GEMM_VARIANT 0..4: 256x256, 256x128, 128x128, 64x128,
-    32x128) unsplit, and the split-K counts 2, 3, 4, 6, 8 (HM_SPLITS) of the
+    """Every GEMM tile (HM_GEMM_VARIANT 0..5: 256x256, 256x128, 128x128, 64x128,
+    32x128, 192x256) unsplit, and the split-K counts 2, 3, 4, 6, 8 (HM_SPLITS) of the
     128x128 and 64x128 tiles, plus the plan's own choice, on the GEMM shapes of
     the bench: one library call (quantization launch included) per distinct
     weight copy, enough copies that they exceed the last-level cache, in a
     graph. Workspaces are created under each setting so split partials fit."""
     from open_rknpu2_lm_infer_amd import device as D
     gen = Gen(torch, 7)
-    configs = [(-1, 0)] + [(v, 1) for v in range(5)] + [(v, sp) for v in (2, 3) for sp in (2, 3, 4, 6, 8)]
+    configs = [(-1, 0)] + [(v, 1) for v in range(6)] + [(v, sp) for v in (2, 3) for sp in (2, 3, 4, 6, 8)]
     out = {}
     for name, bits, m, k, n, sw in SWEEP_SHAPES:
         if only and not any(o in name for o in only):

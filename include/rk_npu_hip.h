@@ -140,8 +140,8 @@ int rk_npu_hip_inject_alloc_failures(int count);
  * variable of the same name, read once per process; this call sets one for
  * the rest of the process (later plans and workspace sizing use it) and
  * stores the value it replaces in *previous (may be NULL). Names and values:
- *   HM_GEMM_VARIANT  -1 by shape; 0..4 forces the 256x256, 256x128, 128x128,
- *                    64x128 or 32x128 GEMM tile
+ *   HM_GEMM_VARIANT  -1 by shape; 0..5 forces the 256x256, 256x128, 128x128,
+ *                    64x128, 32x128 or 192x256 GEMM tile
  *   HM_SPLITS        0 by shape; n > 0 forces n K pieces per GEMM tile
  *   HM_FORCE_GEMM    1: rows <= 8 take the MFMA GEMM instead of the GEMV
  *   HM_GEMV_QW       -1 by shape; 0 never, 1 always (when the rows fit) a

@@ -299,8 +299,8 @@ void weights_destroy(Weights* w) {
 // --- launch plans -------------------------------------------------------------
 
 // (GemmVariant: launch.hpp)
-static const int kBM[] = {256, 256, 128, 64, 32};
-static const int kBN[] = {256, 128, 128, 128, 128};
+static const int kBM[] = {256, 256, 128, 64, 32, 192};
+static const int kBN[] = {256, 128, 128, 128, 128, 256};
 
 // Plan switches for tests and measurements. Each starts from its environment
 // variable, read once when the library first plans a launch; afterwards only
@@ -371,7 +371,7 @@ static Plan plan_gemm(int rows, const Geometry& g, int variant) {
     int v = variant;
     if (v < 0) {
         const int forced = switch_value(SW_GEMM_VARIANT);
-        if (forced >= 0 && forced <= 4)
+        if (forced >= 0 && forced <= 5)
             v = forced;
         else
             v = rows <= 32 ? V32x128 : rows <= 1024 ? V64x128 : V128x128;
@@ -384,6 +384,13 @@ static Plan plan_gemm(int rows, const Geometry& g, int variant) {
             // o 4096x2560 in 68 us against 73 and down 9728x2560 in 158 against
             // 172 (bench.py --tile-sweep), although its 160 tiles leave CUs idle.
             if (t256 >= 8LL * cus || (g.K_pad >= 4096 && t128 > 2LL * cus)) v = V256x256;
+            // 192x256 where it takes fewer rows per CU: M=4096 o 4096x2560 and
+            // down 9728x2560 run 220 tiles of 192 rows in one round instead of
+            // 160 tiles of 256 rows, which left 96 CUs idle.
+            if (v == V256x256) {
+                const long long t192 = (long long)((rows + 191) / 192) * (g.N_pad / 256);
+                if ((t192 + cus - 1) / cus * 192 < (t256 + cus - 1) / cus * 256) v = V192x256;
+            }
         }
     }
     const int KT = g.K_pad / 64;

@@ -721,9 +721,17 @@ struct TileCfg {
     static constexpr int A_STAGE = BM * 64;
     static constexpr int B_STAGE = (BITS == 8) ? BN * 64 : BN * 32;
     static constexpr int STAGE = A_STAGE + B_STAGE;
-    static constexpr int A_LOADS = A_STAGE / 16 / NT;
+    // A rounds of NT 16-byte chunks; when BM * 4 chunks are not a whole
+    // number of rounds (BM = 192), only the first A_LAST_WAVES waves load in
+    // the last A round, so those waves issue LPS loads per stage and the
+    // others LPS - 1.
+    static constexpr int A_CHUNKS = A_STAGE / 16;
+    static constexpr int A_LOADS = (A_CHUNKS + NT - 1) / NT;
+    static constexpr bool A_SPLIT = A_CHUNKS % NT != 0;
+    static constexpr int A_LAST_WAVES = (A_CHUNKS - (A_LOADS - 1) * NT) / 64;
     static constexpr int B_LOADS = B_STAGE / 16 / NT;
     static constexpr int LPS = A_LOADS + B_LOADS;
+    static constexpr int LPS_LO = A_SPLIT ? LPS - 1 : LPS;
     // as many stages as fit in 128 KB of LDS, at most 4
     static constexpr int STAGES = (4 * STAGE <= 131072) ? 4 : (3 * STAGE <= 131072 ? 3 : 2);
     static constexpr int LDS = STAGES * STAGE;
@@ -731,7 +739,7 @@ struct TileCfg {
     // 32 rows per wave (f32, worst case) when that is larger.
     static constexpr int EPI_ROW = TN * 4 + 16;
     static constexpr int SMEM = LDS > WGM * WGN * 32 * EPI_ROW ? LDS : WGM * WGN * 32 * EPI_ROW;
-    static_assert(A_STAGE % (16 * NT) == 0 && B_STAGE % (16 * NT) == 0, "tile/thread mismatch");
+    static_assert(A_CHUNKS % 64 == 0 && B_STAGE % (16 * NT) == 0, "tile/thread mismatch");
     static_assert(BN % 64 == 0, "a wave's B loads must cover one plane");
     static_assert(LPS * (STAGES - 1) <= 63, "vmcnt range");
 };
@@ -793,14 +801,28 @@ __device__ __forceinline__ void gemm_mainloop(uint8_t* smem, const int8_t* __res
     const int b_lane = (half_id * BN + wn * TN + l32) * 16;
 
     // Load d of a stage (A loads first), fragment read f, MFMA t: all indices
-    // are compile-time constants after unrolling.
+    // are compile-time constants after unrolling. In the last A round of a
+    // split A stage the waves past A_LAST_WAVES have no chunk (a uniform
+    // branch), and wait_own waits for each wave's own count.
     auto issue1 = [&](int d, int kt_, int buf) {
         uint8_t* sa = smem + buf * STAGE;
-        if (d < A_LOADS)
-            lds_dma16(ga + ((size_t)kt_ * 4 * a_plane + a_off[d]) * 16, sa + (d * NT + wave * 64) * 16);
-        else
+        if (d < A_LOADS) {
+            if (!C::A_SPLIT || d < A_LOADS - 1 || wave < C::A_LAST_WAVES)
+                lds_dma16(ga + ((size_t)kt_ * 4 * a_plane + a_off[d]) * 16, sa + (d * NT + wave * 64) * 16);
+        } else
             lds_dma16(gb + b_src[d - A_LOADS] + (size_t)kt_ * (PPS * 128),
                       sa + A_STAGE + ((d - A_LOADS) * NT + wave * 64) * 16);
+    };
+    auto wait_own = [&](auto stages) {
+        constexpr int n = decltype(stages)::value;
+        if constexpr (C::A_SPLIT) {
+            if (wave < C::A_LAST_WAVES)
+                wait_vmcnt<LPS * n>();
+            else
+                wait_vmcnt<C::LPS_LO * n>();
+        } else {
+            wait_vmcnt<LPS * n>();
+        }
     };
     auto read1 = [&](int f, int buf) -> v4i {
         const uint8_t* r = smem + buf * STAGE;
@@ -827,7 +849,7 @@ __device__ __forceinline__ void gemm_mainloop(uint8_t* smem, const int8_t* __res
 #pragma unroll
             for (int d = 0; d < LPS; ++d) issue1(d, st, st);
     if (KT >= S)
-        wait_vmcnt<LPS * (S - 1)>();
+        wait_own(IntTag<S - 1>{});
     else
         wait_vmcnt<0>();
     __builtin_amdgcn_s_barrier();
@@ -848,7 +870,7 @@ __device__ __forceinline__ void gemm_mainloop(uint8_t* smem, const int8_t* __res
         wait_lgkmcnt0();                                                                          \
         if ((kt_) + 1 < KT) {                                                                     \
             if ((kt_) + S - 1 < KT)                                                               \
-                wait_vmcnt<LPS * (S - 2)>();                                                      \
+                wait_own(IntTag<S - 2>{});                                                        \
             else                                                                                  \
                 wait_vmcnt<0>();                                                                  \
         }                                                                                         \
@@ -1186,8 +1208,10 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_kernel(GemmParams P) {
     size_t a_off[C::A_LOADS];
 #pragma unroll
     for (int i = 0; i < C::A_LOADS; ++i) {
-        const int c = threadIdx.x + i * NT;
-        a_off[i] = (size_t)(c / BM) * P.M_alloc + m0 + c % BM;
+        // (tile rows past the code buffer's rows, which a 192-row tile of the
+        // last M-tile reaches, read its last row; their outputs are masked)
+        const int c = min((int)threadIdx.x + i * NT, C::A_CHUNKS - 1);
+        a_off[i] = (size_t)(c / BM) * P.M_alloc + min(m0 + c % BM, P.M_alloc - 1);
     }
     EpiPre<BM, BN, WGM, WGN, BITS> pre;
     if constexpr (SPLIT == SPLIT_NONE)

@@ -17,7 +17,7 @@ int device_cus();  // compute units of the current device (hip_matmul.hip)
 
 // GEMM block tiles (rows x columns), indexed by the plan (kBM / kBN in
 // hip_matmul.hip).
-enum GemmVariant { V256x256 = 0, V256x128 = 1, V128x128 = 2, V64x128 = 3, V32x128 = 4 };
+enum GemmVariant { V256x256 = 0, V256x128 = 1, V128x128 = 2, V64x128 = 3, V32x128 = 4, V192x256 = 5 };
 
 // GEMM of one weight width: epi EPI_PLAIN / EPI_SWIGLU_MAX, tile variant v,
 // staged (16-byte aligned output) or not, G.splits K pieces.

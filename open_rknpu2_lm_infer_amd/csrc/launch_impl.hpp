@@ -43,6 +43,9 @@ static void launch_gemm(int v, bool staged, const GemmParams& G, int tiles, hipS
         case V256x256:
             hipLaunchKernelGGL((gemm_kernel<256, 256, 2, 4, BITS, EPI, true>), dim3(tiles), dim3(512), 0, s, G);
             break;
+        case V192x256:
+            hipLaunchKernelGGL((gemm_kernel<192, 256, 2, 4, BITS, EPI, true>), dim3(tiles), dim3(512), 0, s, G);
+            break;
         case V256x128:
             hipLaunchKernelGGL((gemm_kernel<256, 128, 2, 2, BITS, EPI, true>), dim3(tiles), dim3(256), 0, s, G);
             break;

@@ -95,14 +95,19 @@ def test_gemv_matrix_core_dots(ctx, bits, k):
 @pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize("rows,variant,n", [(1100, None, 768), (2100, None, 768), (2100, "0", 768),
                                             (4100, "0", 768), (2100, "0", 640), (300, "0", 896),
-                                            (4100, "0", 640), (300, "1", 896), (4100, "1", 640)])
+                                            (4100, "0", 640), (300, "1", 896), (4100, "1", 640),
+                                            (4096, "5", 768), (4100, "5", 640), (300, "5", 896),
+                                            (192, "5", 768), (2000, "5", 512)])
 def test_device_linear_large_row_tiles(ctx, bits, rows, variant, n):
     """Row counts that select the 128x128 tile, and the 256x256 tile (variant
-    0: chosen by the plan for very wide outputs or long K) and the 256x128
-    tile (variant 1), forced here at small shapes. n = 640 and 896 leave 128
-    padded columns in the last 256-wide tile, as the 2560x151936 lm_head does
-    (plain and SwiGLU stores masked at the edge); 4100 and 300 rows end inside
-    a 256-row tile."""
+    0: chosen by the plan for very wide outputs or long K), the 256x128 tile
+    (variant 1) and the 192x256 tile (variant 5: its last A load round is
+    issued by half of the waves; the plan takes it for M=4096 o and down),
+    forced here at small shapes. n = 640 and 896 leave 128 padded columns in
+    the last 256-wide tile, as the 2560x151936 lm_head does (plain and SwiGLU
+    stores masked at the edge); 4100 and 300 rows end inside a 256-row tile,
+    4096, 4100, 300 and 2000 inside a 192-row tile whose rows reach past the
+    code buffer's (4096 rows: 22 tiles of 192 cover 4224)."""
     with D.plan_switch("HM_GEMM_VARIANT", -1 if variant is None else int(variant)):
         _large_row_tiles(ctx, bits, rows, n)
 
