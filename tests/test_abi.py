@@ -156,7 +156,9 @@ def test_plans():
     assert L.rk_npu_hip_linear_plan(4096, 2560, 151936, 8, ctypes.byref(plan)) == 0
     assert (plan.kind, plan.block_m, plan.block_n, plan.k_splits) == (1, 256, 256, 1)
     assert L.rk_npu_hip_linear_plan(4096, 9728, 2560, 8, ctypes.byref(plan)) == 0
-    assert (plan.kind, plan.block_m, plan.block_n, plan.k_splits, plan.grid) == (1, 256, 256, 1, 16 * 10)
+    # (192x256 where it takes fewer rows per CU: 22 x 10 tiles in one round of
+    # 256 CUs instead of 16 x 10 of 256 rows)
+    assert (plan.kind, plan.block_m, plan.block_n, plan.k_splits, plan.grid) == (1, 192, 256, 1, 22 * 10)
     assert L.rk_npu_hip_linear_plan(3072, 9728, 2560, 8, ctypes.byref(plan)) == 0
     assert (plan.kind, plan.block_m, plan.block_n, plan.k_splits, plan.grid) == (1, 128, 128, 1, 24 * 20)
     assert L.rk_npu_hip_linear_plan(0, 2560, 9728, 8, ctypes.byref(plan)) == F.RK_NPU_ERR_PARAM
