@@ -274,12 +274,26 @@ class DenseLayers:
         self.D = D
 
     def step(self):
+        """One pass over the 36 layers with a layer's data flow: qkv's output
+        feeds o (its first rows x 4096 values standing in for the attention
+        output) and o's output feeds the FFN, so every launch reads what the
+        one before it wrote. Each layer's qkv reads the same fixed input: fed
+        the previous layer's FFN output instead, without the model's RMSNorm
+        (not part of this path), random weights and the SwiGLU's squaring take
+        the values to zero or to overflow within a few layers, and zero data
+        lets the matrix cores hold a higher clock (an M=4096 step measured
+        19.1 ms against 20.3 ms), which would not be the workload."""
         D, ctx, r = self.D, self.ctx, self.rows
+        attn = self.y_qkv.view(-1)[:r * Q].view(r, Q)
         for mats in self.w:
             D.linear(ctx, mats["qkv"], self.x_qkv, self.y_qkv, r, ws=self.ws["qkv"])
-            D.linear(ctx, mats["o"], self.x_o, self.y_o, r, ws=self.ws["o"])
-            D.ffn(ctx, mats["gate_up"], mats["down"], self.x_ffn, self.y_ffn, r, gws=self.ws["gate_up"],
+            D.linear(ctx, mats["o"], attn, self.y_o, r, ws=self.ws["o"])
+            D.ffn(ctx, mats["gate_up"], mats["down"], self.y_o, self.y_ffn, r, gws=self.ws["gate_up"],
                   dws=self.ws["down"])
+
+    def magnitudes(self):
+        """max |value| of the three outputs after a step (the data stays in range)."""
+        return [round(float(t.float().abs().max()), 3) for t in (self.y_qkv, self.y_o, self.y_ffn)]
 
     def bytes_per_layer(self):
         w0, r = self.w[0], self.rows
@@ -355,7 +369,7 @@ def run_decode(torch, ctx, rows, steps, warmup, want_cpu, want_roofline=True, ti
         out.update({"ms_per_step": ms, "value": nbytes / (ms * 1e-3) / 1e9, "ms_eager": ms_eager,
                     "ms_graph": ms_graph, "graph_matches_eager": ok})
         log(f"[bench] decode M={rows}: eager {ms_eager:.3f} ms/step, graph {ms_graph:.3f} ms/step "
-            f"(replay bit-exact: {ok}) -> {out['value']:.1f} GB/s")
+            f"(replay bit-exact: {ok}) -> {out['value']:.1f} GB/s; max |qkv|, |o|, |ffn| {t.magnitudes()}")
     if want_roofline:
         # Dominant kernel: the gate_up GEMV (25 MB of W4 weights per launch).
         passes = decode_passes(torch, ctx, t, reps or steps)
@@ -447,7 +461,7 @@ def run_prefill(torch, ctx, rows, steps, warmup, want_cpu=True, timed=True, reps
     if timed:
         def step():
             t.step()
-            D.linear(ctx, head, t.x_qkv, y_head, rows, ws=ws_head)
+            D.linear(ctx, head, t.y_ffn, y_head, rows, ws=ws_head)  # the last layer's output feeds the lm_head
 
         ms, ms_eager, ms_graph, ok = best_time(torch, step, steps, warmup,
                                                lambda: [t.y_qkv.clone(), t.y_ffn.clone(), y_head.clone()])
@@ -466,7 +480,8 @@ def run_prefill(torch, ctx, rows, steps, warmup, want_cpu=True, timed=True, reps
                                      "HIP events on the replay stream")
     if timed:
         res["vendor_ref"] = vendor_int8_gemm(torch, rows, H, 2 * F)
-        log(f"[bench] prefill: {res['value']} TOPS ({ms:.2f} ms/step); vendor int8 GEMM {res['vendor_ref']}")
+        log(f"[bench] prefill: {res['value']} TOPS ({ms:.2f} ms/step); vendor int8 GEMM {res['vendor_ref']}; "
+            f"max |qkv|, |o|, |ffn| {t.magnitudes()}")
     log(f"[bench] prefill projections: {passes}")
     if want_cpu:
         xs = t.x_qkv[:64].float().cpu().numpy(), t.x_o[:64].float().cpu().numpy()
@@ -501,7 +516,6 @@ def vendor_int8_gemm(torch, m, k, n, reps=20):
 def run_ffn512(torch, ctx, steps, warmup, rows=512, want_cpu=True, timed=True, reps=None):
     """Config 2: M=512 W4A8 gate_up -> SwiGLU -> requant -> W8A8 down, 36 layers."""
     from open_rknpu2_lm_infer_amd import device as D
-    from oracle import oracle
     gen = Gen(torch, 2)
     layers, host0 = [], None
     for l in range(LAYERS):
@@ -537,6 +551,7 @@ def run_ffn512(torch, ctx, steps, warmup, rows=512, want_cpu=True, timed=True, r
                                      "replay stream")
     if want_cpu:
         xs = x[:64].float().cpu().numpy()
+        from oracle import oracle
         sec, reps_c = cpu_median(lambda: oracle.ffn(host0[0], host0[1], host0[2], host0[3], xs), 4.0)
         res["cpu_baseline"] = cpu_baseline(2.0 * 64 * (H * 2 * F + F * H) / sec / 1e12, "TOPS", sec, reps_c,
                                            "64 of 512 rows of layer 0's FFN (gate_up+SwiGLU->requant->down)",
@@ -553,7 +568,6 @@ def run_up128(torch, ctx, steps, warmup, rows=128, want_cpu=True, timed=True, re
     the same call replayed on one weight set (25 MB, cache-resident) is
     reported beside it."""
     from open_rknpu2_lm_infer_amd import device as D
-    from oracle import oracle
     gen = Gen(torch, 0)
     codes, scales = gen.codes("up/w", 8, H, F), gen.scales("up/w", F)
     ws_ = [ctx.weights(8, codes, scales) for _ in range(LAYERS)]
@@ -578,6 +592,7 @@ def run_up128(torch, ctx, steps, warmup, rows=128, want_cpu=True, timed=True, re
         res["cache_resident_us"] = round(ms * 1e3, 2)
     if want_cpu:
         xh = x.float().cpu().numpy()
+        from oracle import oracle
         sec, reps_c = cpu_median(lambda: oracle.linear(host[0], host[1], xh), 4.0)
         res["cpu_baseline"] = cpu_baseline(ops / sec / 1e12, "TOPS", sec, reps_c, "the whole call (128 rows)")
     log(f"[bench] up128: {res['value']} TOPS, {res['gbs']} GB/s per call from HBM")
@@ -661,7 +676,6 @@ def run_moe(torch, ctx, steps, warmup, tokens_list=(512, 1), want_cpu=True):
     from open_rknpu2_lm_infer_amd import _ffi as F_
     from open_rknpu2_lm_infer_amd import device as D
     from open_rknpu2_lm_infer_amd import npu
-    from oracle import oracle
     h, inter, experts, top, sh_inter = 2048, 768, 128, 8, 2048
     g = np.random.default_rng(0x5EED0004)
     L = F_.lib()
@@ -697,7 +711,7 @@ def run_moe(torch, ctx, steps, warmup, tokens_list=(512, 1), want_cpu=True):
         ids = np.zeros((T, top), np.int32)
         rw = np.zeros((T, top), np.float32)
         for r in range(T):
-            ids[r], rw[r] = oracle.routes(logits[r], top)
+            ids[r], rw[r] = npu.routes(logits[r], top)  # the product mirror of the router
         x_host = g.standard_normal((T, h)).astype(np.float32)
         x = torch.from_numpy(x_host).cuda()
         d_ids = torch.from_numpy(ids).cuda()
@@ -738,6 +752,7 @@ def run_moe(torch, ctx, steps, warmup, tokens_list=(512, 1), want_cpu=True):
             gu_l = [(c[0], c[1]) for c in keep]
             dn_l = [(c[2], c[3]) for c in keep]
             shared = ((sh_host[0], sh_host[1]), (sh_host[2], sh_host[3]))
+            from oracle import oracle
             fn = lambda: oracle.moe(gu_l, dn_l, x_host[:sample], ids[:sample], rw[:sample], shared=shared)
             sec, reps_c = cpu_median(fn, 4.0)
             s_ops = (routed_ops + shared_ops) * sample / T
@@ -1008,7 +1023,6 @@ def moe_shared_bank_t1(torch, ctx, steps):
     from open_rknpu2_lm_infer_amd import _ffi as F_
     from open_rknpu2_lm_infer_amd import device as D
     from open_rknpu2_lm_infer_amd import npu
-    from oracle import oracle
     h, inter, experts, top = 2048, 768, 128, 8
     g = np.random.default_rng(0x5EED0004 + 1)
     L = F_.lib()
@@ -1029,7 +1043,8 @@ def moe_shared_bank_t1(torch, ctx, steps):
     work = npu._Handle(L.rk_npu_moe_w4w8_workspace_create(ctx.domain, ctypes.byref(cfg)),
                        L.rk_npu_moe_w8_workspace_free, "MoE workspace", ctx.shared)
     del arr, keep
-    ids, rw = oracle.routes(g.standard_normal(experts).astype(np.float32), top)
+    ids, rw = npu.routes(g.standard_normal(experts).astype(np.float32), top)
+    ids, rw = np.asarray(ids, np.int32), np.asarray(rw, np.float32)
     x = torch.from_numpy(g.standard_normal((1, h)).astype(np.float32)).cuda()
     d_ids = torch.from_numpy(ids[None, :].astype(np.int32)).cuda()
     d_rw = torch.from_numpy(rw[None, :].astype(np.float32)).cuda()
@@ -1754,6 +1769,8 @@ def main():
                                f"gate_up 2560x19456 + SwiGLU -> down 9728x2560), M={args.decode_rows}, 36 layers",
                    "rows": args.decode_rows, "layers": 36, "weight_bits": 4, "activations": "fp16 in/out, per-token dynamic int8",
                    "bytes_per_step": primary["bytes_per_step"], "parallelism": "single GPU",
+                   "data_flow": "within a layer qkv -> o -> FFN, each launch reading the previous one's output; "
+                                "each layer's qkv reads the fixed input",
                    "timing": "faster of eager launches and HIP graph replay of the same step "
                              "(replay checked bit-exact vs eager)", **config_extra},
         "roofline": roof,
