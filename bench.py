@@ -283,13 +283,16 @@ class DenseLayers:
         the values to zero or to overflow within a few layers, and zero data
         lets the matrix cores hold a higher clock (an M=4096 step measured
         19.1 ms against 20.3 ms), which would not be the workload."""
+        for mats in self.w:
+            self.layer(mats)
+
+    def layer(self, mats):
         D, ctx, r = self.D, self.ctx, self.rows
         attn = self.y_qkv.view(-1)[:r * Q].view(r, Q)
-        for mats in self.w:
-            D.linear(ctx, mats["qkv"], self.x_qkv, self.y_qkv, r, ws=self.ws["qkv"])
-            D.linear(ctx, mats["o"], attn, self.y_o, r, ws=self.ws["o"])
-            D.ffn(ctx, mats["gate_up"], mats["down"], self.y_o, self.y_ffn, r, gws=self.ws["gate_up"],
-                  dws=self.ws["down"])
+        D.linear(ctx, mats["qkv"], self.x_qkv, self.y_qkv, r, ws=self.ws["qkv"])
+        D.linear(ctx, mats["o"], attn, self.y_o, r, ws=self.ws["o"])
+        D.ffn(ctx, mats["gate_up"], mats["down"], self.y_o, self.y_ffn, r, gws=self.ws["gate_up"],
+              dws=self.ws["down"])
 
     def magnitudes(self):
         """max |value| of the three outputs after a step (the data stays in range)."""
@@ -992,11 +995,8 @@ def run_probes(torch, ctx, reps=20):
     # 256 MB last-level cache) replayed 36 times: what the step would take if
     # its weight reads cost nothing beyond the cache.
     def layer0_x36():
-        m = t.w[0]
         for _ in range(LAYERS):
-            D.linear(ctx, m["qkv"], t.x_qkv, t.y_qkv, 1, ws=t.ws["qkv"])
-            D.linear(ctx, m["o"], t.x_o, t.y_o, 1, ws=t.ws["o"])
-            D.ffn(ctx, m["gate_up"], m["down"], t.x_ffn, t.y_ffn, 1, gws=t.ws["gate_up"], dws=t.ws["down"])
+            t.layer(t.w[0])
     ms_step, _ = graph_time(torch, t.step, reps)
     ms_warm, _ = graph_time(torch, layer0_x36, reps)
     nbytes = t.bytes_per_layer() * LAYERS
@@ -1005,6 +1005,20 @@ def run_probes(torch, ctx, reps=20):
         "layer 0 x 36 (weights cache-resident)": {"ms": round(ms_warm, 4), "gbs": round(nbytes / ms_warm / 1e6, 1)}}
     log(f"[probe] decode step, cache-warm bound: {res['decode_step_cache_warm']}")
     del t
+    torch.cuda.empty_cache()
+    # One launch reading the decode step's whole weight volume (1.82 GB): the
+    # HBM read rate a single stream sustains, the ceiling of a step whose
+    # launches had no fixed cost.
+    big = torch.empty(nbytes // 16 * 16, dtype=torch.uint8, device="cuda")
+    res["hbm_read_step_volume"] = {"bytes": big.numel()}
+    for blocks, thr in ((1024, 256), (2048, 256), (4096, 256), (1024, 512)):
+        def fn():
+            npu_check(LP.rk_npu_hip_stream_probe(ctypes.c_void_p(big.data_ptr()), big.numel(), blocks, thr, 1,
+                                                ctypes.c_void_p(sinkb.data_ptr()), cur()), "stream probe")
+        ms, _ = graph_time(torch, fn, 5)
+        res["hbm_read_step_volume"][f"{blocks}x{thr}"] = {"ms": round(ms, 4), "gbs": round(big.numel() / ms / 1e6, 1)}
+    log(f"[probe] one launch over the step's bytes: {res['hbm_read_step_volume']}")
+    del big
     res["moe_t1_shared_in_bank"] = moe_shared_bank_t1(torch, ctx, reps * 10)
     log(f"[probe] MoE T=1 with the shared expert in the bank: {res['moe_t1_shared_in_bank']}")
     return res
@@ -1517,6 +1531,15 @@ def profile_probes(probes_json):
         best[p["projection"]] = min(reads)
     c = d["decode_step_cache_warm"]
     a, b = c["36 distinct layers (the bench step)"], c["layer 0 x 36 (weights cache-resident)"]
+    v = d.get("hbm_read_step_volume")
+    if v:
+        rates = {k: x["gbs"] for k, x in v.items() if isinstance(x, dict)}
+        best_k = max(rates, key=rates.get)
+        out += ["", f"One launch reading the decode step's whole weight volume ({v['bytes']} B) with the same loads:",
+                "    " + ", ".join(f"{k} {x['ms']:.4f} ms {x['gbs']:.1f} GB/s" for k, x in v.items()
+                               if isinstance(x, dict)),
+                f"    best {rates[best_k]:.1f} GB/s ({rates[best_k] / 80:.1f}% of 8 TB/s): the HBM read rate one stream "
+                "sustains, the ceiling of a decode step whose launches cost nothing."]
     m = d["moe_t1_shared_in_bank"]
     f1, f0 = m["combine in the shared down GEMV"], m["combine as its own launch"]
     s = sum(best[k] for k in ("qkv", "o", "gate_up", "down"))

@@ -546,7 +546,8 @@ void workspace_destroy(Workspace* ws) {
 // --- enqueue ------------------------------------------------------------------
 
 int enqueue_quant(Workspace* ws, const void* x, int x_type, long lda, int rows, int rule, RowMax in_max,
-                  unsigned* rowmax_clear, hipStream_t s, const int* rows_dev) {
+                  unsigned* rowmax_clear, hipStream_t s, const int* rows_dev, const int* row_map, int map_div,
+                  const QuantOut* out) {
     QuantParams P;
     P.x = x;
     P.x_type = x_type;
@@ -564,6 +565,14 @@ int enqueue_quant(Workspace* ws, const void* x, int x_type, long lda, int rows, 
     P.part_count = in_max.count;
     P.rowmax_clear = rowmax_clear;
     P.rows_dev = rows_dev;
+    P.row_map = row_map;
+    P.map_div = map_div;
+    if (out) {
+        P.codes = out->codes;
+        P.rowscale = out->rowscale;
+        P.rowsum = out->rowsum;
+        P.M_alloc = out->M_alloc;
+    }
     // Measured on the Qwen3-4B activation shapes (M = 128 ... 4096): with
     // aligned rows the row-tiled kernel (4 rows per block, one wave per row,
     // code planes written as 64-byte runs) is fastest, e.g. 31 us instead of

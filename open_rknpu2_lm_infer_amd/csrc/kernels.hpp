@@ -194,7 +194,14 @@ struct QuantParams {
     int part_count;
     unsigned* rowmax_clear;  // zeroed for the block's rows (next middle's max)
     const int* rows_dev;     // optional device-side row count (<= rows)
+    const int* row_map;      // optional: output row r quantizes input row row_map[r] / map_div
+    int map_div;
 };
+
+// Input row of output row r (the MoE slot order: the slot's token).
+__device__ __forceinline__ int quant_src_row(const QuantParams& P, int r) {
+    return P.row_map ? P.row_map[r] / P.map_div : r;
+}
 
 __device__ __forceinline__ void load16(const float* p, float (&v)[16]) {
 #pragma unroll
@@ -345,7 +352,7 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantParams P) {
     if (P.rowmax_clear && tid == 0 && r < P.M_alloc) P.rowmax_clear[r] = 0u;
     if (r >= rows) return;  // uniform over the row's threads (a block or a wave)
     const int KG = P.K_pad >> 4;
-    const T* xr = x + (size_t)r * P.lda;
+    const T* xr = x + (size_t)quant_src_row(P, r) * P.lda;
     // 1. Issue every load (no branches around them: masked-off lanes re-read
     // the row start), then reduce.
     // (a masked-off chunk re-reads the row's first chunk, which aligned rows
@@ -461,7 +468,7 @@ __global__ __launch_bounds__(256) void quant_tile_kernel(QuantParams P) {
     const bool live = r < rows;
     const int KG = P.K_pad >> 4;
     const int groups = (KG + TW - 1) / TW;
-    const T* xr = x + (size_t)(live ? r : r0) * P.lda;
+    const T* xr = x + (size_t)quant_src_row(P, live ? r : r0) * P.lda;
     auto ok = [&](int kg) { return live && kg * 16 < P.K; };
 
     float m = 0.0f;

@@ -354,8 +354,15 @@ static int enqueue_moe(MoeWork* ws, const MoeBank* b, int rows, const float* inp
     // quantization launch); otherwise the rows are quantized first.
     const bool slot_quant = slot_gemv && (ws->h % 16) == 0 && (reinterpret_cast<uintptr_t>(input) & 15) == 0 &&
                             (b->ggu.K_pad / 16) <= 256 * GEMV_XMAX;
+    // Many slots: after routing, the tokens' rows are quantized straight into
+    // slot order (slot s holds token perm[s] / top), so the grouped GEMM's A
+    // loads are contiguous rows; one launch for what was a token quantization
+    // and a gather of its codes (measured at 4096 slots: gate/up 69 -> 57 us
+    // with contiguous rows). Few slots: the tokens are quantized once and the
+    // GEMM gathers rows itself.
+    const bool gather = !slot_gemv && A >= 256;
     int rc = RK_NPU_OK;
-    if (!slot_quant) {
+    if (!slot_quant && !gather) {
         rc = enqueue_quant(ws->xws, input, DT_F32, ws->h, rows, QUANT_MOE, RowMax{nullptr, 0}, nullptr, s);
         if (rc != RK_NPU_OK) return rc;
     }
@@ -451,26 +458,11 @@ static int enqueue_moe(MoeWork* ws, const MoeBank* b, int rows, const float* inp
     // one partial tile per expert.
     const int max_tiles = std::min(A, (A + std::min(A, ws->experts) * (MOE_BM - 1)) / MOE_BM);
 
-    // Many slots: token codes gathered into slot order first, so the grouped
-    // GEMM's A loads are contiguous rows (measured at 4096 slots: gate/up 69 ->
-    // 57 us for a 5.5 us gather). Few slots: the GEMM gathers rows itself.
-    const bool gather = !slot_gemv && A >= 256;
     if (gather) {
-        GatherParams Q;
-        Q.src = ws->xws->codes;
-        Q.src_scale = ws->xws->rowscale;
-        Q.src_sum = ws->xws->rowsum;
-        Q.src_alloc = ws->xws->M_alloc;
-        Q.perm = ws->perm;
-        Q.top = ws->top;
-        Q.counts = ws->counts;
-        Q.dst = ws->gcodes;
-        Q.dst_scale = ws->gscale;
-        Q.dst_sum = ws->gsum;
-        Q.dst_alloc = ws->g_alloc;
-        Q.planes = ws->xws->g.K_pad / 16;
-        const dim3 grid((A + 255) / 256, (Q.planes + GATHER_PLANES - 1) / GATHER_PLANES);
-        hipLaunchKernelGGL(moe_gather_kernel, grid, dim3(256), 0, s, Q);
+        const QuantOut q{ws->gcodes, ws->gscale, ws->gsum, ws->g_alloc};
+        rc = enqueue_quant(ws->xws, input, DT_F32, ws->h, A, QUANT_MOE, RowMax{nullptr, 0}, nullptr, s, ws->counts,
+                           ws->perm, ws->top, &q);
+        if (rc != RK_NPU_OK) return rc;
     }
 
     if (!slot_gemv) {

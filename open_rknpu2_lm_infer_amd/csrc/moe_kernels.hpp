@@ -43,11 +43,21 @@ static __global__ __launch_bounds__(1024) void moe_route_kernel(RouteParams P) {
     }
     for (int i = tid; i < P.rowmax_count; i += 1024) P.rowmax_mid[i] = 0u;
     __syncthreads();
-    for (int a = tid; a < A; a += 1024) {
+    // Each thread's first RC assignments stay in registers for the second
+    // pass (the expert, or -1 for a skipped route); the rest are read again.
+    constexpr int RC = 8;
+    int ce[RC];
+#pragma unroll
+    for (int i = 0; i < RC; ++i) ce[i] = -1;
+    for (int a = tid, i = 0; a < A; a += 1024, ++i) {
         const int e = P.ids[a];
         const bool in_range = e >= 0 && e < P.experts;
         if (!in_range) atomicOr(P.error, 1u);
-        if (in_range && P.routes[a] > 0.0f) atomicAdd(&cnt[e], 1);
+        const bool live = in_range && P.routes[a] > 0.0f;
+        if (live) atomicAdd(&cnt[e], 1);
+#pragma unroll
+        for (int j = 0; j < RC; ++j)
+            if (i == j) ce[j] = live ? e : -1;
     }
     __syncthreads();
     // Exclusive prefix sums of slots and tiles over the experts: wave 0, each
@@ -88,10 +98,18 @@ static __global__ __launch_bounds__(1024) void moe_route_kernel(RouteParams P) {
         }
     }
     __syncthreads();
-    for (int a = tid; a < A; a += 1024) {
-        const int e = P.ids[a];
+    for (int a = tid, i = 0; a < A; a += 1024, ++i) {
+        int e = -1;
+        if (i < RC) {
+#pragma unroll
+            for (int j = 0; j < RC; ++j)
+                if (i == j) e = ce[j];
+        } else {
+            e = P.ids[a];
+            if (!(e >= 0 && e < P.experts && P.routes[a] > 0.0f)) e = -1;
+        }
         int slot = -1;
-        if (e >= 0 && e < P.experts && P.routes[a] > 0.0f) {
+        if (e >= 0) {
             slot = off[e] + atomicAdd(&fill[e], 1);
             P.perm[slot] = a;
         }
@@ -103,50 +121,6 @@ static __global__ __launch_bounds__(1024) void moe_route_kernel(RouteParams P) {
             const int b = off[e] + t * P.bm;
             P.tiles[toff[e] + t] = make_int4(e, b, min(off[e] + cnt[e], b + P.bm), 0);
         }
-    }
-}
-
-// ---------------------------------------------------------------------------
-// Gather of the quantized token rows into slot order (slot s holds token
-// perm[s] / top): thread = one slot and GATHER_PLANES consecutive planes
-// (one index load, then independent 16-byte loads); consecutive threads take
-// consecutive slots, so every plane's writes are contiguous and the grouped
-// gate/up GEMM then reads contiguous A rows. Scales and code sums follow their
-// rows.
-// ---------------------------------------------------------------------------
-constexpr int GATHER_PLANES = 2;
-
-struct GatherParams {
-    const int8_t* src;
-    const float* src_scale;
-    const int* src_sum;
-    int src_alloc;
-    const int* perm;
-    int top;
-    const int* counts;  // [0] slots used
-    int8_t* dst;
-    float* dst_scale;
-    int* dst_sum;
-    int dst_alloc;
-    int planes;
-};
-
-static __global__ __launch_bounds__(256) void moe_gather_kernel(GatherParams P) {
-    const int s = blockIdx.x * 256 + threadIdx.x;
-    const int p0 = blockIdx.y * GATHER_PLANES;
-    if (s >= P.counts[0]) return;
-    const int tok = P.perm[s] / P.top;
-    v4u v[GATHER_PLANES];
-#pragma unroll
-    for (int i = 0; i < GATHER_PLANES; ++i)
-        if (p0 + i < P.planes)
-            v[i] = *reinterpret_cast<const v4u*>(P.src + ((size_t)(p0 + i) * P.src_alloc + tok) * 16);
-#pragma unroll
-    for (int i = 0; i < GATHER_PLANES; ++i)
-        if (p0 + i < P.planes) *reinterpret_cast<v4u*>(P.dst + ((size_t)(p0 + i) * P.dst_alloc + s) * 16) = v[i];
-    if (blockIdx.y == 0) {
-        P.dst_scale[s] = P.src_scale[tok];
-        P.dst_sum[s] = P.src_sum[tok];
     }
 }
 

@@ -124,8 +124,20 @@ struct RowMax {
 };
 
 // Enqueue helpers (no synchronization).
+// Where a quantization writes its codes, row scales and code sums when not
+// into the workspace's own buffers (codes [K_pad/16][M_alloc][16]).
+struct QuantOut {
+    int8_t* codes;
+    float* rowscale;
+    int* rowsum;
+    int M_alloc;
+};
+// Quantizes `rows` rows of x (rows_dev: a device-side count <= rows). With
+// row_map, output row r quantizes input row row_map[r] / map_div (the MoE
+// slot order: slot r holds its assignment's token).
 int enqueue_quant(Workspace* ws, const void* x, int x_type, long lda, int rows, int rule, RowMax in_max,
-                  unsigned* rowmax_clear, hipStream_t s, const int* rows_dev = nullptr);
+                  unsigned* rowmax_clear, hipStream_t s, const int* rows_dev = nullptr, const int* row_map = nullptr,
+                  int map_div = 1, const QuantOut* out = nullptr);
 // A full dynamic-int8 linear from activations x: the GEMV quantizes inside
 // its blocks; the GEMM path quantizes with a separate kernel first. With a
 // SwiGLU+max epilogue, *out_max tells where the middle's row maxima are.
