@@ -745,8 +745,10 @@ def run_moe(torch, ctx, steps, warmup, tokens_list=(512, 1), want_cpu=True):
             res.update(value=round((routed_ops + shared_ops) / (ms * 1e-3) / 1e12, 2), unit="TOPS")
         else:
             res.update(value=round((routed_bytes + shared_bytes) / (ms * 1e-3) / 1e9, 1), unit="GB/s")
-        res["roofline"] = roof_of("hbm", f"MoE call T={T} (route, gather, grouped W4 gate_up + W8 down GEMMs, "
-                                         "combine) + shared FFN call", routed_bytes + shared_bytes, ms * 1e3,
+        parts = ("slot GEMVs W4 gate_up + W8 down, combine" if T == 1 else
+                 "route, quantization into slot order, grouped W4 gate_up + W8 down GEMMs, combine")
+        res["roofline"] = roof_of("hbm", f"MoE call T={T} ({parts}) + shared FFN call", routed_bytes + shared_bytes,
+                                  ms * 1e3,
                                   steps * (10 if T == 1 else 1),
                                   method="whole step (one MoE call + one shared FFN call), faster of eager and "
                                          "graph replay; HIP events")
@@ -1216,7 +1218,7 @@ PROFILE_SETUP = "  cd /tmp && export TMPDIR=/tmp && cd <repo>"
 
 def _last_json(path):
     for line in reversed(open(path).read().strip().splitlines()):
-        if line.strip().startswith("{"):
+        if line.strip()[:1] in ("{", "["):
             return json.loads(line)
     raise ValueError(f"{path}: no JSON line")
 
@@ -1279,7 +1281,7 @@ def _roof_passes(bench, roof):
          "hbm", P["qkv"]["us"], R["qkv"]["us"]),
         ("decode M=1 o 4096x2560 W4", [(["gemv_kernel<__half, 1, 4, 0,"], 81920)], lin_bytes(4, Q, H, 1), "hbm",
          P["o"]["us"], R["o"]["us"]),
-        ("decode M=1 gate_up 2560x19456 W4 +SwiGLU (the bench line's roofline kernel)",
+        ("decode M=1 gate_up 2560x19456 W4 +SwiGLU (roofline kernel)",
          [(["gemv_kernel<__half, 1, 4, 2,"], 389120)], lin_bytes(4, H, 2 * F, 1), "hbm", P["gate_up"]["us"],
          R["gate_up"]["us"]),
         ("decode M=1 down 9728x2560 W4 (second launch of the FFN call)",
@@ -1333,7 +1335,7 @@ def profile_roofline(bench_json, roof_json, trace_csv):
         out.append(f"{label[:62]:62} {mean:8.3f} {med:8.3f} {r_us:8.3f} {b_us:8.3f} {f_r:13.4f} {f_b:11.4f}")
         out.append("    " + " + ".join(f"{k[0]} grid {k[1]} x{len(groups[k])}" for k in keys)
                    + f"; work {work:.6g} {'B' if bound == 'hbm' else 'ops'} per call")
-    gu = next(v for k, v in fr.items() if "roofline kernel" in k)
+    gu = next(v for k, v in fr.items() if "(roofline kernel)" in k)
     out += ["", "Reading:",
             f"- The bench line's roofline kernel (decode gate_up GEMV): {gu[1]:.3f} us per launch back to back in a",
             f"  graph (frac {gu[3]:.4f}), {gu[0]:.3f} us per dispatch under the profiler (frac {gu[2]:.4f}). The profiler",
@@ -1410,24 +1412,26 @@ def profile_traffic(fetch_csv, write_csv):
 
 
 GEMM_ROLES = [
+    # (role, kernel, grid in work-items, o/down told apart by duration, ops,
+    #  wave tile in 32x32 fragments (FM, FN), W4)
     ("qkv 2560x6144 W8 (1536 tiles of 128x128)", "gemm_kernel<128, 128, 2, 2, 8, 0, true, 0>", 393216, None,
-     2.0 * 4096 * H * (Q + 2 * KV)),
-    ("o 4096x2560 W8 (160 tiles of 256x256)", "gemm_kernel<256, 256, 2, 4, 8, 0, true, 0>", 81920, "short",
-     2.0 * 4096 * Q * H),
+     2.0 * 4096 * H * (Q + 2 * KV), 2, 2, False),
+    ("o 4096x2560 W8 (220 tiles of 192x256)", "gemm_kernel<192, 256, 2, 4, 8, 0, true, 0>", 112640, "short",
+     2.0 * 4096 * Q * H, 3, 2, False),
     ("gate_up 2560x19456 W4 +SwiGLU (4864 tiles)", "gemm_kernel<128, 128, 2, 2, 4, 2, true, 0>", 1245184, None,
-     2.0 * 4096 * H * 2 * F),
-    ("down 9728x2560 W8 (160 tiles of 256x256)", "gemm_kernel<256, 256, 2, 4, 8, 0, true, 0>", 81920, "long",
-     2.0 * 4096 * F * H),
-    ("lm_head 2560x151936 W8 (9504 tiles)", "gemm_kernel<256, 256, 2, 4, 8, 0, true, 0>", 4866048, None,
-     2.0 * 4096 * H * VOCAB),
+     2.0 * 4096 * H * 2 * F, 2, 2, True),
+    ("down 9728x2560 W8 (220 tiles of 192x256)", "gemm_kernel<192, 256, 2, 4, 8, 0, true, 0>", 112640, "long",
+     2.0 * 4096 * F * H, 3, 2, False),
+    ("lm_head 2560x151936 W8 (9504 tiles of 256x256)", "gemm_kernel<256, 256, 2, 4, 8, 0, true, 0>", 4866048, None,
+     2.0 * 4096 * H * VOCAB, 4, 2, False),
 ]
 
+
 # LDS bytes read per MFMA (v_mfma_i32_32x32x32_i8: a 32x32 A fragment and a
-# 32x32 B fragment of one 32-k step) by tile: A 1 KB per row block, B 1 KB
-# (W8) or 0.5 KB (W4, packed) per column block, shared by the wave's MFMAs.
-def _lds_per_mfma(role):
-    fm, fn = (2, 2) if "128x128" in role or "4864" in role or "1536" in role else (4, 2)
-    w4 = "W4" in role
+# 32x32 B fragment of one 32-k step) for a wave tile of FM x FN fragments:
+# A 1 KB per row block, B 1 KB (W8) or 0.5 KB (W4, packed) per column block,
+# shared by the wave's FM * FN MFMAs.
+def _lds_per_mfma(fm, fn, w4):
     return (fm * 1024 + fn * (512 if w4 else 1024)) / (fm * fn)
 
 
@@ -1466,7 +1470,7 @@ def profile_gemm_counters(pmc1_csv, pmc2_csv, probes_json):
            "The o and down GEMMs share one kernel and grid; their dispatches are told apart by duration.", "",
            f"{'GEMM (role)':44} {'dur us':>7} {'GHz':>5} {'POP/s':>6} {'MFMA':>5} {'LDS util':>8} {'B/MFMA':>6} "
            f"{'WAIT_ANY':>8} {'WAIT_LDS':>8} {'confl':>6} {'VALU/wave':>9} {'LDS/wave':>8}"]
-    for label, sub, grid, split, ops in GEMM_ROLES:
+    for label, sub, grid, split, ops, fm, fn, w4 in GEMM_ROLES:
         k1, k2 = pick(r1, sub, grid, split), pick(r2, sub, grid, split)
         if not k1 or not k2:
             raise ValueError(f"{label}: no dispatches")
@@ -1478,7 +1482,7 @@ def profile_gemm_counters(pmc1_csv, pmc2_csv, probes_json):
         lds_act = med(r2, k2, "SQ_LDS_IDX_ACTIVE")
         out.append(f"{label:44} {dur:7.1f} {grbm / dur / 1e3:5.2f} {ops / (dur * 1e-6) / 1e15:6.2f} "
                    f"{med(r1, k1, 'SQ_VALU_MFMA_BUSY_CYCLES') / (grbm * 1024):5.3f} {lds_act / (grbm2 * 256):8.3f} "
-                   f"{_lds_per_mfma(label):6.0f} {med(r1, k1, 'SQ_WAIT_ANY') / wc:8.3f} "
+                   f"{_lds_per_mfma(fm, fn, w4):6.0f} {med(r1, k1, 'SQ_WAIT_ANY') / wc:8.3f} "
                    f"{med(r2, k2, 'SQ_WAIT_INST_LDS') / wc:8.3f} {med(r2, k2, 'SQ_LDS_BANK_CONFLICT') / lds_act:6.3f} "
                    f"{med(r2, k2, 'SQ_INSTS_VALU') / waves:9.0f} {med(r1, k1, 'SQ_INSTS_LDS') / waves:8.0f}")
         out.append(f"    {sub} grid {grid} wg {r1[k1[0]][3]} ({len(k1)} + {len(k2)} dispatches)")
@@ -1609,10 +1613,11 @@ def profile_moe(stats_csv, moe_json):
            "> moe.json",
            "  python3 bench.py --profile moe <out>/<host>/<pid>_run_kernel_stats.csv moe.json", "",
            "Workload: rk_npu_hip_moe_run at T=512 and T=1 tokens, steps of both sizes mixed in the table (eager and",
-           "graph replays). T=512: token quantization, device routing (counting sort of the (token, rank) slots),",
-           "gather into slot order, grouped gate_up GEMM + SwiGLU + row max over the ragged expert groups, middle",
-           "requantization, grouped down GEMM, combine; the shared expert as a dense FFN. T=1: slot GEMVs (slot =",
-           "assignment, no routing launch) for gate_up and down, the shared expert's GEMVs, combine.", ""]
+           "graph replays). T=512: device routing (counting sort of the (token, rank) slots), the tokens'",
+           "quantization written straight into slot order (one launch, rows through the routing's slot map),",
+           "grouped gate_up GEMM + SwiGLU + row max over the ragged expert groups, middle requantization, grouped",
+           "down GEMM, combine; the shared expert as a dense FFN. T=1: slot GEMVs (slot = assignment, no routing",
+           "launch) for gate_up and down, the shared expert's GEMVs, combine.", ""]
     out += _stats_table(stats_csv)
     out += ["", "bench.py --only moe in the same profiled run:"]
     for r in (res if isinstance(res, list) else [res]):
