@@ -925,6 +925,43 @@ def lds_probe(torch, LP, cur, iters=4096):
     return out
 
 
+LOAD_PROBE_SPANS = ((2 << 20, "2 MB (resident in each XCD's 4 MB L2)"),
+                    (32 << 20, "32 MB (beyond the L2: the last-level cache)"),
+                    (1 << 30, "1 GB (HBM)"))
+
+
+def load_probe(torch, LP, cur, iters=512):
+    """Global -> LDS load rate (rk_npu_hip_load_probe): every wave streams 1-KB
+    chunks into its own LDS ring through the LDS DMA load the GEMM ring uses,
+    8 loads in flight, from a source region resident in the L2, in the
+    last-level cache, or in HBM; bytes per shader-clock cycle per CU (median
+    block, times blocks per CU) and the aggregate rate over the launch."""
+    import ctypes
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+    out = []
+    for span, where in LOAD_PROBE_SPANS:
+        for threads, per_cu in ((512, 1), (256, 4)):
+            blocks = cus * per_cu
+            sink = torch.empty(blocks * threads // 64, dtype=torch.int32, device="cuda")
+            clocks = torch.empty(blocks * 2, dtype=torch.int64, device="cuda")
+            for _ in range(2):  # the first launch warms the caches and the clock
+                npu_check(LP.rk_npu_hip_load_probe(blocks, threads, 8, 1, ctypes.c_void_p(src.data_ptr()), span, iters,
+                                                   ctypes.c_void_p(sink.data_ptr()),
+                                                   ctypes.c_void_p(clocks.data_ptr()), cur()), "load probe")
+            torch.cuda.synchronize()
+            c = clocks.view(blocks, 2).cpu().tolist()
+            cyc = statistics.median(r[0] for r in c)
+            ticks_max = max(r[1] for r in c)
+            per_block = threads // 64 * iters * 1024
+            out.append({"span": span, "where": where, "threads": threads, "blocks_per_cu": per_cu,
+                        "bytes_per_clk_per_cu": round(per_block * per_cu / cyc, 1),
+                        "tb_s": round(per_block * blocks / (ticks_max / 100e6) / 1e12, 2)})
+            log(f"[probe] load {where} {threads}x{per_cu}/CU: {out[-1]}")
+    del src
+    return out
+
+
 def run_probes(torch, ctx, reps=20):
     """Ceilings measured on this GPU with the roofline probes of the
     measurement-only library libhip_probes.so (rk_npu_hip_mfma_probe,
@@ -950,6 +987,7 @@ def run_probes(torch, ctx, reps=20):
                                  "tops": round(ops / (ms * 1e-3) / 1e12, 1)})
         log(f"[probe] mfma blocks={blocks}: {res['mfma_int8'][-1]['tops']} TOPS")
     res["lds_read"] = lds_probe(torch, LP, cur)
+    res["load_rate"] = load_probe(torch, LP, cur)
     gen = Gen(torch, 1)
     t = DenseLayers(torch, ctx, gen, 1, (4, 4, 4, 4), tag="dec1")
     # per projection: (name, K, N, GEMV grid, GEMV threads per block)
@@ -1413,17 +1451,17 @@ def profile_traffic(fetch_csv, write_csv):
 
 GEMM_ROLES = [
     # (role, kernel, grid in work-items, o/down told apart by duration, ops,
-    #  wave tile in 32x32 fragments (FM, FN), W4)
+    #  wave tile in 32x32 fragments (FM, FN), W4, block tile (BM, BN))
     ("qkv 2560x6144 W8 (1536 tiles of 128x128)", "gemm_kernel<128, 128, 2, 2, 8, 0, true, 0>", 393216, None,
-     2.0 * 4096 * H * (Q + 2 * KV), 2, 2, False),
+     2.0 * 4096 * H * (Q + 2 * KV), 2, 2, False, 128, 128),
     ("o 4096x2560 W8 (220 tiles of 192x256)", "gemm_kernel<192, 256, 2, 4, 8, 0, true, 0>", 112640, "short",
-     2.0 * 4096 * Q * H, 3, 2, False),
+     2.0 * 4096 * Q * H, 3, 2, False, 192, 256),
     ("gate_up 2560x19456 W4 +SwiGLU (4864 tiles)", "gemm_kernel<128, 128, 2, 2, 4, 2, true, 0>", 1245184, None,
-     2.0 * 4096 * H * 2 * F, 2, 2, True),
+     2.0 * 4096 * H * 2 * F, 2, 2, True, 128, 128),
     ("down 9728x2560 W8 (220 tiles of 192x256)", "gemm_kernel<192, 256, 2, 4, 8, 0, true, 0>", 112640, "long",
-     2.0 * 4096 * F * H, 3, 2, False),
+     2.0 * 4096 * F * H, 3, 2, False, 192, 256),
     ("lm_head 2560x151936 W8 (9504 tiles of 256x256)", "gemm_kernel<256, 256, 2, 4, 8, 0, true, 0>", 4866048, None,
-     2.0 * 4096 * H * VOCAB, 4, 2, False),
+     2.0 * 4096 * H * VOCAB, 4, 2, False, 256, 256),
 ]
 
 
@@ -1468,9 +1506,11 @@ def profile_gemm_counters(pmc1_csv, pmc2_csv, probes_json):
            "  WAIT_ANY, WAIT_LDS = SQ_WAIT_ANY, SQ_WAIT_INST_LDS per SQ_WAVE_CYCLES; confl = SQ_LDS_BANK_CONFLICT /",
            "  SQ_LDS_IDX_ACTIVE; VALU/wave, LDS/wave = instructions per wave.",
            "The o and down GEMMs share one kernel and grid; their dispatches are told apart by duration.", "",
-           f"{'GEMM (role)':44} {'dur us':>7} {'GHz':>5} {'POP/s':>6} {'MFMA':>5} {'LDS util':>8} {'B/MFMA':>6} "
-           f"{'WAIT_ANY':>8} {'WAIT_LDS':>8} {'confl':>6} {'VALU/wave':>9} {'LDS/wave':>8}"]
-    for label, sub, grid, split, ops, fm, fn, w4 in GEMM_ROLES:
+           "  load B/clk/CU = the GEMM's stage loads (every tile's A and B bytes for every 64-k stage) per clock",
+           "  cycle per CU holding tiles (min(256, tiles)), at the clock of the same row.", "",
+           f"{'GEMM (role)':44} {'dur us':>7} {'GHz':>5} {'POP/s':>6} {'MFMA':>5} {'load':>5} {'LDS util':>8} "
+           f"{'B/MFMA':>6} {'WAIT_ANY':>8} {'WAIT_LDS':>8} {'confl':>6} {'VALU/wave':>9} {'LDS/wave':>8}"]
+    for label, sub, grid, split, ops, fm, fn, w4, bm, bn in GEMM_ROLES:
         k1, k2 = pick(r1, sub, grid, split), pick(r2, sub, grid, split)
         if not k1 or not k2:
             raise ValueError(f"{label}: no dispatches")
@@ -1480,8 +1520,12 @@ def profile_gemm_counters(pmc1_csv, pmc2_csv, probes_json):
         wc = med(r1, k1, "SQ_WAVE_CYCLES")
         waves = med(r1, k1, "SQ_WAVES")
         lds_act = med(r2, k2, "SQ_LDS_IDX_ACTIVE")
+        tiles = grid // r1[k1[0]][3]
+        load_bytes = ops / 2 * (1.0 / bn + (0.5 if w4 else 1.0) / bm)
+        load = load_bytes / (grbm * min(256, tiles))
         out.append(f"{label:44} {dur:7.1f} {grbm / dur / 1e3:5.2f} {ops / (dur * 1e-6) / 1e15:6.2f} "
-                   f"{med(r1, k1, 'SQ_VALU_MFMA_BUSY_CYCLES') / (grbm * 1024):5.3f} {lds_act / (grbm2 * 256):8.3f} "
+                   f"{med(r1, k1, 'SQ_VALU_MFMA_BUSY_CYCLES') / (grbm * 1024):5.3f} {load:5.1f} "
+                   f"{lds_act / (grbm2 * 256):8.3f} "
                    f"{_lds_per_mfma(fm, fn, w4):6.0f} {med(r1, k1, 'SQ_WAIT_ANY') / wc:8.3f} "
                    f"{med(r2, k2, 'SQ_WAIT_INST_LDS') / wc:8.3f} {med(r2, k2, 'SQ_LDS_BANK_CONFLICT') / lds_act:6.3f} "
                    f"{med(r2, k2, 'SQ_INSTS_VALU') / waves:9.0f} {med(r1, k1, 'SQ_INSTS_LDS') / waves:8.0f}")
@@ -1493,9 +1537,17 @@ def profile_gemm_counters(pmc1_csv, pmc2_csv, probes_json):
                 "LDS reads (conflict-free 16-byte, one block per CU) "
                 + ", ".join(f"{x['bytes_per_clk_per_cu']} B/clk/CU at {x['waves_per_cu']} waves/CU ({x['clock_ghz']} GHz)"
                             for x in probes.get("lds_read", [])) + "."]
+    lr = probes.get("load_rate", [])
+    if lr:
+        out += ["Global -> LDS loads (rk_npu_hip_load_probe, 8 in flight per wave), B/clk/CU: "
+                + "; ".join(f"{x['where'].split(' (')[0]} {x['bytes_per_clk_per_cu']} ({x['threads'] // 64} waves x "
+                            f"{x['blocks_per_cu']})" for x in lr) + " (sources resident in the L2, in the last-level "
+                "cache, in HBM)."]
     out += ["", "Reading: LDS utilisation stays at about a fifth of the cycles and the measured LDS read rate",
             f"({lds_peak} B/clk/CU) is several times what the tiles ask for; bank conflicts are a few percent. The",
-            "matrix cores idle on the rest: the per-stage barrier and the waits for each stage's loads."]
+            "matrix cores idle on the rest: the per-stage barrier and the waits for each stage's loads. The stage",
+            "loads arrive at a rate between the probe's L2-resident and last-level-cache rates: every stage waits",
+            "for its slowest load, and a stage's loads include L2 misses."]
     return "\n".join(out)
 
 
@@ -1518,6 +1570,13 @@ def profile_probes(probes_json):
             "flight); cycles and clock from the kernel's own s_memtime / s_memrealtime:"]
     for r in d.get("lds_read", []):
         out.append(f"    {r['waves_per_cu']} waves/CU: {r['bytes_per_clk_per_cu']} B/clk/CU at {r['clock_ghz']} GHz")
+    if d.get("load_rate"):
+        out += ["", "rk_npu_hip_load_probe: every wave streaming 1-KB chunks into its own LDS ring with the GEMM ring's",
+                "LDS DMA load (global_load_lds_dwordx4), 8 in flight, from a region of the given size (each wave",
+                "walking it from its own start); B/clk/CU from the kernel's cycle counts, TB/s over the launch:"]
+        for r in d["load_rate"]:
+            out.append(f"    {r['where']:46} {r['threads'] // 64} waves x {r['blocks_per_cu']} blocks/CU: "
+                       f"{r['bytes_per_clk_per_cu']:6.1f} B/clk/CU {r['tb_s']:6.2f} TB/s")
     out += ["", "rk_npu_hip_stream_probe: one launch reading each projection's weight bytes (36 distinct buffers in",
             "a graph, so every read comes from HBM) with the GEMV's 16-byte non-temporal loads, at several grids;",
             "'empty' is the same grid with no loads (the launch's fixed cost); the projection's own GEMV launch",

@@ -362,6 +362,8 @@ PROBE_SIGNATURES = {
     "rk_npu_hip_mfma_probe": (c_int, [c_int, c_int, c_void_p, c_void_p]),
     "rk_npu_hip_lds_probe": (c_int, [c_int, c_int, c_int, c_void_p, c_void_p, c_void_p]),
     "rk_npu_hip_wave_place_probe": (c_int, [c_int, c_int, c_void_p, c_void_p]),
+    "rk_npu_hip_load_probe": (c_int, [c_int, c_int, c_int, c_int, c_void_p, c_uint64, c_int, c_void_p, c_void_p,
+                                      c_void_p]),
 }
 
 RECLAIM_CALLBACK = ctypes.CFUNCTYPE(None, c_void_p)

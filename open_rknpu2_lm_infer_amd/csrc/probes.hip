@@ -14,6 +14,13 @@
 //     `blocks` x `threads` threads with 64 KB of LDS each, every wave reading
 //     iters x 8 KB from LDS; sink holds one uint32 per wave, clocks two
 //     uint64 per block (shader-clock cycles, 100 MHz ticks of the loop).
+//   rk_npu_hip_load_probe(blocks, threads, depth, to_lds, src, span, iters,
+//     sink, clocks, stream): every wave of `blocks` x `threads` threads
+//     streams `iters` 1-KB chunks (16 bytes per lane) of a `span`-byte source
+//     region, keeping `depth` (4, 8 or 16) loads in flight: into LDS through
+//     the LDS DMA load the GEMM ring uses (global_load_lds_dwordx4, to_lds =
+//     1; waves x depth KB of LDS) or into registers (0; depth-load batches);
+//     clocks two uint64 per block as above, sink one uint32 per wave.
 //   rk_npu_hip_wave_place_probe(blocks, threads, out, stream): every wave
 //     of `blocks` x `threads` stores its hardware id register (SIMD, CU) at
 //     out[block * waves + wave].
@@ -125,6 +132,58 @@ __global__ __launch_bounds__(512) void lds_probe_kernel(int iters, unsigned* __r
     }
 }
 
+// Global -> LDS (or register) load rate: wave w of block b starts at chunk
+// (b * waves + w) * 613 of the region and walks it chunk by chunk, wrapping
+// at its end. The LDS path keeps DEPTH DMA loads in flight (each wave its
+// own DEPTH-slot ring of 1-KB slots, slot i % DEPTH); the register path
+// issues DEPTH loads, then folds them into an xor that is stored.
+template <int DEPTH, bool TO_LDS>
+__global__ __launch_bounds__(512) void load_probe_kernel(const uint8_t* __restrict__ src, size_t span_chunks,
+                                                         int iters, unsigned* __restrict__ sink,
+                                                         unsigned long long* __restrict__ clocks) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds_ring[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
+    size_t c = ((size_t)blockIdx.x * waves + wave) * 613 % span_chunks;
+    uint8_t* ring = lds_ring + (size_t)wave * DEPTH * 1024;
+    v4u x = {0u, 0u, 0u, 0u};
+    const unsigned long long c0 = __builtin_amdgcn_s_memtime();
+    const unsigned long long r0 = __builtin_amdgcn_s_memrealtime();
+    if constexpr (TO_LDS) {
+        for (int i = 0; i < iters; ++i) {
+            __builtin_amdgcn_global_load_lds(src + c * 1024 + lane * 16,
+                                             (__attribute__((address_space(3))) void*)(ring + (i % DEPTH) * 1024), 16,
+                                             0, 0);
+            c = (c + 1 == span_chunks) ? 0 : c + 1;
+            // (vmcnt: bits 3:0 and 15:14; expcnt and lgkmcnt at their maxima)
+            __builtin_amdgcn_s_waitcnt(((DEPTH - 1) & 15) | (((DEPTH - 1) >> 4) << 14) | (7 << 4) | (15 << 8));
+        }
+        __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));  // vmcnt(0)
+        __syncthreads();
+        x = *reinterpret_cast<const v4u*>(ring + lane * 16);
+    } else {
+        for (int i = 0; i < iters; i += DEPTH) {
+            v4u r[DEPTH];
+#pragma unroll
+            for (int j = 0; j < DEPTH; ++j) {
+                r[j] = *reinterpret_cast<const v4u*>(src + c * 1024 + lane * 16);
+                c = (c + 1 == span_chunks) ? 0 : c + 1;
+            }
+#pragma unroll
+            for (int j = 0; j < DEPTH; ++j) x ^= r[j];
+        }
+    }
+    const unsigned long long c1 = __builtin_amdgcn_s_memtime();
+    const unsigned long long r1 = __builtin_amdgcn_s_memrealtime();
+    unsigned y = x.x ^ x.y ^ x.z ^ x.w;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) y ^= __shfl_xor(y, off);
+    if (lane == 0) sink[(size_t)blockIdx.x * waves + wave] = y;
+    if (threadIdx.x == 0) {
+        clocks[2 * blockIdx.x] = c1 - c0;
+        clocks[2 * blockIdx.x + 1] = r1 - r0;
+    }
+}
+
 // Where the waves of a block run: wave w of block b stores the hardware id
 // register (HW_REG_HW_ID: bits 3:0 wave slot, 5:4 SIMD, 11:8 CU, 15:13 shader
 // engine) at out[b * waves + w].
@@ -161,6 +220,33 @@ int rk_npu_hip_lds_probe(int blocks, int threads, int iters, uint32_t* sink, uin
         return RK_NPU_ERR_PARAM;
     hipLaunchKernelGGL(lds_probe_kernel, dim3(blocks), dim3(threads), 65536, static_cast<hipStream_t>(stream), iters,
                        sink, reinterpret_cast<unsigned long long*>(clocks));
+    return hipGetLastError() == hipSuccess ? RK_NPU_OK : RK_NPU_ERR_DEVICE;
+}
+
+int rk_npu_hip_load_probe(int blocks, int threads, int depth, int to_lds, const void* src, uint64_t span, int iters,
+                          uint32_t* sink, uint64_t* clocks, void* stream) {
+    if (blocks < 1 || blocks > (1 << 20) || threads < 64 || threads > 512 || threads % 64 != 0 || iters < 1 ||
+        (depth != 4 && depth != 8 && depth != 16) || iters % depth != 0 || !src || span < 1024 || !sink || !clocks ||
+        (reinterpret_cast<uintptr_t>(src) & 15) != 0)
+        return RK_NPU_ERR_PARAM;
+    const size_t lds = to_lds ? (size_t)(threads / 64) * depth * 1024 : 0;
+    if (lds > 160 * 1024) return RK_NPU_ERR_PARAM;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    const uint8_t* p = static_cast<const uint8_t*>(src);
+    const size_t chunks = span / 1024;
+    unsigned long long* ck = reinterpret_cast<unsigned long long*>(clocks);
+#define HM_LOAD_PROBE(D, L) \
+    hipLaunchKernelGGL((load_probe_kernel<D, L>), dim3(blocks), dim3(threads), lds, s, p, chunks, iters, sink, ck)
+    if (to_lds) {
+        if (depth == 4) HM_LOAD_PROBE(4, true);
+        else if (depth == 8) HM_LOAD_PROBE(8, true);
+        else HM_LOAD_PROBE(16, true);
+    } else {
+        if (depth == 4) HM_LOAD_PROBE(4, false);
+        else if (depth == 8) HM_LOAD_PROBE(8, false);
+        else HM_LOAD_PROBE(16, false);
+    }
+#undef HM_LOAD_PROBE
     return hipGetLastError() == hipSuccess ? RK_NPU_OK : RK_NPU_ERR_DEVICE;
 }
 
