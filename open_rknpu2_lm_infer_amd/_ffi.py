@@ -360,6 +360,7 @@ PROBE_LIB_PATH = os.path.join(PKG_DIR, "libhip_probes.so")
 PROBE_SIGNATURES = {
     "rk_npu_hip_stream_probe": (c_int, [c_void_p, c_uint64, c_int, c_int, c_int, c_void_p, c_void_p]),
     "rk_npu_hip_mfma_probe": (c_int, [c_int, c_int, c_void_p, c_void_p]),
+    "rk_npu_hip_mfma_rand_probe": (c_int, [c_int, c_int, c_void_p, c_void_p]),
     "rk_npu_hip_lds_probe": (c_int, [c_int, c_int, c_int, c_void_p, c_void_p, c_void_p]),
     "rk_npu_hip_wave_place_probe": (c_int, [c_int, c_int, c_void_p, c_void_p]),
     "rk_npu_hip_load_probe": (c_int, [c_int, c_int, c_int, c_int, c_void_p, c_uint64, c_int, c_void_p, c_void_p,

@@ -9,7 +9,8 @@
 //     threads; sink holds one uint32 per block;
 //   rk_npu_hip_mfma_probe(blocks, iters, sink, stream): `blocks` x 256
 //     threads, each wave `iters` rounds of 8 MFMAs (65536 int8 ops each);
-//     sink holds one int32 per thread.
+//     sink holds one int32 per thread. rk_npu_hip_mfma_rand_probe: the same
+//     with full-range operand bytes, a different operand pair per MFMA.
 //   rk_npu_hip_lds_probe(blocks, threads, iters, sink, clocks, stream):
 //     `blocks` x `threads` threads with 64 KB of LDS each, every wave reading
 //     iters x 8 KB from LDS; sink holds one uint32 per wave, clocks two
@@ -76,7 +77,20 @@ __global__ __launch_bounds__(512) void stream_probe_kernel(const v4u* __restrict
 }
 
 // Each wave keeps 8 independent 32x32 int32 accumulators and issues
-// `iters` rounds of 8 MFMAs on operands held in registers.
+// `iters` rounds of 8 MFMAs on operands held in registers: one operand pair
+// of small values (mostly zero bytes) for every MFMA, or (RND) eight pairs of
+// hashed, full-range bytes, a different pair for each MFMA of a round, as the
+// fragments of a GEMM on real data are (the datapath's switching, and with it
+// the power the chip draws, depends on the operand bits).
+__device__ __forceinline__ int probe_hash(unsigned x) {
+    x ^= x >> 16;
+    x *= 0x7feb352dU;
+    x ^= x >> 15;
+    x *= 0x846ca68bU;
+    x ^= x >> 16;
+    return (int)x;
+}
+template <bool RND>
 __global__ __launch_bounds__(256) void mfma_probe_kernel(int iters, int* __restrict__ sink) {
     v16i acc[8];
 #pragma unroll
@@ -84,10 +98,18 @@ __global__ __launch_bounds__(256) void mfma_probe_kernel(int iters, int* __restr
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[j][r] = 0;
     const int t = threadIdx.x;
-    v4i a = {t, t + 1, t + 2, t + 3}, b = {t ^ 5, t ^ 6, t ^ 7, t ^ 9};
+    v4i a[8], b[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const unsigned seed = (blockIdx.x * 256u + t) * 64u + 8u * j;
+        a[j] = RND ? v4i{probe_hash(seed), probe_hash(seed + 1), probe_hash(seed + 2), probe_hash(seed + 3)}
+                   : v4i{t, t + 1, t + 2, t + 3};
+        b[j] = RND ? v4i{probe_hash(seed + 4), probe_hash(seed + 5), probe_hash(seed + 6), probe_hash(seed + 7)}
+                   : v4i{t ^ 5, t ^ 6, t ^ 7, t ^ 9};
+    }
     for (int it = 0; it < iters; ++it) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, acc[j], 0, 0, 0);
+        for (int j = 0; j < 8; ++j) acc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[j], b[j], acc[j], 0, 0, 0);
     }
     int s = 0;
 #pragma unroll
@@ -210,7 +232,15 @@ int rk_npu_hip_stream_probe(const void* src, uint64_t bytes, int blocks, int thr
 
 int rk_npu_hip_mfma_probe(int blocks, int iters, int32_t* sink, void* stream) {
     if (blocks < 1 || blocks > (1 << 20) || iters < 1 || !sink) return RK_NPU_ERR_PARAM;
-    hipLaunchKernelGGL(mfma_probe_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream), iters, sink);
+    hipLaunchKernelGGL(mfma_probe_kernel<false>, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream), iters,
+                       sink);
+    return hipGetLastError() == hipSuccess ? RK_NPU_OK : RK_NPU_ERR_DEVICE;
+}
+
+int rk_npu_hip_mfma_rand_probe(int blocks, int iters, int32_t* sink, void* stream) {
+    if (blocks < 1 || blocks > (1 << 20) || iters < 1 || !sink) return RK_NPU_ERR_PARAM;
+    hipLaunchKernelGGL(mfma_probe_kernel<true>, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream), iters,
+                       sink);
     return hipGetLastError() == hipSuccess ? RK_NPU_OK : RK_NPU_ERR_DEVICE;
 }
 
