@@ -1,8 +1,7 @@
 """Oracle parity at the benchmarked shapes themselves (Qwen3-4B and the
-35B-A3B-class MoE): each case runs the GPU path at its real size and checks it
-bit for bit against the oracle (all rows where the oracle takes seconds,
-sampled rows where it would take minutes; rows are independent, since
-quantization, products and epilogues act row by row).
+35B-A3B-class MoE): each case runs the GPU path at its real size and checks
+every row bit for bit against the oracle (the C oracle with OpenMP takes
+seconds even for the 4096 x 151936 lm_head).
 
 - W8A8 linear M128 K2560 N9728 with outlier channels, through the reference's
   host-buffer signature rk_npu_f32i8f32_run_dynamic (src/npu.rs:1412-1417)
@@ -10,9 +9,9 @@ quantization, products and epilogues act row by row).
 - Decode M=1 and M=4 W4A8: qkv 2560->6144, o 4096->2560, and the fused
   gate_up 2560->19456 + SwiGLU -> requant -> down 9728->2560 (the split-K
   one-row GEMV and the quantization wave at M=1).
-- Prefill M=4096: qkv/o W8A8, gate_up W4A8 + SwiGLU -> down W8A8, and the
-  2560->151936 W8 lm_head (the 256x256 tile with its last 128 columns
-  padded), rows 0, tile edges and 4095.
+- Prefill M=4096: qkv/o W8A8 (128x128 and 192x256 tiles), gate_up W4A8 +
+  SwiGLU -> down W8A8, and the 2560->151936 W8 lm_head (the 256x256 tile
+  with its last 128 columns padded), all 4096 rows.
 - MoE T=1: hidden 2048, 128 experts, top-8, I=768, W4 gate_up + W8 down, and
   the shared W8 FFN of intermediate 2048."""
 import ctypes
@@ -31,7 +30,6 @@ pytestmark = pytest.mark.gpu
 torch = pytest.importorskip("torch")
 
 H, Q, KV, FF, VOCAB = 2560, 4096, 1024, 9728, 151936
-SAMPLE_4096 = np.array([0, 1, 127, 128, 255, 256, 1023, 1024, 2047, 2048, 3071, 4095])
 
 
 @pytest.fixture(scope="module")
@@ -94,7 +92,6 @@ def test_decode_projection_set_w4a8(ctx, rows):
 
 def test_prefill_m4096_projection_set(ctx):
     rows = 4096
-    s = SAMPLE_4096
     for name, bits, k, n in (("qkv", 8, H, Q + 2 * KV), ("o", 8, Q, H)):
         print(f"prefill M=4096 {name} {k}x{n} W{bits}", flush=True)
         codes, scales = R.weights(3, f"cfg3-{name}", bits, k, n)
@@ -103,8 +100,7 @@ def test_prefill_m4096_projection_set(ctx):
         y = torch.empty(rows, n, dtype=torch.float16, device="cuda")
         D.linear(ctx, w, dev(x).half(), y, rows)
         torch.cuda.synchronize()
-        got = y[torch.from_numpy(s).cuda()].cpu().numpy()
-        assert np.array_equal(got, oracle.linear(codes, scales, x[s]).astype(np.float16))
+        assert np.array_equal(y.cpu().numpy(), oracle.linear(codes, scales, x).astype(np.float16))
         del w, y
     print("prefill M=4096 FFN gate_up W4 2560x19456 + SwiGLU -> down W8 9728x2560", flush=True)
     gc, gs = R.weights(3, "cfg3-gu", 4, H, 2 * FF)
@@ -117,10 +113,9 @@ def test_prefill_m4096_projection_set(ctx):
     m = torch.empty(rows, FF, dtype=torch.float16, device="cuda")
     D.linear(ctx, gu, xd, m, rows, swiglu=True)
     torch.cuda.synchronize()
-    idx = torch.from_numpy(s).cuda()
-    want, mid = oracle.ffn(gc, gs, dc, ds, x[s], with_middle=True)
-    assert np.array_equal(y[idx].cpu().numpy(), want.astype(np.float16))
-    assert np.array_equal(m[idx].cpu().numpy(), mid.astype(np.float16))
+    want, mid = oracle.ffn(gc, gs, dc, ds, x, with_middle=True)
+    assert np.array_equal(y.cpu().numpy(), want.astype(np.float16))
+    assert np.array_equal(m.cpu().numpy(), mid.astype(np.float16))
 
 
 def test_prefill_m4096_lm_head(ctx):
@@ -135,9 +130,10 @@ def test_prefill_m4096_lm_head(ctx):
     y = torch.empty(rows, VOCAB, dtype=torch.float16, device="cuda")
     D.linear(ctx, w, dev(x).half(), y, rows)
     torch.cuda.synchronize()
-    s = SAMPLE_4096
-    got = y[torch.from_numpy(s).cuda()].cpu().numpy()
-    assert np.array_equal(got, oracle.linear(codes, scales, x[s]).astype(np.float16))
+    got = y.cpu().numpy()
+    del y, w
+    for r0 in range(0, rows, 1024):  # (the oracle's f32 output in slices of 1024 rows: 0.6 GB each)
+        assert np.array_equal(got[r0:r0 + 1024], oracle.linear(codes, scales, x[r0:r0 + 1024]).astype(np.float16))
 
 
 def test_moe_35b_a3b_t1_with_shared_ffn():
