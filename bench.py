@@ -1653,6 +1653,14 @@ def profile_gemm_counters(pmc1_csv, pmc2_csv, probes_json):
                 "LDS reads (conflict-free 16-byte, one block per CU) "
                 + ", ".join(f"{x['bytes_per_clk_per_cu']} B/clk/CU at {x['waves_per_cu']} waves/CU ({x['clock_ghz']} GHz)"
                             for x in probes.get("lds_read", [])) + "."]
+    rnd = probes.get("mfma_int8_random", [])
+    if rnd:
+        out += ["int8 MFMA from registers on random operand bytes (the bit activity of real data): "
+                + ", ".join(f"{x['tops'] / 1000:.2f} POP/s at {x['waves_per_simd']} waves/SIMD" for x in rnd)
+                + " (the clock lowered by the board's power management)."]
+    for r in probes.get("power", []):
+        if r.get("tops"):
+            out += [f"Power, {r['phase']}: {r['watts']:.0f} W at {r['sclk_mhz']} MHz ({r['tops'] / 1000:.2f} POP/s)."]
     lr = probes.get("load_rate", [])
     if lr:
         out += ["Global -> LDS loads (rk_npu_hip_load_probe, 8 in flight per wave), B/clk/CU: "
