@@ -68,7 +68,7 @@ struct MoeWork {
     int* counts;
     unsigned* error;
     float* out;
-    int8_t* gcodes;   // token codes gathered into slot order [h_pad/16][g_alloc][16]
+    int8_t* gcodes;   // token codes quantized in slot order [h_pad/16][g_alloc][16]
     float* gscale;    // [g_alloc]
     int* gsum;        // [g_alloc]
     int g_alloc;
@@ -221,7 +221,7 @@ static MoeWork* work_create(Domain* d, const rk_npu_moe_w8_config* cfg) {
         ws->sgws = workspace_create(d, 8, cfg->max_rows, w.hidden, 2 * w.intermediate);
         ws->sdws = workspace_create(d, 8, cfg->max_rows, w.intermediate, w.hidden);
     }
-    // ids | routes | pos | perm | tiles | counts | error | out | gathered codes | scales | sums
+    // ids | routes | pos | perm | tiles | counts | error | out | slot-order codes | scales | sums
     const size_t sz_a = round_up_z((size_t)A * 4, 256);
     const size_t sz_tiles = round_up_z((size_t)A * 16, 256);
     const size_t sz_out = round_up_z((size_t)cfg->max_rows * w.hidden * 4, 256);
@@ -360,9 +360,9 @@ static int enqueue_moe(MoeWork* ws, const MoeBank* b, int rows, const float* inp
     // and a gather of its codes (measured at 4096 slots: gate/up 69 -> 57 us
     // with contiguous rows). Few slots: the tokens are quantized once and the
     // GEMM gathers rows itself.
-    const bool gather = !slot_gemv && A >= 256;
+    const bool slot_order = !slot_gemv && A >= 256;
     int rc = RK_NPU_OK;
-    if (!slot_quant && !gather) {
+    if (!slot_quant && !slot_order) {
         rc = enqueue_quant(ws->xws, input, DT_F32, ws->h, rows, QUANT_MOE, RowMax{nullptr, 0}, nullptr, s);
         if (rc != RK_NPU_OK) return rc;
     }
@@ -458,7 +458,7 @@ static int enqueue_moe(MoeWork* ws, const MoeBank* b, int rows, const float* inp
     // one partial tile per expert.
     const int max_tiles = std::min(A, (A + std::min(A, ws->experts) * (MOE_BM - 1)) / MOE_BM);
 
-    if (gather) {
+    if (slot_order) {
         const QuantOut q{ws->gcodes, ws->gscale, ws->gsum, ws->g_alloc};
         rc = enqueue_quant(ws->xws, input, DT_F32, ws->h, A, QUANT_MOE, RowMax{nullptr, 0}, nullptr, s, ws->counts,
                            ws->perm, ws->top, &q);
@@ -467,12 +467,12 @@ static int enqueue_moe(MoeWork* ws, const MoeBank* b, int rows, const float* inp
 
     if (!slot_gemv) {
     MoeGemmParams G;
-    G.a = gather ? ws->gcodes : ws->xws->codes;
-    G.a_alloc = gather ? ws->g_alloc : ws->xws->M_alloc;
-    G.perm = gather ? nullptr : ws->perm;
+    G.a = slot_order ? ws->gcodes : ws->xws->codes;
+    G.a_alloc = slot_order ? ws->g_alloc : ws->xws->M_alloc;
+    G.perm = slot_order ? nullptr : ws->perm;
     G.top = ws->top;
-    G.rowscale = gather ? ws->gscale : ws->xws->rowscale;
-    G.rowsum = gather ? ws->gsum : ws->xws->rowsum;
+    G.rowscale = slot_order ? ws->gscale : ws->xws->rowscale;
+    G.rowsum = slot_order ? ws->gsum : ws->xws->rowsum;
     G.b_tab = b->d_gu;
     G.s_tab = b->d_gus;
     G.tiles = ws->tiles;
