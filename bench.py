@@ -358,6 +358,27 @@ def decode_passes(torch, ctx, t, reps):
     return out
 
 
+def stream_read_us(torch, nbytes, reps=20, blocks=2048, threads=256):
+    """One launch reading `nbytes` of device memory with the GEMV's 16-byte
+    non-temporal loads (rk_npu_hip_stream_probe), on 36 distinct buffers
+    launched back to back in a graph (so every read comes from HBM): average
+    microseconds per launch."""
+    import ctypes
+    from open_rknpu2_lm_infer_amd import _ffi as FFI
+    LP = FFI.probe_lib()
+    bufs = [torch.empty(nbytes, dtype=torch.uint8, device="cuda") for _ in range(LAYERS)]
+    sink = torch.empty(blocks, dtype=torch.int32, device="cuda")
+
+    def fn():
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        for b in bufs:
+            npu_check(LP.rk_npu_hip_stream_probe(ctypes.c_void_p(b.data_ptr()), nbytes, blocks, threads, 1,
+                                                 ctypes.c_void_p(sink.data_ptr()), st), "stream probe")
+    ms, _ = graph_time(torch, fn, reps)
+    del bufs
+    return ms * 1e3 / LAYERS
+
+
 def run_decode(torch, ctx, rows, steps, warmup, want_cpu, want_roofline=True, timed=True, reps=None):
     gen = Gen(torch, 1)
     log(f"[bench] decode M={rows}: creating 36 layers of W4 weights")
@@ -381,6 +402,15 @@ def run_decode(torch, ctx, rows, steps, warmup, want_cpu, want_roofline=True, ti
         out["roofline"] = roof_of("hbm", f"gemv_kernel (W4, SwiGLU epilogue) gate_up 2560x19456, M={rows}",
                                   gu["bytes"], gu["us"], LAYERS * (reps or steps),
                                   traffic=TRAFFIC_GEMV_GATE_UP.get(rows))
+        # The measured ceiling of one launch of this size: a plain read of the
+        # same bytes with the same loads, launched the same way.
+        read_us = stream_read_us(torch, gu["bytes"])
+        ceil = gu["bytes"] / (read_us * 1e-6) / 1e9
+        out["roofline"]["measured_ceiling"] = {
+            "value": round(ceil, 1), "unit": "GB/s", "frac": round(out["roofline"]["achieved"] / ceil, 4),
+            "us": round(read_us, 3),
+            "what": "one launch reading the same bytes with the GEMV's 16-byte non-temporal loads "
+                    "(rk_npu_hip_stream_probe, 2048 x 256 threads), 36 distinct buffers back to back in a graph"}
         log(f"[bench] decode M={rows} projections: {passes}")
         log(f"[bench] decode roofline: {out['roofline']}")
     if want_cpu:
