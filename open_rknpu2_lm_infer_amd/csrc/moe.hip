@@ -373,7 +373,6 @@ static int enqueue_moe(MoeWork* ws, const MoeBank* b, int rows, const float* inp
     R.rows = rows;
     R.top = ws->top;
     R.experts = ws->experts;
-    R.bm = MOE_BM;
     R.pos = ws->pos;
     R.perm = ws->perm;
     R.tiles = ws->tiles;
@@ -381,7 +380,7 @@ static int enqueue_moe(MoeWork* ws, const MoeBank* b, int rows, const float* inp
     R.rowmax_mid = ws->mws->rowmax;
     R.rowmax_count = A;
     R.error = ws->error;
-    hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(1024), 0, s, R);
+    hipLaunchKernelGGL(moe_route_kernel<MOE_BM>, dim3(1), dim3(1024), 0, s, R);
     }
 
     if (slot_gemv) {

@@ -13,14 +13,14 @@ constexpr int MOE_MAX_EXPERTS = 512;
 // route <= 0 are skipped (they contribute nothing to the combine); an expert id
 // outside [0, experts) raises the error flag and is skipped as well. Each
 // expert's assignments get a contiguous run of slots; every run is cut into
-// m-tiles of `bm` slots for the grouped GEMM. Within a run the slot order is
+// m-tiles of BM slots for the grouped GEMM. Within a run the slot order is
 // arbitrary: every slot is computed independently and the combine reads
 // slots through pos[] in rank order, so results do not depend on it.
 // ---------------------------------------------------------------------------
 struct RouteParams {
     const int* ids;
     const float* routes;
-    int rows, top, experts, bm;
+    int rows, top, experts;
     int* pos;       // [rows*top] slot or -1
     int* perm;      // [rows*top] slot -> assignment
     int4* tiles;    // [max_tiles] {expert, slot_begin, slot_end, 0}
@@ -30,7 +30,8 @@ struct RouteParams {
     unsigned* error;
 };
 
-static __global__ __launch_bounds__(1024) void moe_route_kernel(RouteParams P) {
+template <int BM>
+__global__ __launch_bounds__(1024) void moe_route_kernel(RouteParams P) {
     __shared__ int cnt[MOE_MAX_EXPERTS];
     __shared__ int fill[MOE_MAX_EXPERTS];
     __shared__ int off[MOE_MAX_EXPERTS];
@@ -43,21 +44,36 @@ static __global__ __launch_bounds__(1024) void moe_route_kernel(RouteParams P) {
     }
     for (int i = tid; i < P.rowmax_count; i += 1024) P.rowmax_mid[i] = 0u;
     __syncthreads();
-    // Each thread's first RC assignments stay in registers for the second
-    // pass (the expert, or -1 for a skipped route); the rest are read again.
+    // Each thread's first RC assignments are requested at once (one memory
+    // round trip instead of one per assignment; indices past A re-read the
+    // last assignment and are masked) and their experts stay in registers
+    // for the second pass (-1 for a skipped route); later ones are read again.
     constexpr int RC = 8;
-    int ce[RC];
+    int ce[RC], idv[RC];
+    float rv[RC];
 #pragma unroll
-    for (int i = 0; i < RC; ++i) ce[i] = -1;
-    for (int a = tid, i = 0; a < A; a += 1024, ++i) {
+    for (int i = 0; i < RC; ++i) {
+        const int a = min(tid + 1024 * i, A - 1);
+        idv[i] = P.ids[a];
+        rv[i] = P.routes[a];
+    }
+#pragma unroll
+    for (int i = 0; i < RC; ++i) {
+        ce[i] = -1;
+        if (tid + 1024 * i < A) {
+            const int e = idv[i];
+            const bool in_range = e >= 0 && e < P.experts;
+            if (!in_range) atomicOr(P.error, 1u);
+            const bool live = in_range && rv[i] > 0.0f;
+            if (live) atomicAdd(&cnt[e], 1);
+            ce[i] = live ? e : -1;
+        }
+    }
+    for (int a = tid + 1024 * RC; a < A; a += 1024) {
         const int e = P.ids[a];
         const bool in_range = e >= 0 && e < P.experts;
         if (!in_range) atomicOr(P.error, 1u);
-        const bool live = in_range && P.routes[a] > 0.0f;
-        if (live) atomicAdd(&cnt[e], 1);
-#pragma unroll
-        for (int j = 0; j < RC; ++j)
-            if (i == j) ce[j] = live ? e : -1;
+        if (in_range && P.routes[a] > 0.0f) atomicAdd(&cnt[e], 1);
     }
     __syncthreads();
     // Exclusive prefix sums of slots and tiles over the experts: wave 0, each
@@ -70,7 +86,7 @@ static __global__ __launch_bounds__(1024) void moe_route_kernel(RouteParams P) {
             const int e = tid * PER + i;
             const int c = e < P.experts ? cnt[e] : 0;
             ls += c;
-            lt += (c + P.bm - 1) / P.bm;
+            lt += (c + BM - 1) / BM;
         }
         int is = ls, it = lt;  // inclusive scans over lanes
 #pragma unroll
@@ -89,7 +105,7 @@ static __global__ __launch_bounds__(1024) void moe_route_kernel(RouteParams P) {
                 off[e] = run;
                 toff[e] = tiles;
                 run += cnt[e];
-                tiles += (cnt[e] + P.bm - 1) / P.bm;
+                tiles += (cnt[e] + BM - 1) / BM;
             }
         }
         if (tid == 63) {
@@ -116,10 +132,10 @@ static __global__ __launch_bounds__(1024) void moe_route_kernel(RouteParams P) {
         P.pos[a] = slot;
     }
     for (int e = tid; e < P.experts; e += 1024) {
-        const int n = (cnt[e] + P.bm - 1) / P.bm;
+        const int n = (cnt[e] + BM - 1) / BM;
         for (int t = 0; t < n; ++t) {
-            const int b = off[e] + t * P.bm;
-            P.tiles[toff[e] + t] = make_int4(e, b, min(off[e] + cnt[e], b + P.bm), 0);
+            const int b = off[e] + t * BM;
+            P.tiles[toff[e] + t] = make_int4(e, b, min(off[e] + cnt[e], b + BM), 0);
         }
     }
 }
