@@ -1205,6 +1205,19 @@ def run_probes(torch, ctx, reps=20):
         res["hbm_read_step_volume"][f"{blocks}x{thr}"] = {"ms": round(ms, 4), "gbs": round(big.numel() / ms / 1e6, 1)}
     log(f"[probe] one launch over the step's bytes: {res['hbm_read_step_volume']}")
     del big
+    # The fixed cost of a launch against its grid: 36 launches of a kernel
+    # that loads nothing, back to back in a graph (the decode GEMVs launch
+    # 640-1280 blocks).
+    res["launch_cost"] = []
+    for blocks, thr in ((1, 64), (8, 256), (64, 256), (256, 256), (640, 256), (1280, 256), (2560, 256),
+                        (5120, 256)):
+        def fn():
+            for _ in range(LAYERS):
+                npu_check(LP.rk_npu_hip_stream_probe(ctypes.c_void_p(sinkb.data_ptr()), 0, blocks, thr, 0,
+                                                    ctypes.c_void_p(sinkb.data_ptr()), cur()), "stream probe")
+        ms, _ = graph_time(torch, fn, reps)
+        res["launch_cost"].append({"blocks": blocks, "threads": thr, "us": round(ms * 1e3 / LAYERS, 3)})
+    log(f"[probe] empty launches in a graph: {res['launch_cost']}")
     res["moe_t1_shared_in_bank"] = moe_shared_bank_t1(torch, ctx, reps * 10)
     log(f"[probe] MoE T=1 with the shared expert in the bank: {res['moe_t1_shared_in_bank']}")
     return res
@@ -1771,6 +1784,10 @@ def profile_probes(probes_json):
                                if isinstance(x, dict)),
                 f"    best {rates[best_k]:.1f} GB/s ({rates[best_k] / 80:.1f}% of 8 TB/s): the HBM read rate one stream "
                 "sustains, the ceiling of a decode step whose launches cost nothing."]
+    if d.get("launch_cost"):
+        out += ["", "Fixed cost of a launch against its grid (36 launches of a kernel that loads nothing, back to back",
+                "in a graph, us per launch):",
+                "    " + ", ".join(f"{r['blocks']} x {r['threads']}: {r['us']:.2f}" for r in d["launch_cost"])]
     m = d["moe_t1_shared_in_bank"]
     f1, f0 = m["combine in the shared down GEMV"], m["combine as its own launch"]
     s = sum(best[k] for k in ("qkv", "o", "gate_up", "down"))
