@@ -158,9 +158,16 @@ int rk_npu_hip_inject_alloc_failures(int count);
  *   HM_GEMV_COMBINE  1: a one-token MoE call with a shared expert runs the
  *                    combine in the shared down GEMV's epilogue where that
  *                    GEMV allows; 0: always as a separate launch
- *   HM_HOST_SPIN     0: a host-buffer call (rk_npu_*_run_f32, _run_dynamic,
- *                    the MoE run) waits for its work in hipStreamSynchronize;
- *                    1: by polling its stream (slower here)
+ *   HM_HOST_FLAG     1: a host-buffer call (rk_npu_*_run_f32, _run_dynamic,
+ *                    the MoE run) whose input and output each fit 64 KB
+ *                    runs on the compute queue: a kernel fetches its inputs
+ *                    from the workspace's pinned stage, and a copy kernel
+ *                    writes C and a completion word into the stage, which
+ *                    the CPU polls; 0: copies in and out and a wait on the
+ *                    stream (HM_HOST_SPIN), as larger calls always do
+ *   HM_HOST_SPIN     0: a host-buffer call that waits on its stream does so
+ *                    in hipStreamSynchronize; 1: by polling its stream
+ *                    (slower here)
  * Unknown names return RK_NPU_ERR_PARAM. */
 int rk_npu_hip_set_switch(const char* name, int value, int* previous);
 

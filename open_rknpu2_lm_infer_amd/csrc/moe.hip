@@ -668,23 +668,14 @@ int rk_npu_moe_w8_run_f32(rk_npu_moe_w8_workspace* workspace, const rk_npu_moe_w
     hipStream_t s = ws->stream;
     float* x = ws->xws->a_f32;
     // Inputs (rows, ids, routes) and later the output pass through the input
-    // workspace's pinned stage when they fit it, else straight from pageable memory.
+    // workspace's pinned stage when they fit it (each input at a 256-byte
+    // aligned offset), else straight from pageable memory.
     const size_t xb = (size_t)rows * ws->h * 4, ab = (size_t)A * 4;
-    uint8_t* st = reinterpret_cast<uint8_t*>(host_stage(ws->xws, xb + 2 * ab));
-    const void* src_x = input;
-    const void* src_ids = ids;
-    const void* src_routes = routes;
-    if (st) {
-        std::memcpy(st, input, xb);
-        std::memcpy(st + xb, ids, ab);
-        std::memcpy(st + xb + ab, routes, ab);
-        src_x = st;
-        src_ids = st + xb;
-        src_routes = st + xb + ab;
-    }
-    if (hipMemcpyAsync(x, src_x, xb, hipMemcpyHostToDevice, s) != hipSuccess ||
-        hipMemcpyAsync(ws->ids, src_ids, ab, hipMemcpyHostToDevice, s) != hipSuccess ||
-        hipMemcpyAsync(ws->routes, src_routes, ab, hipMemcpyHostToDevice, s) != hipSuccess) {
+    const size_t off_ids = round_up_z(xb, 256), off_routes = off_ids + round_up_z(ab, 256);
+    void* st = host_stage(ws->xws, std::max(off_routes + round_up_z(ab, 16), xb));
+    const bool small = host_small(ws->xws, st, off_routes + ab, xb);
+    const HostSeg segs[3] = {{input, x, xb, 0}, {ids, ws->ids, ab, off_ids}, {routes, ws->routes, ab, off_routes}};
+    if (!upload_host(ws->xws, small, st, segs, 3, s)) {
         (void)hipStreamSynchronize(s);
         return RK_NPU_ERR_DEVICE;
     }
@@ -696,11 +687,7 @@ int rk_npu_moe_w8_run_f32(rk_npu_moe_w8_workspace* workspace, const rk_npu_moe_w
     }
     if (timings && hipStreamSynchronize(s) != hipSuccess) return RK_NPU_ERR_DEVICE;
     const double t2 = now_us();
-    if (hipMemcpyAsync(st ? static_cast<void*>(st) : static_cast<void*>(output), ws->out, xb, hipMemcpyDeviceToHost,
-                       s) != hipSuccess ||
-        host_wait(s) != hipSuccess)
-        return RK_NPU_ERR_DEVICE;
-    if (st) std::memcpy(output, st, xb);
+    if (!download_host(ws->xws, small, st, output, ws->out, xb, s)) return RK_NPU_ERR_DEVICE;
     if (timings) {
         std::memset(timings, 0, sizeof(*timings));
         const double t3 = now_us();

@@ -88,9 +88,16 @@ struct Workspace {
     unsigned long long* kacc;  // split-K GEMV column slots [N_pad] + row code-sum slot, kept zero between calls
     unsigned* sync;            // one-launch FFN synchronisation words (FfnSync), kept zero between calls
     bool fused_pending;        // a one-launch FFN ran since its error word was last read (host side)
-    // pinned host staging of the host-buffer calls (allocated on first use)
+    // pinned host staging of the host-buffer calls (allocated on first use):
+    // host_stage_bytes of data, then a completion word (host_done) that a
+    // copy kernel sets to the call's sequence number once C is in the stage;
+    // *_dev are the device addresses of both
     void* host_stage;
     size_t host_stage_bytes;
+    void* host_stage_dev;
+    unsigned* host_done;
+    unsigned* host_done_dev;
+    unsigned host_seq;
 };
 
 size_t workspace_bytes(const Geometry& g, int M);
@@ -167,6 +174,22 @@ int device_of(Domain* d);
 // Wait for a host-buffer call's stream (block in hipStreamSynchronize, or
 // poll hipStreamQuery with HM_HOST_SPIN=1).
 hipError_t host_wait(hipStream_t s);
+// Host-buffer transfers through the workspace's stage `st` (from
+// host_stage(ws, ...), sized for the call; nullptr: pageable copies). A call
+// is small (host_small) when its input and output fit the kernel path: its
+// inputs are fetched by one kernel launch and its output published by a
+// copy kernel and a completion word the CPU polls; otherwise copies and a
+// wait on the stream. Both ends of a call take the same `small`.
+struct HostSeg {
+    const void* src;   // caller's host memory
+    void* dst;         // device memory (16-byte aligned, extending to a whole 16-byte piece)
+    size_t bytes;
+    size_t stage_off;  // 256-byte aligned offset of this segment in the stage
+};
+bool host_small(const Workspace* ws, const void* st, size_t in_bytes, size_t out_bytes);
+bool upload_host(Workspace* ws, bool small, void* st, const HostSeg* segs, int n, hipStream_t s);
+// Returns once C holds `bytes` of the device output `src`.
+bool download_host(Workspace* ws, bool small, void* st, void* C, const void* src, size_t bytes, hipStream_t s);
 struct BusyGuard {
     std::atomic<bool>* flag;
     bool ok;

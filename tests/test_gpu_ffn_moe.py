@@ -311,3 +311,47 @@ def test_moe_device_entry_aligned_unaligned_and_bad_ids(rows):
         assert rc == 0
         assert L.rk_npu_hip_moe_status(work.raw) == F.RK_NPU_ERR_PARAM, f"live route {live}"
         assert L.rk_npu_hip_moe_status(work.raw) == 0
+
+
+@pytest.mark.parametrize("flag_order", [(1, 0, 1), (0, 1, 0)])
+def test_host_calls_kernel_path_and_copies(flag_order):
+    """Host-buffer calls whose input and output each fit 64 KB run on the
+    compute queue (a fetch kernel, the work, a copy kernel that publishes C
+    and a completion word the CPU polls); HM_HOST_FLAG=0 and larger calls
+    copy and wait on the stream. Both paths, alternated on the same
+    workspaces (the polled path returns with the stream's last launch still
+    ending), give the oracle's result bit for bit: linear W4/W8 at 1 and 3
+    rows (small) and 8 rows of K=4096 (128 KB of A: copies either way), the
+    fused FFN at M=1, and the MoE at one token and at 40 (output 40 KB,
+    inputs at 256-byte aligned stage offsets)."""
+    from open_rknpu2_lm_infer_amd import device as D
+    backend = npu.Backend(npu.ModelOptions(chunk=64))
+    lin = {}
+    for bits in (4, 8):
+        for rows, k, n in ((1, 2560, 384), (3, 2560, 384), (8, 4096, 256)):
+            codes, scales = R.weights(9, f"hostk{bits}-{k}-{n}", bits, k, n)
+            lin[(bits, rows)] = (backend.load(npu.QuantMatrix(bits, k, n, codes, scales)), codes, scales, k, n)
+    ffn = FFN(backend, 256, 384, 1, 8, "hostk-ffn")
+    h, inter, experts, top = 256, 96, 16, 4
+    gate, down = moe_bank(h, inter, experts, 8, "hostk-moe")
+    moe = backend.load_moe(gate, down, top)
+    for flag in flag_order:
+        print(f"HM_HOST_FLAG={flag}", flush=True)
+        with D.plan_switch("HM_HOST_FLAG", flag):
+            for (bits, rows), (linear, codes, scales, k, n) in lin.items():
+                x = R.activations(9, f"hostk-x{rows}-{k}-{flag}", rows, k)
+                out = np.full((rows, n), np.nan, np.float32)
+                linear.run(x, out, rows)
+                assert np.array_equal(out, oracle.linear(codes, scales, x)), (bits, rows, flag)
+                sw = np.full((rows, n // 2), np.nan, np.float32)
+                if linear.run_swiglu(x, sw, rows):  # (W4 weights only)
+                    assert np.array_equal(sw, oracle.linear_swiglu(codes, scales, x)), (bits, rows, flag)
+            x = R.activations(9, f"hostk-ffn-x{flag}", 1, 256)
+            assert np.array_equal(ffn.run(x), oracle.ffn(ffn.gc, ffn.gs, ffn.dc, ffn.ds, x))
+            for rows in (1, 40):
+                x = R.activations(9, f"hostk-moe-x{rows}-{flag}", rows, h)
+                ids, w = routed(rows, experts, top, f"hostk-moe-r{rows}-{flag}")
+                out = np.full((rows, h), np.nan, np.float32)
+                moe.run(x, ids, w, out, rows)
+                ref = oracle.moe([(g.codes, g.scales) for g in gate], [(d.codes, d.scales) for d in down], x, ids, w)
+                assert np.array_equal(out, ref), (rows, flag)
