@@ -707,6 +707,8 @@ struct AttnCache {
     size_t bytes_each;  // of k and of v
     uint64_t generation;  // bumped whenever the K/V storage is replaced or reloaded
     DevFence fence;       // device-path appends (writes) and runs (reads) of the rows
+    hipStream_t stream = nullptr;  // host-buffer appends (created on the first)
+    HostStage hs;                  // their pinned staging
 };
 
 struct AttnWork {
@@ -720,6 +722,7 @@ struct AttnWork {
     hipStream_t stream;
     std::atomic<bool> busy;
     DevFence fence;  // device-path runs writing this workspace's partials
+    HostStage hs;    // pinned staging of host-buffer runs
 };
 
 // The reference's checks (src/npu.rs:714-728) plus this library's limits.
@@ -807,6 +810,54 @@ static int cache_put(AttnCache* c, const void* k, const void* v, int rows, hipMe
     if (e1 != hipSuccess || e2 != hipSuccess) return RK_NPU_ERR_DEVICE;
     c->length += rows;
     return RK_NPU_OK;
+}
+
+// Host-buffer append: rows of K and V ([kv_heads][rows][D] each, V at
+// byte offset voff of the stage) copied into the cache rows [length, length +
+// rows) of every head, 16 bytes per thread and step.
+__global__ __launch_bounds__(256) void attn_append_kernel(const v4u* __restrict__ src, size_t voff_pieces,
+                                                          v4u* __restrict__ k, v4u* __restrict__ v, int rows,
+                                                          int row_pieces, size_t head_pieces, int length,
+                                                          size_t total) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (size_t)gridDim.x * 256) {
+        const size_t per_head = (size_t)rows * row_pieces;
+        const size_t h = i / per_head, r = i % per_head;
+        const size_t at = h * head_pieces + (size_t)length * row_pieces + r;
+        k[at] = src[i];
+        v[at] = src[voff_pieces + i];
+    }
+}
+
+// Appends host rows through the cache's pinned stage and stream, returning
+// once they are in the cache (the stage's completion word); false when the
+// stage path is not available (the caller copies directly).
+static bool cache_put_staged(AttnCache* c, const void* k, const void* v, int rows, int& rc) {
+    const int kh = c->cfg.kv_heads, D = c->cfg.head_dim;
+    const size_t each = (size_t)kh * rows * D * sizeof(__half), voff = round_up_z(each, 256);
+    if (!host_kernels_enabled()) return false;
+    if (!c->stream && hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+        (void)hipGetLastError();
+        c->stream = nullptr;
+        return false;
+    }
+    void* st = stage_reserve(c->hs, voff + each, c->stream);
+    if (!st) return false;
+    std::memcpy(st, k, each);
+    std::memcpy(static_cast<uint8_t*>(st) + voff, v, each);
+    const int row_pieces = D / 8;
+    const size_t total = (size_t)kh * rows * row_pieces;
+    const int blocks = (int)std::min<size_t>(1024, (total + 255) / 256);
+    hipLaunchKernelGGL(attn_append_kernel, dim3(blocks), dim3(256), 0, c->stream, static_cast<const v4u*>(c->hs.dev),
+                       voff / 16, reinterpret_cast<v4u*>(c->k), reinterpret_cast<v4u*>(c->v), rows, row_pieces,
+                       (size_t)c->capacity * row_pieces, c->length, total);
+    if (hipGetLastError() != hipSuccess || !stage_download(c->hs, true, st, nullptr, nullptr, 0, c->stream)) {
+        (void)hipStreamSynchronize(c->stream);
+        rc = RK_NPU_ERR_DEVICE;
+        return true;
+    }
+    c->length += rows;
+    rc = RK_NPU_OK;
+    return true;
 }
 
 struct AttnPlan {
@@ -941,19 +992,28 @@ static int run_host(rk_npu_attention_f16_workspace* workspace, rk_npu_attention_
     // Device-path appends and runs (rk_npu_hip_attention_cache_append / _run)
     // are enqueued on the caller's streams and may still be writing the
     // cache's rows or this workspace's partials: this call's stream waits for
-    // them first.
+    // them first. q comes in and the output goes out through the workspace's
+    // pinned stage (the kernel path of small calls, else copies and a wait).
+    const size_t qb = n * sizeof(__half), ob = n * (out_f16 ? sizeof(__half) : sizeof(float));
+    void* st = nullptr;
+    bool small = false;
     if (hipSetDevice(device_of(w->domain)) != hipSuccess || c->fence.wait(w->stream) != hipSuccess ||
-        w->fence.wait(w->stream) != hipSuccess ||
-        hipMemcpyAsync(w->q, q, n * sizeof(__half), hipMemcpyHostToDevice, w->stream) != hipSuccess ||
-        hipStreamSynchronize(w->stream) != hipSuccess)
+        w->fence.wait(w->stream) != hipSuccess) {
         rc = RK_NPU_ERR_DEVICE;
+    } else {
+        st = stage_reserve(w->hs, std::max(qb, ob), w->stream);
+        small = stage_small(w->hs, st, qb, ob);
+        const HostSeg seg{q, w->q, qb, 0};
+        if (!stage_upload(w->hs, small, st, &seg, 1, w->stream) ||
+            (t && hipStreamSynchronize(w->stream) != hipSuccess))
+            rc = RK_NPU_ERR_DEVICE;
+    }
     const double t1 = now_us();
     if (rc == RK_NPU_OK) rc = enqueue_attention(w, c, w->q, rows, pos, w->out, out_f16, w->stream);
-    if (rc == RK_NPU_OK && hipStreamSynchronize(w->stream) != hipSuccess) rc = RK_NPU_ERR_DEVICE;
+    if (rc == RK_NPU_OK && t && hipStreamSynchronize(w->stream) != hipSuccess) rc = RK_NPU_ERR_DEVICE;
     const double t2 = now_us();
-    if (rc == RK_NPU_OK &&
-        hipMemcpy(out, w->out, n * (out_f16 ? sizeof(__half) : sizeof(float)), hipMemcpyDeviceToHost) != hipSuccess)
-        rc = RK_NPU_ERR_DEVICE;
+    if (rc == RK_NPU_OK && !stage_download(w->hs, small, st, out, w->out, ob, w->stream)) rc = RK_NPU_ERR_DEVICE;
+    if (rc != RK_NPU_OK) (void)hipStreamSynchronize(w->stream);
     const double t3 = now_us();
     if (t) {
         t->upload_us = t1 - t0;
@@ -1039,6 +1099,7 @@ void rk_npu_attention_f16_workspace_free(rk_npu_attention_f16_workspace* workspa
     }
     (void)w->fence.wait(nullptr);
     w->fence.destroy();
+    stage_release(w->hs);
     domain_free(w->domain, w->q, w->q_bytes);
     domain_free(w->domain, w->out, w->out_bytes);
     domain_free(w->domain, w->part, w->part_bytes);
@@ -1078,6 +1139,11 @@ void rk_npu_attention_f16_cache_free(rk_npu_attention_f16_cache* cache) {
     (void)hipSetDevice(device_of(c->domain));
     (void)c->fence.wait(nullptr);
     c->fence.destroy();
+    if (c->stream) {
+        (void)hipStreamSynchronize(c->stream);
+        (void)hipStreamDestroy(c->stream);
+    }
+    stage_release(c->hs);
     domain_free(c->domain, c->k, c->bytes_each);
     domain_free(c->domain, c->v, c->bytes_each);
     c->magic = 0;
@@ -1118,6 +1184,8 @@ int rk_npu_attention_f16_cache_append(rk_npu_ctx* ctx, rk_npu_attention_f16_cach
         int rc = cache_grow(c, grown);
         if (rc != RK_NPU_OK) return rc;
     }
+    int rc = RK_NPU_OK;
+    if (cache_put_staged(c, k, v, rows, rc)) return rc;
     return cache_put(c, k, v, rows, hipMemcpyHostToDevice, nullptr, false);
 }
 

@@ -486,13 +486,8 @@ Workspace* workspace_create(Domain* d, int bits, int M, int K, int N) {
     ws->domain = d;
     ws->busy.store(false);
     ws->stream = nullptr;
-    ws->host_stage = nullptr;
-    ws->host_stage_bytes = 0;
+    ws->hs = HostStage{};
     ws->fused_pending = false;
-    ws->host_stage_dev = nullptr;
-    ws->host_done = nullptr;
-    ws->host_done_dev = nullptr;
-    ws->host_seq = 0;
     const WsLayout L = ws_layout(ws->g, M);
     ws->bytes = L.total;
     uint8_t* base = static_cast<uint8_t*>(domain_alloc(d, L.total));
@@ -540,7 +535,7 @@ void workspace_destroy(Workspace* ws) {
         (void)hipStreamDestroy(ws->stream);
     }
     domain_free(ws->domain, ws->a_f32, ws->bytes);
-    if (ws->host_stage) (void)hipHostFree(ws->host_stage);
+    stage_release(ws->hs);
     if (ws->magic == MAGIC_WS8)
         delete static_cast<rk_npu_matmul_workspace*>(ws);
     else
@@ -997,13 +992,8 @@ static bool scratch_workspace(uint8_t* base, const Weights* w, int rows, Workspa
     ws.domain = w->domain;
     ws.stream = nullptr;
     ws.busy.store(false);
-    ws.host_stage = nullptr;
-    ws.host_stage_bytes = 0;
+    ws.hs = HostStage{};
     ws.fused_pending = false;
-    ws.host_stage_dev = nullptr;
-    ws.host_done = nullptr;
-    ws.host_done_dev = nullptr;
-    ws.host_seq = 0;
     ws.a_f32 = nullptr;
     ws.c_f32 = nullptr;
     size_t off = 0;
@@ -1038,38 +1028,40 @@ static bool scratch_workspace(uint8_t* base, const Weights* w, int rows, Workspa
 constexpr size_t HOST_STAGE_CAP = 8u << 20;
 
 // The stage is coherent (fine-grained) pinned memory, so the copy kernel's
-// stores and its completion word reach host memory without a cache flush;
-// 256 bytes after the data hold the completion word.
-float* host_stage(Workspace* ws, size_t bytes) {
+// stores and its completion word reach host memory without a cache flush.
+void* stage_reserve(HostStage& st, size_t bytes, hipStream_t s) {
     if (bytes == 0 || bytes > HOST_STAGE_CAP) return nullptr;
-    if (ws->host_stage_bytes < bytes) {
-        if (ws->host_stage) {
-            (void)hipStreamSynchronize(ws->stream);  // (a previous call's copy kernel may still be ending)
-            (void)hipHostFree(ws->host_stage);
+    if (st.bytes < bytes) {
+        if (st.host) {
+            if (s) (void)hipStreamSynchronize(s);  // (a previous call's copy kernel may still be ending)
+            (void)hipHostFree(st.host);
         }
-        ws->host_stage = nullptr;
-        ws->host_stage_bytes = 0;
-        ws->host_stage_dev = nullptr;
-        ws->host_done = nullptr;
-        ws->host_done_dev = nullptr;
+        st = HostStage{};
         const size_t want = std::min(HOST_STAGE_CAP, std::max(bytes, (size_t)64 << 10));
         void* dev = nullptr;
-        if (hipHostMalloc(&ws->host_stage, want + 256, hipHostMallocCoherent | hipHostMallocMapped) != hipSuccess ||
-            hipHostGetDevicePointer(&dev, ws->host_stage, 0) != hipSuccess) {
-            if (ws->host_stage) (void)hipHostFree(ws->host_stage);
-            ws->host_stage = nullptr;
+        void* host = nullptr;
+        if (hipHostMalloc(&host, want + 256, hipHostMallocCoherent | hipHostMallocMapped) != hipSuccess ||
+            hipHostGetDevicePointer(&dev, host, 0) != hipSuccess) {
+            if (host) (void)hipHostFree(host);
             (void)hipGetLastError();
             return nullptr;
         }
-        ws->host_stage_bytes = want;
-        ws->host_stage_dev = dev;
-        ws->host_done = reinterpret_cast<unsigned*>(static_cast<uint8_t*>(ws->host_stage) + want);
-        ws->host_done_dev = reinterpret_cast<unsigned*>(static_cast<uint8_t*>(dev) + want);
-        __atomic_store_n(ws->host_done, 0u, __ATOMIC_RELEASE);
-        ws->host_seq = 0;
+        st.host = host;
+        st.dev = dev;
+        st.bytes = want;
+        st.done = reinterpret_cast<unsigned*>(static_cast<uint8_t*>(host) + want);
+        st.done_dev = reinterpret_cast<unsigned*>(static_cast<uint8_t*>(dev) + want);
+        __atomic_store_n(st.done, 0u, __ATOMIC_RELEASE);
     }
-    return static_cast<float*>(ws->host_stage);
+    return st.host;
 }
+
+void stage_release(HostStage& st) {
+    if (st.host) (void)hipHostFree(st.host);
+    st = HostStage{};
+}
+
+float* host_stage(Workspace* ws, size_t bytes) { return static_cast<float*>(stage_reserve(ws->hs, bytes, ws->stream)); }
 
 // Host-buffer transfers. A small call (input and output each at most
 // HOST_SMALL bytes, and a stage) stays on the compute queue from start to
@@ -1114,12 +1106,13 @@ __global__ __launch_bounds__(1024) void host_publish_kernel(const v4u* __restric
     if (threadIdx.x == 0) __hip_atomic_store(done, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
-bool host_small(const Workspace* ws, const void* st, size_t in_bytes, size_t out_bytes) {
-    return st && ws->host_done && in_bytes <= HOST_SMALL && out_bytes <= HOST_SMALL &&
-           switch_value(SW_HOST_FLAG) != 0;
+bool host_kernels_enabled() { return switch_value(SW_HOST_FLAG) != 0; }
+
+bool stage_small(const HostStage& st, const void* p, size_t in_bytes, size_t out_bytes) {
+    return p && st.done && in_bytes <= HOST_SMALL && out_bytes <= HOST_SMALL && switch_value(SW_HOST_FLAG) != 0;
 }
 
-bool upload_host(Workspace* ws, bool small, void* st, const HostSeg* segs, int n, hipStream_t s) {
+bool stage_upload(HostStage& stg, bool small, void* st, const HostSeg* segs, int n, hipStream_t s) {
     if (n < 1 || n > 3) return false;
     if (!st) {
         for (int k = 0; k < n; ++k)
@@ -1135,7 +1128,7 @@ bool upload_host(Workspace* ws, bool small, void* st, const HostSeg* segs, int n
         std::memcpy(at, segs[k].src, segs[k].bytes);
         if (!small && hipMemcpyAsync(segs[k].dst, at, segs[k].bytes, hipMemcpyHostToDevice, s) != hipSuccess)
             return false;
-        F.src[k] = reinterpret_cast<const v4u*>(static_cast<uint8_t*>(ws->host_stage_dev) + segs[k].stage_off);
+        F.src[k] = reinterpret_cast<const v4u*>(static_cast<uint8_t*>(stg.dev) + segs[k].stage_off);
         F.dst[k] = static_cast<v4u*>(segs[k].dst);
         F.pieces[k] = (int)((segs[k].bytes + 15) / 16);
         most = std::max(most, F.pieces[k]);
@@ -1160,32 +1153,34 @@ hipError_t host_wait(hipStream_t s) {
     return hipStreamSynchronize(s);
 }
 
-bool download_host(Workspace* ws, bool small, void* st, void* C, const void* src, size_t bytes, hipStream_t s) {
-    if (!st) return hipMemcpyAsync(C, src, bytes, hipMemcpyDeviceToHost, s) == hipSuccess && host_wait(s) == hipSuccess;
+bool stage_download(HostStage& stg, bool small, void* st, void* C, const void* src, size_t bytes, hipStream_t s) {
     if (!small) {
+        if (bytes == 0) return host_wait(s) == hipSuccess;
+        if (!st)
+            return hipMemcpyAsync(C, src, bytes, hipMemcpyDeviceToHost, s) == hipSuccess && host_wait(s) == hipSuccess;
         if (hipMemcpyAsync(st, src, bytes, hipMemcpyDeviceToHost, s) != hipSuccess || host_wait(s) != hipSuccess)
             return false;
         std::memcpy(C, st, bytes);
         return true;
     }
-    const unsigned seq = ++ws->host_seq == 0 ? ++ws->host_seq : ws->host_seq;  // (0 is the word's initial value)
+    const unsigned seq = ++stg.seq == 0 ? ++stg.seq : stg.seq;  // (0 is the word's initial value)
     const int pieces = (int)((bytes + 15) / 16);
     hipLaunchKernelGGL(host_publish_kernel, dim3(1), dim3(1024), 0, s, static_cast<const v4u*>(src),
-                       static_cast<v4u*>(ws->host_stage_dev), pieces, ws->host_done_dev, seq);
+                       static_cast<v4u*>(stg.dev), pieces, stg.done_dev, seq);
     if (hipGetLastError() != hipSuccess) {
         (void)hipStreamSynchronize(s);
         return false;
     }
     const double t0 = now_us();
-    for (unsigned n = 1; __atomic_load_n(ws->host_done, __ATOMIC_ACQUIRE) != seq; ++n) {
+    for (unsigned n = 1; __atomic_load_n(stg.done, __ATOMIC_ACQUIRE) != seq; ++n) {
         if ((n & 255) == 0 && now_us() - t0 > HOST_POLL_US) {
-            if (hipStreamSynchronize(s) != hipSuccess || __atomic_load_n(ws->host_done, __ATOMIC_ACQUIRE) != seq)
+            if (hipStreamSynchronize(s) != hipSuccess || __atomic_load_n(stg.done, __ATOMIC_ACQUIRE) != seq)
                 return false;
             break;
         }
         __builtin_ia32_pause();
     }
-    std::memcpy(C, st, bytes);
+    if (bytes) std::memcpy(C, st, bytes);
     return true;
 }
 
@@ -1391,9 +1386,9 @@ static int run_host(Workspace* ws, const Weights* w, const float* A, float* C, i
     const int M = ws->M, K = w->g.K, N = w->g.N;
     const int width = epi == EPI_PLAIN ? N : N / 2;
     float* st = host_stage(ws, std::max((size_t)M * K * 4, (size_t)M * width * 4));
-    const bool small = host_small(ws, st, (size_t)M * K * 4, (size_t)M * width * 4);
+    const bool small = stage_small(ws->hs, st, (size_t)M * K * 4, (size_t)M * width * 4);
     const HostSeg seg{A, ws->a_f32, (size_t)M * K * 4, 0};
-    if (!upload_host(ws, small, st, &seg, 1, ws->stream)) {
+    if (!stage_upload(ws->hs, small, st, &seg, 1, ws->stream)) {
         (void)hipStreamSynchronize(ws->stream);
         return RK_NPU_ERR_DEVICE;
     }
@@ -1406,7 +1401,7 @@ static int run_host(Workspace* ws, const Weights* w, const float* A, float* C, i
     }
     if (timings && hipStreamSynchronize(ws->stream) != hipSuccess) return RK_NPU_ERR_DEVICE;
     const double t2 = now_us();
-    if (!download_host(ws, small, st, C, ws->c_f32, (size_t)M * width * 4, ws->stream)) return RK_NPU_ERR_DEVICE;
+    if (!stage_download(ws->hs, small, st, C, ws->c_f32, (size_t)M * width * 4, ws->stream)) return RK_NPU_ERR_DEVICE;
     if (timings) {
         const double t3 = now_us();
         timings->upload_us = t1 - t0;
@@ -1536,11 +1531,10 @@ int rk_npu_w4a8_run_ffn_f32(rk_npu_w4a8_workspace* gate_up_workspace, const rk_n
     hipStream_t s = gws->stream;
     float* st_in = host_stage(gws, (size_t)M * H * 4);
     float* st_out = host_stage(dws, (size_t)M * H * 4);
-    const bool small_in = host_small(gws, st_in, (size_t)M * H * 4, 0);
-    const bool small_out = host_small(dws, st_out, 0, (size_t)M * H * 4);
-    const bool small = small_in && small_out;
+    const bool small =
+        stage_small(gws->hs, st_in, (size_t)M * H * 4, 0) && stage_small(dws->hs, st_out, 0, (size_t)M * H * 4);
     const HostSeg seg{A, gws->a_f32, (size_t)M * H * 4, 0};
-    if (!upload_host(gws, small, st_in, &seg, 1, s)) {
+    if (!stage_upload(gws->hs, small, st_in, &seg, 1, s)) {
         (void)hipStreamSynchronize(s);
         return RK_NPU_ERR_DEVICE;
     }
@@ -1552,7 +1546,7 @@ int rk_npu_w4a8_run_ffn_f32(rk_npu_w4a8_workspace* gate_up_workspace, const rk_n
     }
     if (timings && hipStreamSynchronize(s) != hipSuccess) return RK_NPU_ERR_DEVICE;
     const double t2 = now_us();
-    if (!download_host(dws, small, st_out, C, dws->c_f32, (size_t)M * H * 4, s)) return RK_NPU_ERR_DEVICE;
+    if (!stage_download(dws->hs, small, st_out, C, dws->c_f32, (size_t)M * H * 4, s)) return RK_NPU_ERR_DEVICE;
     rc = ffn_take_error(dws);
     if (rc != RK_NPU_OK) return rc;
     if (timings) {

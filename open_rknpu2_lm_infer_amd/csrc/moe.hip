@@ -673,9 +673,9 @@ int rk_npu_moe_w8_run_f32(rk_npu_moe_w8_workspace* workspace, const rk_npu_moe_w
     const size_t xb = (size_t)rows * ws->h * 4, ab = (size_t)A * 4;
     const size_t off_ids = round_up_z(xb, 256), off_routes = off_ids + round_up_z(ab, 256);
     void* st = host_stage(ws->xws, std::max(off_routes + round_up_z(ab, 16), xb));
-    const bool small = host_small(ws->xws, st, off_routes + ab, xb);
+    const bool small = stage_small(ws->xws->hs, st, off_routes + ab, xb);
     const HostSeg segs[3] = {{input, x, xb, 0}, {ids, ws->ids, ab, off_ids}, {routes, ws->routes, ab, off_routes}};
-    if (!upload_host(ws->xws, small, st, segs, 3, s)) {
+    if (!stage_upload(ws->xws->hs, small, st, segs, 3, s)) {
         (void)hipStreamSynchronize(s);
         return RK_NPU_ERR_DEVICE;
     }
@@ -687,7 +687,7 @@ int rk_npu_moe_w8_run_f32(rk_npu_moe_w8_workspace* workspace, const rk_npu_moe_w
     }
     if (timings && hipStreamSynchronize(s) != hipSuccess) return RK_NPU_ERR_DEVICE;
     const double t2 = now_us();
-    if (!download_host(ws->xws, small, st, output, ws->out, xb, s)) return RK_NPU_ERR_DEVICE;
+    if (!stage_download(ws->xws->hs, small, st, output, ws->out, xb, s)) return RK_NPU_ERR_DEVICE;
     if (timings) {
         std::memset(timings, 0, sizeof(*timings));
         const double t3 = now_us();

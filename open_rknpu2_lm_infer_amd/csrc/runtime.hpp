@@ -66,6 +66,25 @@ struct Weights {
     uint64_t fingerprint;
 };
 
+// Pinned host staging of host-buffer calls: coherent (fine-grained) pinned
+// memory of `bytes` data bytes, then 256 bytes holding a completion word that
+// a kernel sets to a call's sequence number; dev / done_dev are the device
+// addresses of both. Allocated on first use and grown on demand (up to
+// 8 MiB); stage_reserve returns nullptr for larger requests or when the
+// allocation fails, and the caller then copies pageable memory directly.
+struct HostStage {
+    void* host = nullptr;
+    void* dev = nullptr;
+    size_t bytes = 0;
+    unsigned* done = nullptr;
+    unsigned* done_dev = nullptr;
+    unsigned seq = 0;
+};
+// The stage's data (at least `bytes`), growing it after stream `s` (the
+// stage's user) has finished with the old one.
+void* stage_reserve(HostStage& st, size_t bytes, hipStream_t s);
+void stage_release(HostStage& st);
+
 struct Workspace {
     uint32_t magic;
     Geometry g;
@@ -88,24 +107,13 @@ struct Workspace {
     unsigned long long* kacc;  // split-K GEMV column slots [N_pad] + row code-sum slot, kept zero between calls
     unsigned* sync;            // one-launch FFN synchronisation words (FfnSync), kept zero between calls
     bool fused_pending;        // a one-launch FFN ran since its error word was last read (host side)
-    // pinned host staging of the host-buffer calls (allocated on first use):
-    // host_stage_bytes of data, then a completion word (host_done) that a
-    // copy kernel sets to the call's sequence number once C is in the stage;
-    // *_dev are the device addresses of both
-    void* host_stage;
-    size_t host_stage_bytes;
-    void* host_stage_dev;
-    unsigned* host_done;
-    unsigned* host_done_dev;
-    unsigned host_seq;
+    HostStage hs;  // pinned host staging of the host-buffer calls (allocated on first use)
 };
 
 size_t workspace_bytes(const Geometry& g, int M);
 Workspace* workspace_create(Domain* d, int bits, int M, int K, int N);
 void workspace_destroy(Workspace* ws);
-// The workspace's pinned host stage of at least `bytes` (allocated or grown
-// on demand, up to 8 MiB), or nullptr when the request is larger or the
-// allocation fails; the caller then copies pageable memory directly.
+// The workspace's pinned host stage of at least `bytes` (stage_reserve).
 float* host_stage(Workspace* ws, size_t bytes);
 
 Weights* weights_create(Domain* d, int bits, int K, int N, const int8_t* codes, const float* scales,
@@ -174,22 +182,25 @@ int device_of(Domain* d);
 // Wait for a host-buffer call's stream (block in hipStreamSynchronize, or
 // poll hipStreamQuery with HM_HOST_SPIN=1).
 hipError_t host_wait(hipStream_t s);
-// Host-buffer transfers through the workspace's stage `st` (from
-// host_stage(ws, ...), sized for the call; nullptr: pageable copies). A call
-// is small (host_small) when its input and output fit the kernel path: its
-// inputs are fetched by one kernel launch and its output published by a
-// copy kernel and a completion word the CPU polls; otherwise copies and a
-// wait on the stream. Both ends of a call take the same `small`.
+// Host-buffer transfers through a stage's data `p` (from stage_reserve, sized
+// for the call; nullptr: pageable copies). A call is small (stage_small)
+// when its input and output fit the kernel path: its inputs are fetched by
+// one kernel launch and its output published by a copy kernel and the
+// completion word, which the CPU polls; otherwise copies and a wait on the
+// stream. Both ends of a call take the same `small`.
 struct HostSeg {
     const void* src;   // caller's host memory
     void* dst;         // device memory (16-byte aligned, extending to a whole 16-byte piece)
     size_t bytes;
     size_t stage_off;  // 256-byte aligned offset of this segment in the stage
 };
-bool host_small(const Workspace* ws, const void* st, size_t in_bytes, size_t out_bytes);
-bool upload_host(Workspace* ws, bool small, void* st, const HostSeg* segs, int n, hipStream_t s);
-// Returns once C holds `bytes` of the device output `src`.
-bool download_host(Workspace* ws, bool small, void* st, void* C, const void* src, size_t bytes, hipStream_t s);
+bool stage_small(const HostStage& st, const void* p, size_t in_bytes, size_t out_bytes);
+// HM_HOST_FLAG: host-buffer calls may take the kernel path at all.
+bool host_kernels_enabled();
+bool stage_upload(HostStage& st, bool small, void* p, const HostSeg* segs, int n, hipStream_t s);
+// Returns once C holds `bytes` of the device output `src` (bytes may be 0:
+// then it returns once the work enqueued before it has finished).
+bool stage_download(HostStage& st, bool small, void* p, void* C, const void* src, size_t bytes, hipStream_t s);
 struct BusyGuard {
     std::atomic<bool>* flag;
     bool ok;

@@ -271,3 +271,47 @@ def test_device_entry_points_match_host_path():
     finally:
         L.rk_npu_attention_f16_cache_free(cache)
         L.rk_npu_attention_f16_workspace_free(ws)
+
+
+@pytest.mark.parametrize("flag_order", [(1, 0, 1), (0, 1, 0)])
+def test_host_transfer_paths_agree(flag_order):
+    """Host-buffer appends and runs take the kernel path (pinned stage,
+    fetch and copy kernels, polled completion word) when the run's q and
+    output each fit 64 KB, or copies with waits (HM_HOST_FLAG=0, larger
+    runs, appends: a cache stage and stream against 2-D copies). Alternating
+    the two on one cache and workspace gives the same bits, and the oracle's
+    result within TOL: 1-row decode steps (16 KB output: kernel path), a
+    3-row step (48 KB) and a 5-row step (80 KB: copies either way), 32 query
+    heads over 8 KV heads, d = 128, after 300 cached rows."""
+    from open_rknpu2_lm_infer_amd import device as D
+    qh, kh, d = 32, 8, 128
+    scale = d ** -0.5
+    results = {}
+    for order in (flag_order, tuple(1 - f for f in flag_order)):
+        be = npu.Backend(npu.ModelOptions(chunk=128, context=1024))
+        att = be.attention(qh, kh, d, scale)
+        rng = np.random.default_rng(11)
+        k_all = np.zeros((0, kh, d), np.float16)
+        v_all = np.zeros((0, kh, d), np.float16)
+        pos = 0
+        outs = []
+        for step, rows in enumerate((128, 128, 44, 1, 1, 3, 5, 1)):
+            flag = order[step % len(order)]
+            print(f"order={order} step={step} rows={rows} HM_HOST_FLAG={flag}", flush=True)
+            q = rng.standard_normal((rows, qh, d)).astype(np.float32)
+            k = rng.standard_normal((rows, kh, d)).astype(np.float32)
+            v = rng.standard_normal((rows, kh, d)).astype(np.float32)
+            out = np.full((rows, qh, d), np.nan, np.float32)
+            with D.plan_switch("HM_HOST_FLAG", flag):
+                att.run(q, k, v, out, rows, pos)
+            k_all = np.concatenate([k_all, k.astype(np.float16)])
+            v_all = np.concatenate([v_all, v.astype(np.float16)])
+            want = oracle.attention(heads_major(q.astype(np.float16)), heads_major(k_all), heads_major(v_all),
+                                    float(np.float32(scale)), pos, True)
+            close(heads_major(out), want)
+            outs.append(out)
+            pos += rows
+        assert att.info().length == pos
+        results[order] = outs
+    a, b = results.values()
+    assert all(np.array_equal(x, y) for x, y in zip(a, b))
