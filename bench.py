@@ -10,7 +10,7 @@ Secondary workloads (same JSON line, "secondary"): M=4 decode, the M=4096
 W8A8/W4A8 prefill projection set x36 + lm_head (int8 TOPS), the M=512 FFN
 block x36, the M=128 W8A8 up projection, the 35B-A3B-class MoE at T=512
 and T=1, the attention lines, and the PCIe-inclusive rates of the reference's
-host-buffer signatures (decode set and M=128 up projection).
+host-buffer signatures (decode set, M=128 up projection, decode attention).
 
 Timing (every workload): the step runs eagerly (host launches between two
 synchronizations) and as a HIP graph replay (checked bit-exact against eager
@@ -693,15 +693,57 @@ def run_host_abi(layers=4, reps=20):
     for _ in range(reps * 5):
         up.run(xu, yu, 128)
     us_up = (time.perf_counter() - t0) * 1e6 / (reps * 5)
+    # Decode attention through the reference's host-buffer calls (as
+    # Attention::run makes them: rk_npu_attention_f16_cache_append of the
+    # token's K/V row, then rk_npu_attention_f16_run of its query), 32 query
+    # heads over 8 KV heads, d = 128, at 4000 cached rows (loaded through the
+    # host mirror's prefill chunks).
+    att_backend = npu.Backend(npu.ModelOptions(chunk=256, context=4224))
+    att = att_backend.attention(32, 8, 128, 128 ** -0.5)
+    pos = 0
+    while pos < 4000:
+        rows = min(250, 4000 - pos)
+        kv = g.standard_normal((rows, 8, 128)).astype(np.float32)
+        att.run(g.standard_normal((rows, 32, 128)).astype(np.float32), kv, kv, np.empty((rows, 32, 128), np.float32),
+                rows, pos)
+        pos += rows
+    # the two C calls per step on fp16 bits packed beforehand, as the
+    # reference's caller hands them over (no Python-side conversion timed)
+    from open_rknpu2_lm_infer_amd import _ffi as F_
+    Lh = F_.lib()
+    qa = g.standard_normal((32, 1, 128)).astype(np.float16).view(np.uint16)
+    ka = g.standard_normal((8, 1, 128)).astype(np.float16).view(np.uint16)
+    oa = np.empty((32, 1, 128), np.float32)
+    ws_raw, cache_raw, ctx_raw = att_backend._attention.workspace.raw, att.cache.raw, att_backend.ctx
+    steps = 100
+
+    def att_step(p):
+        npu.check(Lh.rk_npu_attention_f16_cache_append(ctx_raw, cache_raw, ka.ctypes.data, ka.ctypes.data, 1),
+                  "append")
+        npu.check(Lh.rk_npu_attention_f16_run(ctx_raw, ws_raw, cache_raw, qa.ctypes.data, 1, p, oa.ctypes.data,
+                                              None, None), "run")
+
+    for i in range(8):
+        att_step(pos + i)
+    t0 = time.perf_counter()
+    for i in range(steps):
+        att_step(pos + 8 + i)
+    us_att = (time.perf_counter() - t0) * 1e6 / steps
+    kv_bytes = 2 * 8 * 128 * 2 * (pos + 8 + steps // 2)  # K and V rows read per step (mean length)
+    del att, att_backend
     res = [{"workload": f"host-buffer C ABI (rk_npu_w4a8_run_f32 / _run_swiglu_f32, f32 A and C in host memory): "
                         f"decode M=1 W4A8 set, {layers} layers",
             "value": round(bytes_layer / (us_layer * 1e-6) / 1e9, 1), "unit": "GB/s", "us_per_layer": round(us_layer, 2),
             "note": "PCIe-inclusive, one synchronization per call"},
            {"workload": "host-buffer C ABI (rk_npu_f32i8f32_run_dynamic): W8A8 linear M=128 K=2560 N=9728",
             "value": round(2.0 * 128 * H * F / (us_up * 1e-6) / 1e12, 2), "unit": "TOPS", "us_per_call": round(us_up, 2),
-            "note": "PCIe-inclusive: 1.3 MB of f32 A in, 5.0 MB of f32 C out per call"}]
+            "note": "PCIe-inclusive: 1.3 MB of f32 A in, 5.0 MB of f32 C out per call"},
+           {"workload": "host-buffer C ABI (rk_npu_attention_f16_cache_append + rk_npu_attention_f16_run): decode "
+                        "attention, GQA 32/8 heads, d=128, one token appended and attended at ~4000 cached rows",
+            "value": round(kv_bytes / (us_att * 1e-6) / 1e9, 1), "unit": "GB/s", "us_per_layer": round(us_att, 2),
+            "note": "K/V bytes read per step over the wall time of the two host calls (PCIe-inclusive)"}]
     log(f"[bench] host ABI: {res[0]['value']} GB/s decode ({us_layer:.1f} us/layer), "
-        f"{res[1]['value']} TOPS up M=128 ({us_up:.1f} us/call)")
+        f"{res[1]['value']} TOPS up M=128 ({us_up:.1f} us/call), attention {us_att:.1f} us/layer")
     return res
 
 
@@ -2022,7 +2064,11 @@ def main():
             host[1]["cpu_baseline"] = dict(up["cpu_baseline"], note="the same work as the M=128 up line's sample")
         secondary.extend(host)
         secondary.extend(run_moe(torch, ctx, max(4, args.steps // 2), 2, want_cpu=cpu))
-        secondary.extend(run_attention(torch, ctx, max(4, args.steps // 2), want_cpu=cpu))
+        attn = run_attention(torch, ctx, max(4, args.steps // 2), want_cpu=cpu)
+        secondary.extend(attn)
+        if cpu and attn and attn[0].get("cpu_baseline"):
+            host[2]["cpu_baseline"] = dict(attn[0]["cpu_baseline"],
+                                           note="the resident attention decode line's sample (the same attention)")
     for s in secondary:
         s.pop("kernels", None)
         if "roofline" in s:
