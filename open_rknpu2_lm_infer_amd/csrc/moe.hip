@@ -485,7 +485,7 @@ static int enqueue_moe(MoeWork* ws, const MoeBank* b, int rows, const float* inp
     G.N_pad = b->ggu.N_pad;
     G.half = b->ggu.half;
     G.tiles_n = b->ggu.N_pad / MOE_BN;
-    launch_moe_gemm<4, EPI_SWIGLU_MAX>(G, max_tiles * G.tiles_n, s, A);
+    launch_moe_gemm<4, EPI_SWIGLU_MAX>(G, round_up(max_tiles, 8) * G.tiles_n, s, A);
 
     rc = enqueue_quant(ws->mws, ws->mws->a_f32, DT_F32, ws->inter, A, QUANT_MOE,
                        RowMax{reinterpret_cast<const float*>(ws->mws->rowmax), 1}, nullptr, s, ws->counts);
@@ -507,9 +507,9 @@ static int enqueue_moe(MoeWork* ws, const MoeBank* b, int rows, const float* inp
     G.half = b->gdn.half;
     G.tiles_n = b->gdn.N_pad / MOE_BN;
     if (b->dn_bits == 8)
-        launch_moe_gemm<8, EPI_PLAIN>(G, max_tiles * G.tiles_n, s, A);
+        launch_moe_gemm<8, EPI_PLAIN>(G, round_up(max_tiles, 8) * G.tiles_n, s, A);
     else
-        launch_moe_gemm<4, EPI_PLAIN>(G, max_tiles * G.tiles_n, s, A);
+        launch_moe_gemm<4, EPI_PLAIN>(G, round_up(max_tiles, 8) * G.tiles_n, s, A);
     if (hipGetLastError() != hipSuccess) return RK_NPU_ERR_DEVICE;
     }
 

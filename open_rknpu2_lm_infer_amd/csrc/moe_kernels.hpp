@@ -169,7 +169,19 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void moe_gemm_kernel(MoeGemmParam
     using C = TileCfg<BM, BN, WGM, WGN, BITS>;
     __shared__ __attribute__((aligned(16))) uint8_t smem[C::SMEM];
     __shared__ int s_rows[BM];
+#ifndef MOE_XCD_ORDER
+#define MOE_XCD_ORDER 1
+#endif
+#if MOE_XCD_ORDER
+    // Blocks are dealt to the 8 XCDs round-robin: XCD x = block % 8 takes the
+    // row tiles x, x + 8, ..., all N-tiles of one row tile in a row, so the
+    // tile's activation rows are fetched into that XCD's L2 once and shared
+    // by its N-tiles (the grid is 8 * ceil(max tiles / 8) * tiles_n blocks).
+    const int i = blockIdx.x >> 3;
+    const int t = (blockIdx.x & 7) + 8 * (i / P.tiles_n), tn = i % P.tiles_n;
+#else
     const int t = blockIdx.x / P.tiles_n, tn = blockIdx.x % P.tiles_n;
+#endif
     if (t >= P.counts[1]) return;
     const int4 tile = P.tiles[t];
     const int e = tile.x, begin = tile.y, end = tile.z;
