@@ -269,6 +269,24 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnParams P) {
 // 4(l/16)..+3 of column l%16.
 constexpr float ATTN_LAZY = 8.0f;
 
+// Max / sum over the 4 lanes l % 16 + 16 j (a query row's lanes in the
+// accumulator layout), in each of them: v_permlane16_swap exchanges odd with
+// even 16-lane rows and v_permlane32_swap the upper with the lower half, so
+// each swap's two results are a lane pair 16 (then 32) apart, without an LDS
+// round trip.
+__device__ __forceinline__ float max_rows4(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float sum_rows4(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 template <int D>
 __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnParams P) {
     typedef _Float16 h8 __attribute__((ext_vector_type(8)));
@@ -427,8 +445,7 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnParams P) {
 #pragma unroll
         for (int cb = 0; cb < 4; ++cb)
             tmax = fmaxf(fmaxf(tmax, fmaxf(sacc[cb][0], sacc[cb][1])), fmaxf(sacc[cb][2], sacc[cb][3]));
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+        tmax = max_rows4(tmax);
         const float tm = tmax * c;
         const bool grow = tm > mrun + ATTN_LAZY;
         if (__builtin_expect(__builtin_amdgcn_ballot_w64(grow) != 0, 0)) {  // (uniform, rare after the first tile)
@@ -469,8 +486,7 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnParams P) {
         }
     }
     float l = lpart;
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
+    l = sum_rows4(l);
     if (!row_ok) return;
     const int h = g * G + rr / P.m, qr = rr % P.m;
     if (P.splits == 1) {
