@@ -165,6 +165,9 @@ int rk_npu_hip_inject_alloc_failures(int count);
  *                    writes C and a completion word into the stage, which
  *                    the CPU polls; 0: copies in and out and a wait on the
  *                    stream (HM_HOST_SPIN), as larger calls always do
+ *   HM_HOST_POLL     microseconds a host-buffer call on the kernel path
+ *                    polls its completion word before it waits on its
+ *                    stream instead (2000; 0: after the first 256 polls)
  *   HM_HOST_SPIN     0: a host-buffer call that waits on its stream does so
  *                    in hipStreamSynchronize; 1: by polling its stream
  *                    (slower here)

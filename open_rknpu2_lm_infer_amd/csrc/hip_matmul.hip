@@ -306,7 +306,7 @@ static const int kBN[] = {256, 128, 128, 128, 128, 256};
 // variable, read once when the library first plans a launch; afterwards only
 // rk_npu_hip_set_switch changes it, so no launch reads the environment.
 enum SwitchId { SW_GEMM_VARIANT, SW_SPLITS, SW_FORCE_GEMM, SW_GEMV_QW, SW_GEMV_SPLITS, SW_FFN_FUSED, SW_FFN_SPIN,
-                SW_GEMV_PREQ, SW_HOST_SPIN, SW_GEMV_COMBINE, SW_HOST_FLAG, SW_COUNT };
+                SW_GEMV_PREQ, SW_HOST_SPIN, SW_GEMV_COMBINE, SW_HOST_FLAG, SW_HOST_POLL, SW_COUNT };
 struct SwitchDef {
     const char* name;
     int fallback;
@@ -314,7 +314,7 @@ struct SwitchDef {
 static const SwitchDef kSwitches[SW_COUNT] = {
     {"HM_GEMM_VARIANT", -1}, {"HM_SPLITS", 0},         {"HM_FORCE_GEMM", 0}, {"HM_GEMV_QW", -1},
     {"HM_GEMV_SPLITS", 0},   {"HM_FFN_FUSED", 0},      {"HM_FFN_SPIN", 1 << 16}, {"HM_GEMV_PREQ", -1},
-    {"HM_HOST_SPIN", 0},     {"HM_GEMV_COMBINE", 1},   {"HM_HOST_FLAG", 1}};
+    {"HM_HOST_SPIN", 0},     {"HM_GEMV_COMBINE", 1},   {"HM_HOST_FLAG", 1},       {"HM_HOST_POLL", 2000}};
 
 static std::atomic<int>* switch_table() {
     static std::atomic<int> table[SW_COUNT];
@@ -1074,12 +1074,12 @@ float* host_stage(Workspace* ws, size_t bytes) { return static_cast<float*>(stag
 // 24.1 against copies and hipStreamSynchronize; with the copies kept for
 // the upload only the download side changes and down takes 35.8 (the next
 // call's copy engine then waits on the compute queue's completion). The
-// poll gives way to hipStreamSynchronize after HOST_POLL_US, which also
-// reports a failed stream. Larger calls copy through the stage (or pageable
+// poll gives way to hipStreamSynchronize after HM_HOST_POLL microseconds
+// (2000; tests set 0 to take that way every time), which also reports a
+// failed stream. Larger calls copy through the stage (or pageable
 // memory) and wait on the stream (HM_HOST_SPIN). HM_HOST_FLAG=0 makes every
 // call take the copies.
 constexpr size_t HOST_SMALL = 64u << 10;
-constexpr double HOST_POLL_US = 2000.0;
 
 // Segments of a fetch: up to three (source in the stage, device destination,
 // 16-byte pieces); every source and destination is 16-byte aligned and
@@ -1171,9 +1171,9 @@ bool stage_download(HostStage& stg, bool small, void* st, void* C, const void* s
         (void)hipStreamSynchronize(s);
         return false;
     }
-    const double t0 = now_us();
+    const double t0 = now_us(), limit = (double)switch_value(SW_HOST_POLL);
     for (unsigned n = 1; __atomic_load_n(stg.done, __ATOMIC_ACQUIRE) != seq; ++n) {
-        if ((n & 255) == 0 && now_us() - t0 > HOST_POLL_US) {
+        if ((n & 255) == 0 && now_us() - t0 >= limit) {
             if (hipStreamSynchronize(s) != hipSuccess || __atomic_load_n(stg.done, __ATOMIC_ACQUIRE) != seq)
                 return false;
             break;

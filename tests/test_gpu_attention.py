@@ -315,3 +315,16 @@ def test_host_transfer_paths_agree(flag_order):
         results[order] = outs
     a, b = results.values()
     assert all(np.array_equal(x, y) for x, y in zip(a, b))
+
+
+def test_host_poll_fallback_appends_and_runs():
+    """HM_HOST_POLL=0: the append and run calls stop polling their
+    completion words early and wait on their streams; decode steps after a
+    prefill chunk still match the oracle within TOL."""
+    from open_rknpu2_lm_infer_amd import device as D
+    be = npu.Backend(npu.ModelOptions(chunk=128, context=512))
+    qh, kh, d = 32, 8, 128
+    scale = d ** -0.5
+    att = be.attention(qh, kh, d, scale)
+    with D.plan_switch("HM_HOST_POLL", 0):
+        run_sequence(att, qh, kh, d, (100, 1, 1, 2), np.random.default_rng(12), scale)

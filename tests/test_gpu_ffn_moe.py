@@ -355,3 +355,33 @@ def test_host_calls_kernel_path_and_copies(flag_order):
                 moe.run(x, ids, w, out, rows)
                 ref = oracle.moe([(g.codes, g.scales) for g in gate], [(d.codes, d.scales) for d in down], x, ids, w)
                 assert np.array_equal(out, ref), (rows, flag)
+
+
+def test_host_calls_poll_fallback():
+    """With HM_HOST_POLL=0 a kernel-path host call stops polling its
+    completion word after the first 256 polls and waits on its stream, then
+    reads the word (set by then): the results equal the oracle's bit for bit
+    (linear W4 at 1 row, the fused FFN at M=1, the MoE at one token)."""
+    from open_rknpu2_lm_infer_amd import device as D
+    backend = npu.Backend(npu.ModelOptions(chunk=64))
+    codes, scales = R.weights(9, "hostpoll", 4, 2560, 384)
+    linear = backend.load(npu.QuantMatrix(4, 2560, 384, codes, scales))
+    ffn = FFN(backend, 256, 384, 1, 8, "hostpoll-ffn")
+    h, inter, experts, top = 256, 96, 16, 4
+    gate, down = moe_bank(h, inter, experts, 8, "hostpoll-moe")
+    moe = backend.load_moe(gate, down, top)
+    with D.plan_switch("HM_HOST_FLAG", 1), D.plan_switch("HM_HOST_POLL", 0):
+        for rep in range(3):
+            print(f"HM_HOST_POLL=0 rep {rep}", flush=True)
+            x = R.activations(9, f"hostpoll-x{rep}", 1, 2560)
+            out = np.full((1, 384), np.nan, np.float32)
+            linear.run(x, out, 1)
+            assert np.array_equal(out, oracle.linear(codes, scales, x))
+            xf = R.activations(9, f"hostpoll-ffn-x{rep}", 1, 256)
+            assert np.array_equal(ffn.run(xf), oracle.ffn(ffn.gc, ffn.gs, ffn.dc, ffn.ds, xf))
+            xm = R.activations(9, f"hostpoll-moe-x{rep}", 1, h)
+            ids, w = routed(1, experts, top, f"hostpoll-moe-r{rep}")
+            om = np.full((1, h), np.nan, np.float32)
+            moe.run(xm, ids, w, om, 1)
+            ref = oracle.moe([(g.codes, g.scales) for g in gate], [(d.codes, d.scales) for d in down], xm, ids, w)
+            assert np.array_equal(om, ref)
