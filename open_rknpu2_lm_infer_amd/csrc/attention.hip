@@ -856,7 +856,7 @@ static bool cache_put_staged(AttnCache* c, const void* k, const void* v, int row
         c->stream = nullptr;
         return false;
     }
-    void* st = stage_reserve(c->hs, voff + each, c->stream);
+    void* st = stage_reserve(c->hs, voff + each);
     if (!st) return false;
     std::memcpy(st, k, each);
     std::memcpy(static_cast<uint8_t*>(st) + voff, v, each);
@@ -1017,7 +1017,7 @@ static int run_host(rk_npu_attention_f16_workspace* workspace, rk_npu_attention_
         w->fence.wait(w->stream) != hipSuccess) {
         rc = RK_NPU_ERR_DEVICE;
     } else {
-        st = stage_reserve(w->hs, std::max(qb, ob), w->stream);
+        st = stage_reserve(w->hs, std::max(qb, ob));
         small = stage_small(w->hs, st, qb, ob);
         const HostSeg seg{q, w->q, qb, 0};
         if (!stage_upload(w->hs, small, st, &seg, 1, w->stream) ||

@@ -1029,11 +1029,11 @@ constexpr size_t HOST_STAGE_CAP = 8u << 20;
 
 // The stage is coherent (fine-grained) pinned memory, so the copy kernel's
 // stores and its completion word reach host memory without a cache flush.
-void* stage_reserve(HostStage& st, size_t bytes, hipStream_t s) {
+void* stage_reserve(HostStage& st, size_t bytes) {
     if (bytes == 0 || bytes > HOST_STAGE_CAP) return nullptr;
     if (st.bytes < bytes) {
         if (st.host) {
-            if (s) (void)hipStreamSynchronize(s);  // (a previous call's copy kernel may still be ending)
+            if (st.last) (void)hipStreamSynchronize(st.last);  // (a previous call's copy kernel may still be ending)
             (void)hipHostFree(st.host);
         }
         st = HostStage{};
@@ -1061,7 +1061,7 @@ void stage_release(HostStage& st) {
     st = HostStage{};
 }
 
-float* host_stage(Workspace* ws, size_t bytes) { return static_cast<float*>(stage_reserve(ws->hs, bytes, ws->stream)); }
+float* host_stage(Workspace* ws, size_t bytes) { return static_cast<float*>(stage_reserve(ws->hs, bytes)); }
 
 // Host-buffer transfers. A small call (input and output each at most
 // HOST_SMALL bytes, and a stage) stays on the compute queue from start to
@@ -1114,6 +1114,7 @@ bool stage_small(const HostStage& st, const void* p, size_t in_bytes, size_t out
 
 bool stage_upload(HostStage& stg, bool small, void* st, const HostSeg* segs, int n, hipStream_t s) {
     if (n < 1 || n > 3) return false;
+    if (st) stg.last = s;
     if (!st) {
         for (int k = 0; k < n; ++k)
             if (hipMemcpyAsync(segs[k].dst, segs[k].src, segs[k].bytes, hipMemcpyHostToDevice, s) != hipSuccess)
@@ -1154,6 +1155,7 @@ hipError_t host_wait(hipStream_t s) {
 }
 
 bool stage_download(HostStage& stg, bool small, void* st, void* C, const void* src, size_t bytes, hipStream_t s) {
+    if (st) stg.last = s;
     if (!small) {
         if (bytes == 0) return host_wait(s) == hipSuccess;
         if (!st)
@@ -1529,12 +1531,12 @@ int rk_npu_w4a8_run_ffn_f32(rk_npu_w4a8_workspace* gate_up_workspace, const rk_n
     if (hipSetDevice(device_of(gws->domain)) != hipSuccess) return RK_NPU_ERR_DEVICE;
     const int M = gws->M, H = gw->g.K;
     hipStream_t s = gws->stream;
-    float* st_in = host_stage(gws, (size_t)M * H * 4);
-    float* st_out = host_stage(dws, (size_t)M * H * 4);
-    const bool small =
-        stage_small(gws->hs, st_in, (size_t)M * H * 4, 0) && stage_small(dws->hs, st_out, 0, (size_t)M * H * 4);
+    // A in and C out through the gate_up workspace's stage (both M x H f32),
+    // on that workspace's stream, which runs the whole call
+    float* st = host_stage(gws, (size_t)M * H * 4);
+    const bool small = stage_small(gws->hs, st, (size_t)M * H * 4, (size_t)M * H * 4);
     const HostSeg seg{A, gws->a_f32, (size_t)M * H * 4, 0};
-    if (!stage_upload(gws->hs, small, st_in, &seg, 1, s)) {
+    if (!stage_upload(gws->hs, small, st, &seg, 1, s)) {
         (void)hipStreamSynchronize(s);
         return RK_NPU_ERR_DEVICE;
     }
@@ -1546,7 +1548,7 @@ int rk_npu_w4a8_run_ffn_f32(rk_npu_w4a8_workspace* gate_up_workspace, const rk_n
     }
     if (timings && hipStreamSynchronize(s) != hipSuccess) return RK_NPU_ERR_DEVICE;
     const double t2 = now_us();
-    if (!stage_download(dws->hs, small, st_out, C, dws->c_f32, (size_t)M * H * 4, s)) return RK_NPU_ERR_DEVICE;
+    if (!stage_download(gws->hs, small, st, C, dws->c_f32, (size_t)M * H * 4, s)) return RK_NPU_ERR_DEVICE;
     rc = ffn_take_error(dws);
     if (rc != RK_NPU_OK) return rc;
     if (timings) {

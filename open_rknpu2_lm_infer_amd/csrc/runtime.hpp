@@ -79,10 +79,12 @@ struct HostStage {
     unsigned* done = nullptr;
     unsigned* done_dev = nullptr;
     unsigned seq = 0;
+    hipStream_t last = nullptr;  // the stream of the last transfer through the stage
 };
-// The stage's data (at least `bytes`), growing it after stream `s` (the
-// stage's user) has finished with the old one.
-void* stage_reserve(HostStage& st, size_t bytes, hipStream_t s);
+// The stage's data (at least `bytes`), growing it after the stream of its
+// last transfer has finished with the old one. A stage is only used on its
+// owner's stream; stage_release expects that stream to be idle.
+void* stage_reserve(HostStage& st, size_t bytes);
 void stage_release(HostStage& st);
 
 struct Workspace {
