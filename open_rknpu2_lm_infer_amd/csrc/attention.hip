@@ -39,7 +39,7 @@ constexpr uint32_t MAGIC_ATTN_WORK = 0x57414841u;
 constexpr int ATTN_KT = 64;              // keys per tile
 constexpr int ATTN_MAX_SPLITS = 256;     // key splits per (KV head, row tile)
 // Partial rows a workspace holds: plan_attention launches at most 2048
-// blocks when it splits the keys, each with at most 64 query rows (head_dim
+// blocks when it splits the keys, each with at most 128 query rows (head_dim
 // 64 and 128, MFMA tiles) or 16 (head_dim 256).
 static inline size_t attn_partial_rows(int head_dim) { return (size_t)2048 * (head_dim <= 128 ? 64 : 16); }
 
@@ -241,7 +241,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnParams P) {
 }
 
 // Matrix-core variant for 16 or more query rows per KV head (head_dim 64 or
-// 128). Block = 4 waves, each owning 16 query rows of one KV head, over
+// 128). Block = NW waves (4 or 8), each owning 16 query rows of one KV head, over
 // 64-key tiles of its key split; the K/V tile is shared by the block (K
 // row-major, V transposed in LDS; the next tile's loads are in flight in
 // registers meanwhile). Per tile, with v_mfma_f32_16x16x32_f16 (fp16
@@ -287,8 +287,8 @@ __device__ __forceinline__ float sum_rows4(float v) {
     return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
-template <int D>
-__global__ __launch_bounds__(256) void attn_mfma_kernel(AttnParams P) {
+template <int D, int NW>
+__global__ __launch_bounds__(64 * NW) void attn_mfma_kernel(AttnParams P) {
     typedef _Float16 h8 __attribute__((ext_vector_type(8)));
     typedef _Float16 hh2 __attribute__((ext_vector_type(2)));
     typedef float f4 __attribute__((ext_vector_type(4)));
@@ -297,9 +297,10 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnParams P) {
     constexpr int KP = D + 8, VP = KT + 4;  // row pads: fragment reads of 16 lanes hit distinct banks
     constexpr int KPIECES = KT * (D / 8);        // 16-byte K pieces per tile
     constexpr int VPIECES = (KT / 4) * (D / 8);  // 4 keys x 8 dims V pieces per tile
-    constexpr int KPT = KPIECES / 256;
+    constexpr int NT = 64 * NW;
+    constexpr int KPT = KPIECES / NT;
     static_assert(D == 64 || D == 128, "MFMA attention: head_dim 64 or 128");
-    static_assert(KT == 64 && KPIECES % 256 == 0 && VPIECES <= 256, "tile shape");
+    static_assert(KT == 64 && KPIECES % NT == 0 && VPIECES <= NT, "tile shape");
     __shared__ __attribute__((aligned(16))) __half ks[KT][KP];
     __shared__ __attribute__((aligned(16))) __half vt[D][VP];
     const int split = blockIdx.x, rt = blockIdx.y, g = blockIdx.z;
@@ -312,7 +313,7 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnParams P) {
     const __half* kbase = P.k + (size_t)g * P.cap * D;
     const __half* vbase = P.v + (size_t)g * P.cap * D;
     // this lane's query row, its key limit and Q fragments
-    const int rr = rt * 64 + wave * 16 + lo;
+    const int rr = rt * (16 * NW) + wave * 16 + lo;
     const bool row_ok = rr < R;
     int lim = 0;
     if (row_ok) {
@@ -344,7 +345,7 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnParams P) {
     unsigned koff[KPT], voff[4];
 #pragma unroll
     for (int t = 0; t < KPT; ++t) {
-        const int i = tid + 256 * t;
+        const int i = tid + NT * t;
         koff[t] = (unsigned)((i / (D / 8)) * D + (i % (D / 8)) * 8) * 2u;
     }
 #pragma unroll
@@ -363,7 +364,7 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnParams P) {
         } else {  // keys past the split read the tile's first row (zeroed in store)
 #pragma unroll
             for (int t = 0; t < KPT; ++t) {
-                const int key = kb + (tid + 256 * t) / (D / 8);
+                const int key = kb + (tid + NT * t) / (D / 8);
                 kr[t] = *reinterpret_cast<const v4u*>(kt + (key < k1 ? koff[t] : 0u));
             }
             if (vthread) {
@@ -379,14 +380,14 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnParams P) {
         if (kb + KT > k1) {  // (block-uniform) zero the keys past the split
 #pragma unroll
             for (int t = 0; t < KPT; ++t)
-                if (kb + (tid + 256 * t) / (D / 8) >= k1) kr[t] = v4u{0u, 0u, 0u, 0u};
+                if (kb + (tid + NT * t) / (D / 8) >= k1) kr[t] = v4u{0u, 0u, 0u, 0u};
 #pragma unroll
             for (int t = 0; t < 4; ++t)
                 if (kb + 4 * vj + t >= k1) vr[t] = v4u{0u, 0u, 0u, 0u};
         }
 #pragma unroll
         for (int t = 0; t < KPT; ++t) {
-            const int i = tid + 256 * t;
+            const int i = tid + NT * t;
             *reinterpret_cast<v4u*>(&ks[i / (D / 8)][(i % (D / 8)) * 8]) = kr[t];
         }
         if (vthread) {
@@ -877,15 +878,18 @@ static bool cache_put_staged(AttnCache* c, const void* k, const void* v, int row
 }
 
 struct AttnPlan {
-    bool mfma;  // attn_mfma_kernel (64-row tiles) instead of attn_split_kernel
+    bool mfma;  // attn_mfma_kernel (64- or 128-row tiles) instead of attn_split_kernel
     int rt, row_tiles, splits, keys_per_split, key_end;
 };
 
-// Rows per tile: 4 when a KV head has at most 4 query rows (decode: one row
-// of a 4-head group), else 16. Keys: enough splits that about 512 blocks run
-// (each split a whole number of 64-key tiles); with more than one split the
-// blocks write partials, at most 512 + row_tiles * kv_heads <= 1024 of them.
-// Override for measurement: HM_ATTN_BLOCKS (blocks the key splits aim at).
+// Rows per tile: VALU kernel 4 when a KV head has at most 4 query rows
+// (decode: one row of a 4-head group), else 16; MFMA kernel (16 or more rows
+// per KV head) 64, or 128 from 128 rows on. Keys: enough splits that about
+// 512 blocks run (256 of the 8-wave 128-row blocks, one per CU), each split
+// a whole number of 64-key tiles; with more than one split the blocks write
+// partials (enqueue_attention checks that the workspace holds them).
+// Overrides for measurement: HM_ATTN_BLOCKS, HM_ATTN_WIDE_BLOCKS (the block
+// counts the key splits aim at).
 static int attn_env(const char* name, int fallback) {
     const char* v = std::getenv(name);
     return v ? std::atoi(v) : fallback;
@@ -896,13 +900,17 @@ static AttnPlan plan_attention(const rk_npu_attention_f16_config& c, int rows, i
     const int G = c.query_heads / c.kv_heads, R = G * rows;
     p.mfma = R >= 16 && (c.head_dim == 64 || c.head_dim == 128);
     static const int env_blocks = attn_env("HM_ATTN_BLOCKS", 512);
-    p.rt = p.mfma ? 64 : (R <= 4 ? 4 : 16);
+    static const int env_wide = attn_env("HM_ATTN_WIDE_BLOCKS", 256);
+    // 128 or more rows per KV head: 8-wave blocks of 128 rows, one per CU
+    // (a K/V tile shared by twice the waves, and the two waves on a SIMD
+    // belong to one block), aiming at HM_ATTN_WIDE_BLOCKS blocks
+    p.rt = p.mfma ? (R >= 128 ? 128 : 64) : (R <= 4 ? 4 : 16);
     p.row_tiles = (R + p.rt - 1) / p.rt;
     p.key_end = (c.mask_mode == RK_NPU_ATTENTION_F16_CAUSAL) ? std::min(len, pos + rows) : len;
     const int kt = c.head_dim == 256 ? 32 : ATTN_KT;  // keys per tile of the kernel
     const int tiles = (p.key_end + kt - 1) / kt;
     const int base = p.row_tiles * c.kv_heads;
-    const int target = std::min(std::max(env_blocks, 64), 1024);
+    const int target = std::min(std::max(p.rt == 128 ? env_wide : env_blocks, 64), 1024);
     int want = base >= target ? 1 : (target + base - 1) / base;
     want = std::max(1, std::min(std::min(want, tiles), ATTN_MAX_SPLITS));
     const int tiles_per_split = (tiles + want - 1) / want;
@@ -954,9 +962,15 @@ static int enqueue_attention(AttnWork* w, AttnCache* c, const __half* q, int row
         launch_attn<DD, 16>(P, pl, cfg.kv_heads, s);
     const dim3 grid(pl.splits, pl.row_tiles, cfg.kv_heads);
     if (pl.mfma && D == 64) {
-        hipLaunchKernelGGL(attn_mfma_kernel<64>, grid, dim3(256), 0, s, P);
+        if (pl.rt == 128)
+            hipLaunchKernelGGL((attn_mfma_kernel<64, 8>), grid, dim3(512), 0, s, P);
+        else
+            hipLaunchKernelGGL((attn_mfma_kernel<64, 4>), grid, dim3(256), 0, s, P);
     } else if (pl.mfma && D == 128) {
-        hipLaunchKernelGGL(attn_mfma_kernel<128>, grid, dim3(256), 0, s, P);
+        if (pl.rt == 128)
+            hipLaunchKernelGGL((attn_mfma_kernel<128, 8>), grid, dim3(512), 0, s, P);
+        else
+            hipLaunchKernelGGL((attn_mfma_kernel<128, 4>), grid, dim3(256), 0, s, P);
     } else if (D == 64) {
         HM_ATTN(64)
     } else if (D == 128) {
