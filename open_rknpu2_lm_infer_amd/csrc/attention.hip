@@ -258,7 +258,9 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnParams P) {
 //   O^T += V^T P^T  A = V^T rows from LDS, B = the weights as they lie (the
 //                 accumulator layout of S^T is the B layout of P^T once each
 //                 lane's 8 k-slots name keys {4(l/16)..+3, 16+4(l/16)..+3} of
-//                 a 32-key step, which A reads to match),
+//                 a 32-key step, which A reads to match: V^T rows keep each
+//                 32-key chunk's 4-key groups in the order 0 4 1 5 2 6 3 7,
+//                 so those 8 keys are one 16-byte read),
 // so a lane's O^T accumulators all belong to its own query row and every
 // rescale is lane-local; each lane keeps a partial sum of its own weights
 // (v_dot2 against ones: the fp16 weights summed exactly in f32), added over
@@ -294,7 +296,8 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_kernel(AttnParams P) {
     typedef float f4 __attribute__((ext_vector_type(4)));
     typedef unsigned u2 __attribute__((ext_vector_type(2)));
     constexpr int KT = ATTN_KT, KS = D / 32, NB = D / 16;
-    constexpr int KP = D + 8, VP = KT + 4;  // row pads: fragment reads of 16 lanes hit distinct banks
+    // row pads: fragment reads of 16 lanes hit distinct banks
+    constexpr int KP = D + 8, VP = KT + 8;
     constexpr int KPIECES = KT * (D / 8);        // 16-byte K pieces per tile
     constexpr int VPIECES = (KT / 4) * (D / 8);  // 4 keys x 8 dims V pieces per tile
     constexpr int NT = 64 * NW;
@@ -402,7 +405,11 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_kernel(AttnParams P) {
                     x[0] = (vr[0][cw] & 0xffffu) | (vr[1][cw] << 16);
                     x[1] = (vr[2][cw] & 0xffffu) | (vr[3][cw] << 16);
                 }
-                *reinterpret_cast<u2*>(&vt[vc * 8 + e][4 * vj]) = x;
+                // within each 32-key chunk the 4-key groups lie in the order
+                // 0 4 1 5 2 6 3 7, so a lane's 8 k-slots (groups hi, hi + 4)
+                // are one 16-byte read
+                const int lg = vj & 7, pos = lg < 4 ? 2 * lg : 2 * lg - 7;
+                *reinterpret_cast<u2*>(&vt[vc * 8 + e][32 * (vj >> 3) + 4 * pos]) = x;
             }
         }
     };
@@ -478,9 +485,7 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_kernel(AttnParams P) {
             h8 va[NB];
 #pragma unroll
             for (int n = 0; n < NB; ++n) {
-                const u2 a0 = *reinterpret_cast<const u2*>(&vt[16 * n + lo][32 * k + 4 * hi]);
-                const u2 a1 = *reinterpret_cast<const u2*>(&vt[16 * n + lo][32 * k + 16 + 4 * hi]);
-                va[n] = __builtin_bit_cast(h8, v4u{a0[0], a0[1], a1[0], a1[1]});
+                va[n] = __builtin_bit_cast(h8, *reinterpret_cast<const v4u*>(&vt[16 * n + lo][32 * k + 8 * hi]));
             }
 #pragma unroll
             for (int n = 0; n < NB; ++n) o[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[n], pb[k], o[n], 0, 0, 0);
