@@ -296,8 +296,10 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_kernel(AttnParams P) {
     typedef float f4 __attribute__((ext_vector_type(4)));
     typedef unsigned u2 __attribute__((ext_vector_type(2)));
     constexpr int KT = ATTN_KT, KS = D / 32, NB = D / 16;
-    // row pads: fragment reads of 16 lanes hit distinct banks
-    constexpr int KP = D + 8, VP = KT + 8;
+    // row pads against LDS bank conflicts in the fragment reads (pads of 16
+    // halves measured fastest: 8 / 8 -> 16 / 16 took the prefill layer
+    // 25.95 -> 24.72 us; 32 or 48 for K, 24 or 32 for V no better)
+    constexpr int KP = D + 16, VP = KT + 16;
     constexpr int KPIECES = KT * (D / 8);        // 16-byte K pieces per tile
     constexpr int VPIECES = (KT / 4) * (D / 8);  // 4 keys x 8 dims V pieces per tile
     constexpr int NT = 64 * NW;
