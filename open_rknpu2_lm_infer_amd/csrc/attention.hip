@@ -599,12 +599,12 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams P) {
 }
 
 // The same combine for few splits (at most 64) over many rows: one wave per
-// row, lane s holds split s's weight; the splits' accumulators are loaded 16
-// at a time (dims lane + 64 j) and each weight is broadcast from its lane.
-template <int D>
+// row, lane s holds split s's weight; the splits' accumulators are loaded B
+// (8 or 16) at a time (dims lane + 64 j) and each weight is broadcast from
+// its lane.
+template <int D, int B>
 __global__ __launch_bounds__(256) void attn_combine_rows_kernel(AttnParams P) {
     constexpr int ND = D / 64;
-    constexpr int B = 16;
     constexpr size_t STRIDE = D + 2;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int rr = blockIdx.x * 4 + wave, g = blockIdx.y;
@@ -994,12 +994,20 @@ static int enqueue_attention(AttnWork* w, AttnCache* c, const __half* q, int row
         const bool by_wave = pl.splits <= 16;
         const dim3 cgrid(by_wave ? (G * rows + 3) / 4 : G * rows, cfg.kv_heads);
         if (by_wave) {
-            if (D == 64)
-                hipLaunchKernelGGL(attn_combine_rows_kernel<64>, cgrid, dim3(256), 0, s, P);
-            else if (D == 128)
-                hipLaunchKernelGGL(attn_combine_rows_kernel<128>, cgrid, dim3(256), 0, s, P);
-            else
-                hipLaunchKernelGGL(attn_combine_rows_kernel<256>, cgrid, dim3(256), 0, s, P);
+            // (splits loaded per batch: 8 when there are at most 8, else 16)
+#define HM_COMB_ROWS(DD)                                                                            \
+    if (pl.splits <= 8)                                                                             \
+        hipLaunchKernelGGL((attn_combine_rows_kernel<DD, 8>), cgrid, dim3(256), 0, s, P);           \
+    else                                                                                            \
+        hipLaunchKernelGGL((attn_combine_rows_kernel<DD, 16>), cgrid, dim3(256), 0, s, P);
+            if (D == 64) {
+                HM_COMB_ROWS(64)
+            } else if (D == 128) {
+                HM_COMB_ROWS(128)
+            } else {
+                HM_COMB_ROWS(256)
+            }
+#undef HM_COMB_ROWS
         } else if (D == 64) {
             hipLaunchKernelGGL(attn_combine_kernel<64>, cgrid, dim3(256), 0, s, P);
         } else if (D == 128) {
