@@ -550,6 +550,15 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams P) {
     const int h = g * G + rr / P.m, qr = rr % P.m;
     const int S = P.splits;
     const float* p0 = P.part + ((size_t)g * P.rows_pad + rr) * S * STRIDE;
+    // the first batch of accumulators is requested with the maxima and sums
+    // (its addresses do not depend on them: one memory round trip)
+    float v[B][ND];
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+        const int sp = min(wave + 4 * u, S - 1);
+#pragma unroll
+        for (int d = 0; d < ND; ++d) v[u][d] = p0[sp * STRIDE + 2 + lane + 64 * d];
+    }
     const float m = tid < S ? p0[tid * STRIDE] : -INFINITY;
     const float l = tid < S ? p0[tid * STRIDE + 1] : 0.0f;
     float mx = group_max<64>(m);
@@ -565,12 +574,13 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams P) {
 #pragma unroll
     for (int d = 0; d < ND; ++d) num[d] = 0.0f;
     for (int s0 = wave; s0 < S; s0 += 4 * B) {
-        float v[B][ND];
+        if (s0 != wave) {
 #pragma unroll
-        for (int u = 0; u < B; ++u) {
-            const int sp = min(s0 + 4 * u, S - 1);
+            for (int u = 0; u < B; ++u) {
+                const int sp = min(s0 + 4 * u, S - 1);
 #pragma unroll
-            for (int d = 0; d < ND; ++d) v[u][d] = p0[sp * STRIDE + 2 + lane + 64 * d];
+                for (int d = 0; d < ND; ++d) v[u][d] = p0[sp * STRIDE + 2 + lane + 64 * d];
+            }
         }
 #pragma unroll
         for (int u = 0; u < B; ++u) {
