@@ -242,30 +242,39 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnParams P) {
 
 // Matrix-core variant for 16 or more query rows per KV head (head_dim 64 or
 // 128). Block = NW waves (4 or 8), each owning 16 query rows of one KV head, over
-// 64-key tiles of its key split; the K/V tile is shared by the block (K
-// row-major, V transposed in LDS; the next tile's loads are in flight in
-// registers meanwhile). Per tile, with v_mfma_f32_16x16x32_f16 (fp16
-// operands, f32 accumulation):
+// 64-key tiles of its key split; the K/V tile is shared by the block. Per
+// tile, with v_mfma_f32_16x16x32_f16 (fp16 operands, f32 accumulation):
 //   S^T = K Q^T   A = K rows from LDS, B = Q fragments held in registers;
 //                 the accumulator gives lane l the raw scores of query row
 //                 l%16 for keys 4(l/16)..+3 of each 16-key block,
-//   softmax       row max over the lane's 16 scores and the 3 other lanes of
-//                 its row; weights p = 2^(s c - m) with c = scale * log2(e)
-//                 and m the running max in those units, rounded to fp16 in
-//                 place; m moves only when a row's max grows by more than
-//                 ATTN_LAZY (so p <= 2^ATTN_LAZY, which fp16 holds), and only
-//                 then are the accumulators and sums rescaled,
-//   O^T += V^T P^T  A = V^T rows from LDS, B = the weights as they lie (the
+//   softmax       weights p = 2^(s c - m) with c = scale * log2(e) and m the
+//                 row's running max in those units, rounded to fp16 in place;
+//                 m moves only when a row's max grows by more than ATTN_LAZY
+//                 (so p <= 2^ATTN_LAZY, which fp16 holds), and only then are
+//                 the accumulators and sums rescaled: each lane compares the
+//                 max of its own 16 scores with that bound, and the row max
+//                 over the row's 4 lanes is formed only when one passes it,
+//   O^T += V^T P^T  A = V^T fragments, B = the weights as they lie (the
 //                 accumulator layout of S^T is the B layout of P^T once each
 //                 lane's 8 k-slots name keys {4(l/16)..+3, 16+4(l/16)..+3} of
-//                 a 32-key step, which A reads to match: V^T rows keep each
-//                 32-key chunk's 4-key groups in the order 0 4 1 5 2 6 3 7,
-//                 so those 8 keys are one 16-byte read),
+//                 a 32-key step, which the A fragments are read to match),
 // so a lane's O^T accumulators all belong to its own query row and every
 // rescale is lane-local; each lane keeps a partial sum of its own weights
 // (v_dot2 against ones: the fp16 weights summed exactly in f32), added over
 // the row's 4 lanes at the end. Masks (causal, keys past the split) apply
 // only on tiles that cross them.
+// Tiles reach LDS in one of two ways:
+//   8 waves (one block per CU): direct global->LDS loads into three tile
+//     buffers, K and V row-major (key, dim) in 16-byte slots permuted within
+//     each row against bank conflicts; tile t + 2 is requested after tile t's
+//     last LDS reads, into the buffer of tile t - 1 (every wave has passed
+//     tile t's barrier, so it is free), one barrier per tile; V^T fragments
+//     come from transposing LDS reads (ds_read_b64_tr_b16);
+//   4 waves (several blocks per CU, where 96 KB of tile buffers would leave
+//     one): the next tile's K/V in registers while this one is used, stored
+//     between two barriers, V transposed on the way in (each 32-key chunk's
+//     4-key groups in the order 0 4 1 5 2 6 3 7, so a lane's 8 k-slots are
+//     one 16-byte read).
 // Operand layouts (16x16x32, wave64): A lane l = row l%16, k-slots
 // 8(l/16)..+7; B lane l = column l%16, same k-slots; C lane l = rows
 // 4(l/16)..+3 of column l%16.
@@ -295,19 +304,28 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_kernel(AttnParams P) {
     typedef _Float16 hh2 __attribute__((ext_vector_type(2)));
     typedef float f4 __attribute__((ext_vector_type(4)));
     typedef unsigned u2 __attribute__((ext_vector_type(2)));
+    typedef short s4 __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) s4 lds_s4;
     constexpr int KT = ATTN_KT, KS = D / 32, NB = D / 16;
-    // row pads against LDS bank conflicts in the fragment reads (pads of 16
-    // halves measured fastest: 8 / 8 -> 16 / 16 took the prefill layer
-    // 25.95 -> 24.72 us; 32 or 48 for K, 24 or 32 for V no better)
-    constexpr int KP = D + 16, VP = KT + 16;
-    constexpr int KPIECES = KT * (D / 8);        // 16-byte K pieces per tile
-    constexpr int VPIECES = (KT / 4) * (D / 8);  // 4 keys x 8 dims V pieces per tile
     constexpr int NT = 64 * NW;
-    constexpr int KPT = KPIECES / NT;
+    constexpr bool DMA = NW == 8;
     static_assert(D == 64 || D == 128, "MFMA attention: head_dim 64 or 128");
-    static_assert(KT == 64 && KPIECES % NT == 0 && VPIECES <= NT, "tile shape");
-    __shared__ __attribute__((aligned(16))) __half ks[KT][KP];
-    __shared__ __attribute__((aligned(16))) __half vt[D][VP];
+    static_assert(KT == 64, "tile shape");
+    // direct loads: 16-byte slots per row, bytes of one matrix of a tile,
+    // slots per thread per matrix, tile buffers
+    constexpr int SPR = D / 8, MAT = KT * D * 2, DPT = KT * SPR / NT, NBUF = 3;
+    static_assert(!DMA || KT * SPR % NT == 0, "tile shape");
+    // register path: row pads against LDS bank conflicts in the fragment
+    // reads (pads of 16 halves measured fastest), 16-byte K pieces per tile,
+    // V pieces of 4 keys x 8 dims per tile
+    constexpr int KP = D + 16, VP = KT + 16;
+    constexpr int KPIECES = KT * (D / 8), VPIECES = (KT / 4) * (D / 8), KPT = KPIECES / NT;
+    static_assert(DMA || (KPIECES % NT == 0 && VPIECES <= NT), "tile shape");
+    constexpr int SMEM = DMA ? NBUF * 2 * MAT : (KT * KP + D * VP) * 2;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[SMEM];
+    auto ks = reinterpret_cast<__half (*)[KP]>(smem);
+    auto vt = reinterpret_cast<__half (*)[VP]>(smem + KT * KP * 2);
+
     const int split = blockIdx.x, rt = blockIdx.y, g = blockIdx.z;
     const int G = P.qh / P.kh, R = G * P.m;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -342,21 +360,57 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_kernel(AttnParams P) {
             qf[k] = __builtin_bit_cast(h8, x);
         }
     }
-    // K piece i: key i / (D/8), dims 8 (i % (D/8)); V piece (tid): keys
-    // 4 (tid % 16)..+3, dims 8 (tid / 16)..+7
+
+    // --- direct loads. Slot c of row r lies at c ^ swk(r) (K: 16 consecutive
+    // rows take 16 distinct slots of one logical column, which the score
+    // fragments read per 16 lanes) or c ^ swv(r) (V: 8 consecutive rows take
+    // distinct slot pairs 2c, 2c + 1, the 32 bytes of each of 8 rows a half
+    // wave's transposing reads take).
+    auto swk = [](int r) { return D == 128 ? (r & 15) : ((r >> 1) & 7); };
+    auto swv = [](int r) { return D == 128 ? 2 * (r & 7) : 2 * ((r >> 1) & 3); };
+    // this thread's slots: physical slot t * NT + tid of each matrix -> row,
+    // and the logical slot (16-byte column) it holds
+    int drow[DMA ? DPT : 1], dkc[DMA ? DPT : 1], dvc[DMA ? DPT : 1];
+    if constexpr (DMA) {
+#pragma unroll
+        for (int t = 0; t < DPT; ++t) {
+            const int pslot = t * NT + tid, r = pslot / SPR, ps = pslot % SPR;
+            drow[t] = r;
+            dkc[t] = ps ^ swk(r);
+            dvc[t] = ps ^ swv(r);
+        }
+    }
+    // keys past the split read the split's last key (finite data; masked)
+    auto issue_dma = [&](int kb, int buf) {
+        const char* kt = reinterpret_cast<const char*>(kbase + (size_t)kb * D);
+        const char* vtp = reinterpret_cast<const char*>(vbase + (size_t)kb * D);
+        const int last = k1 - 1 - kb;
+        uint8_t* dst = smem + buf * 2 * MAT + (wave * 64) * 16;
+#pragma unroll
+        for (int t = 0; t < DPT; ++t) {
+            const int r = min(drow[t], last);
+            lds_dma16(kt + (r * D + dkc[t] * 8) * 2, dst + t * NT * 16);
+            lds_dma16(vtp + (r * D + dvc[t] * 8) * 2, dst + MAT + t * NT * 16);
+        }
+    };
+
+    // --- register path. K piece i: key i / (D/8), dims 8 (i % (D/8)); V
+    // piece (tid): keys 4 (tid % 16)..+3, dims 8 (tid / 16)..+7
     const bool vthread = tid < VPIECES;
     const int vj = tid & 15, vc = tid >> 4;
     // byte offsets within a tile (the tile base is uniform): K piece t, V row t
-    unsigned koff[KPT], voff[4];
+    unsigned koff[DMA ? 1 : KPT], voff[4];
+    v4u kr[DMA ? 1 : KPT], vr[4];
+    if constexpr (!DMA) {
 #pragma unroll
-    for (int t = 0; t < KPT; ++t) {
-        const int i = tid + NT * t;
-        koff[t] = (unsigned)((i / (D / 8)) * D + (i % (D / 8)) * 8) * 2u;
+        for (int t = 0; t < KPT; ++t) {
+            const int i = tid + NT * t;
+            koff[t] = (unsigned)((i / (D / 8)) * D + (i % (D / 8)) * 8) * 2u;
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) voff[t] = (unsigned)((4 * vj + t) * D + vc * 8) * 2u;
     }
-#pragma unroll
-    for (int t = 0; t < 4; ++t) voff[t] = (unsigned)((4 * vj + t) * D + vc * 8) * 2u;
-    v4u kr[KPT], vr[4];
-    auto issue = [&](int kb) {
+    auto issue_regs = [&](int kb) {
         const char* kt = reinterpret_cast<const char*>(kbase + (size_t)kb * D);
         const char* vtp = reinterpret_cast<const char*>(vbase + (size_t)kb * D);
         if (kb + KT <= k1) {  // (uniform) whole tile inside the split
@@ -381,7 +435,7 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_kernel(AttnParams P) {
             }
         }
     };
-    auto store = [&](int kb) {
+    auto store_regs = [&](int kb) {
         if (kb + KT > k1) {  // (block-uniform) zero the keys past the split
 #pragma unroll
             for (int t = 0; t < KPT; ++t)
@@ -407,25 +461,39 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_kernel(AttnParams P) {
                     x[0] = (vr[0][cw] & 0xffffu) | (vr[1][cw] << 16);
                     x[1] = (vr[2][cw] & 0xffffu) | (vr[3][cw] << 16);
                 }
-                // within each 32-key chunk the 4-key groups lie in the order
-                // 0 4 1 5 2 6 3 7, so a lane's 8 k-slots (groups hi, hi + 4)
-                // are one 16-byte read
                 const int lg = vj & 7, pos = lg < 4 ? 2 * lg : 2 * lg - 7;
                 *reinterpret_cast<u2*>(&vt[vc * 8 + e][32 * (vj >> 3) + 4 * pos]) = x;
             }
         }
     };
+
     f4 o[NB];
 #pragma unroll
     for (int n = 0; n < NB; ++n) o[n] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     float mrun = -INFINITY, lpart = 0.0f;
     const hh2 ones = {(_Float16)1.0f, (_Float16)1.0f};
-    if (k0 < k1) issue(k0);
+    if constexpr (DMA) {
+        if (k0 < k1) issue_dma(k0, 0);
+        if (k0 + KT < k1) issue_dma(k0 + KT, 1);
+    } else {
+        if (k0 < k1) issue_regs(k0);
+    }
+    int buf = 0;
     for (int kb = k0; kb < k1; kb += KT) {
-        __syncthreads();  // (the previous tile's LDS reads are done)
-        store(kb);
-        __syncthreads();
-        if (kb + KT < k1) issue(kb + KT);
+        const uint8_t* kst = smem + buf * 2 * MAT;
+        const uint8_t* vst = kst + MAT;
+        if constexpr (DMA) {
+            if (kb + KT < k1)
+                wait_vmcnt<2 * DPT>();  // (this thread's loads of the tile have landed; the next tile's may not)
+            else
+                wait_vmcnt<0>();
+            __syncthreads();  // (every thread's have)
+        } else {
+            __syncthreads();  // (the previous tile's LDS reads are done)
+            store_regs(kb);
+            __syncthreads();
+            if (kb + KT < k1) issue_regs(kb + KT);
+        }
         // (k outermost: the 4 key blocks' products are independent, so they
         // issue back to back instead of waiting on each other)
         f4 sacc[4];
@@ -433,8 +501,12 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_kernel(AttnParams P) {
 #pragma unroll
         for (int k = 0; k < KS; ++k)
 #pragma unroll
-            for (int cb = 0; cb < 4; ++cb)
-                ka[cb][k] = __builtin_bit_cast(h8, *reinterpret_cast<const v4u*>(&ks[cb * 16 + lo][32 * k + 8 * hi]));
+            for (int cb = 0; cb < 4; ++cb) {
+                const void* src = DMA ? static_cast<const void*>(kst + (cb * 16 + lo) * (D * 2) +
+                                                                ((4 * k + hi) ^ swk(lo)) * 16)
+                                      : static_cast<const void*>(&ks[cb * 16 + lo][32 * k + 8 * hi]);
+                ka[cb][k] = __builtin_bit_cast(h8, *reinterpret_cast<const v4u*>(src));
+            }
 #pragma unroll
         for (int cb = 0; cb < 4; ++cb) sacc[cb] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -451,16 +523,18 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_kernel(AttnParams P) {
                     if (!(key < lim && key < k1)) sacc[cb][r] = -INFINITY;
                 }
         }
-        float tmax = -INFINITY;
+        // the lane's max of its 16 scores (3-input maxima); the row max only
+        // when some lane's max passes its row's bound
+        float lmax = -INFINITY;
 #pragma unroll
         for (int cb = 0; cb < 4; ++cb)
-            tmax = fmaxf(fmaxf(tmax, fmaxf(sacc[cb][0], sacc[cb][1])), fmaxf(sacc[cb][2], sacc[cb][3]));
-        tmax = max_rows4(tmax);
-        const float tm = tmax * c;
-        const bool grow = tm > mrun + ATTN_LAZY;
-        if (__builtin_expect(__builtin_amdgcn_ballot_w64(grow) != 0, 0)) {  // (uniform, rare after the first tile)
+            lmax = __builtin_elementwise_maximum(
+                __builtin_elementwise_maximum(lmax, __builtin_elementwise_maximum(sacc[cb][0], sacc[cb][1])),
+                __builtin_elementwise_maximum(sacc[cb][2], sacc[cb][3]));
+        if (__builtin_expect(__builtin_amdgcn_ballot_w64(lmax * c > mrun + ATTN_LAZY) != 0, 0)) {  // (uniform)
+            const float tm = max_rows4(lmax) * c;
             float alpha = 1.0f;
-            if (grow) {
+            if (tm > mrun + ATTN_LAZY) {
                 alpha = __builtin_amdgcn_exp2f(mrun - tm);  // (0 from -inf)
                 mrun = tm;
             }
@@ -487,10 +561,31 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_kernel(AttnParams P) {
             h8 va[NB];
 #pragma unroll
             for (int n = 0; n < NB; ++n) {
-                va[n] = __builtin_bit_cast(h8, *reinterpret_cast<const v4u*>(&vt[16 * n + lo][32 * k + 8 * hi]));
+                if constexpr (DMA) {
+                    // transposing reads: lane j of a 16-lane group names dims
+                    // 4 (j % 4)..+3 of key row 4 (j / 4) of the group's 16
+                    // keys; lane i receives dim i of the rows named by lanes
+                    // i / 4, 4 + i / 4, 8 + i / 4, 12 + i / 4: its dim of keys
+                    // 4 hi..+3 (then of keys 16 + 4 hi..+3) of the step
+                    const int vr0 = 32 * k + 4 * hi + (lo >> 2);
+                    const uint8_t* p =
+                        vst + vr0 * (D * 2) + (((2 * n + ((lo & 3) >> 1)) ^ swv(vr0)) * 16) + (lo & 1) * 8;
+                    const s4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)p);
+                    const s4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(p + 16 * (D * 2)));
+                    const u2 ua = __builtin_bit_cast(u2, a), ub = __builtin_bit_cast(u2, b);
+                    va[n] = __builtin_bit_cast(h8, v4u{ua[0], ua[1], ub[0], ub[1]});
+                } else {
+                    va[n] = __builtin_bit_cast(h8, *reinterpret_cast<const v4u*>(&vt[16 * n + lo][32 * k + 8 * hi]));
+                }
             }
 #pragma unroll
             for (int n = 0; n < NB; ++n) o[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[n], pb[k], o[n], 0, 0, 0);
+        }
+        if constexpr (DMA) {
+            // (the compiler waits for every direct load in flight before a
+            // transposing read, so the request comes after this tile's)
+            if (kb + 2 * KT < k1) issue_dma(kb + 2 * KT, buf == 0 ? NBUF - 1 : buf - 1);
+            buf = buf == NBUF - 1 ? 0 : buf + 1;
         }
     }
     float l = lpart;
