@@ -541,7 +541,12 @@ static int enqueue_moe(MoeWork* ws, const MoeBank* b, int rows, const float* inp
     Cb.top = ws->top;
     Cb.h = ws->h;
     Cb.out = out;
-    hipLaunchKernelGGL(moe_combine_kernel, dim3((ws->h + 255) / 256, rows), dim3(256), 0, s, Cb);
+    const bool vec4 = ws->h % 4 == 0 && ((reinterpret_cast<uintptr_t>(Cb.contrib) | reinterpret_cast<uintptr_t>(out) |
+                                           reinterpret_cast<uintptr_t>(shared)) & 15) == 0;
+    if (vec4)
+        hipLaunchKernelGGL(moe_combine_kernel<4>, dim3((ws->h / 4 + 255) / 256, rows), dim3(256), 0, s, Cb);
+    else
+        hipLaunchKernelGGL(moe_combine_kernel<1>, dim3((ws->h + 255) / 256, rows), dim3(256), 0, s, Cb);
     return hipGetLastError() == hipSuccess ? RK_NPU_OK : RK_NPU_ERR_DEVICE;
 }
 

@@ -229,18 +229,59 @@ struct CombineParams {
     float* out;
 };
 
+// VEC output columns per thread (4 when every row is 16-byte aligned): the
+// ranks' slots and weights (uniform over the block: scalar loads) and the
+// contributions are requested together, 8 ranks at a time (one memory round
+// trip instead of one per rank), then added in rank order, so each sum is the
+// same sequence of single-rounding fma as the reference's rank loop. A
+// skipped rank reads a valid row and is not added.
+constexpr int COMBINE_BATCH = 8;
+template <int VEC>
 static __global__ __launch_bounds__(256) void moe_combine_kernel(CombineParams P) {
+    typedef float fv __attribute__((ext_vector_type(VEC)));
     const int r = blockIdx.y;
-    const int c = blockIdx.x * 256 + threadIdx.x;
+    const int c = (blockIdx.x * 256 + threadIdx.x) * VEC;
     if (c >= P.h) return;
-    float sum = 0.0f;
-    for (int rank = 0; rank < P.top; ++rank) {
-        const int a = r * P.top + rank;
-        const int s = P.pos ? P.pos[a] : (P.routes[a] > 0.0f ? a : -1);
-        if (s >= 0) sum = __builtin_fmaf(P.contrib[(size_t)s * P.h + c], P.routes[a], sum);
+    fv sum = fv(0.0f);
+    for (int r0 = 0; r0 < P.top; r0 += COMBINE_BATCH) {
+        const int a0 = r * P.top + r0;
+        const int n = min(COMBINE_BATCH, P.top - r0);
+        float w[COMBINE_BATCH];
+        int slot[COMBINE_BATCH];
+        fv v[COMBINE_BATCH];
+        if (n == COMBINE_BATCH) {
+#pragma unroll
+            for (int i = 0; i < COMBINE_BATCH; ++i) w[i] = P.routes[a0 + i];
+            if (P.pos) {
+#pragma unroll
+                for (int i = 0; i < COMBINE_BATCH; ++i) slot[i] = P.pos[a0 + i];
+            } else {
+#pragma unroll
+                for (int i = 0; i < COMBINE_BATCH; ++i) slot[i] = w[i] > 0.0f ? a0 + i : -1;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < COMBINE_BATCH; ++i) {
+                w[i] = i < n ? P.routes[a0 + i] : 0.0f;
+                slot[i] = i >= n ? -1 : (P.pos ? P.pos[a0 + i] : (w[i] > 0.0f ? a0 + i : -1));
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < COMBINE_BATCH; ++i)
+            v[i] = *reinterpret_cast<const fv*>(P.contrib + (size_t)max(slot[i], 0) * P.h + c);
+#pragma unroll
+        for (int i = 0; i < COMBINE_BATCH; ++i)
+            if (slot[i] >= 0) {
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) sum[e] = __builtin_fmaf(v[i][e], w[i], sum[e]);
+            }
     }
-    if (P.shared) sum = sum + P.shared[(size_t)r * P.h + c];
-    P.out[(size_t)r * P.h + c] = sum;
+    if (P.shared) {
+        const fv sh = *reinterpret_cast<const fv*>(P.shared + (size_t)r * P.h + c);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) sum[e] = sum[e] + sh[e];
+    }
+    *reinterpret_cast<fv*>(P.out + (size_t)r * P.h + c) = sum;
 }
 
 }  // namespace hm
