@@ -65,11 +65,15 @@ def run_sequence(att, qh, kh, d, chunks, rng, scale):
     return k_all, v_all
 
 
-def test_causal_gqa_sequence_matches_oracle():
+@pytest.mark.parametrize("d", [128, 64])
+def test_causal_gqa_sequence_matches_oracle(d):
     """Prefill chunks, then single-row decode steps and a multi-token step
-    (src/npu/attention.rs:299-352), 8 query heads over 2 KV heads."""
+    (src/npu/attention.rs:299-352), 8 query heads over 2 KV heads. The 37-
+    and 128-row chunks give 148 and 512 rows per KV head (8-wave blocks, tiles
+    by direct loads over one and several tiles per key split), the 64- and
+    17-row chunks 256 and 68 (8- and 4-wave blocks)."""
     be = npu.Backend(npu.ModelOptions(chunk=128, context=1024))
-    qh, kh, d = 8, 2, 128
+    qh, kh = 8, 2
     scale = d ** -0.5
     att = be.attention(qh, kh, d, scale)
     run_sequence(att, qh, kh, d, (37, 128, 64, 1, 1, 17, 4, 1), np.random.default_rng(3), scale)
@@ -130,16 +134,17 @@ def test_bidirectional_gqa_matches_oracle(qh, kh, d):
         pos += rows
 
 
-@pytest.mark.parametrize("causal", [True, False])
-def test_growing_scores_match_oracle(causal):
+@pytest.mark.parametrize("causal,d", [(True, 128), (False, 128), (True, 64)])
+def test_growing_scores_match_oracle(causal, d):
     """Keys whose magnitude grows along the sequence, so a row's running max
     rises many times over the tiles of one key split (scaled scores up to
     ~50, far past what unshifted fp16 weights hold). 32 query heads over 8
     KV heads with 128 query rows over 2048 keys: the matrix-core path splits
-    the keys 8 ways, 4 tiles each, so its deferred rescaling runs inside a
-    split; then a 1-row decode step over the same cache."""
+    the keys 8 ways, 4 tiles each (more tiles than its 8-wave blocks' three
+    tile buffers), so its deferred rescaling runs inside a split; then a
+    1-row decode step over the same cache."""
     be = npu.Backend(npu.ModelOptions(chunk=128, context=2048))
-    qh, kh, d, length = 32, 8, 128, 2048
+    qh, kh, length = 32, 8, 2048
     scale = d ** -0.5
     att = be.attention(qh, kh, d, scale) if causal else be.noncausal_gqa(qh, kh, d)
     rng = np.random.default_rng(9)
